@@ -1,0 +1,239 @@
+"""Delta-attention layer prefill benchmark on one MI355X.
+
+Workload: one Llama-3.1-8B-shaped attention layer prefill at 128K tokens --
+batch 1, 32 query heads / 8 key-value heads, head_dim 128, seq 131072,
+Q/K/V ~ N(0,1) (Q scaled by 1/sqrt(128)), RoPE theta 500000 on Q/K, bf16,
+causal, window 2048 + 128 sink tokens, gamma 64. A step is one full layer
+prefill: kernel (1) key-sparse attention, kernel (2) query-sparse dense rows
+with the fused delta epilogue, kernel (3) delta broadcast-add, with the inputs
+resident in HBM.
+
+Prints ONE JSON line: value = TFLOP/s of the layer (algorithmic FLOPs of
+kernels 1+2 / layer time), ms_per_step = layer time, plus the roofline of the
+dominant kernel (HIP events on the launch stream), per-kernel figures and the
+CPU oracle timed on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "delta-attention_amd"))
+sys.path.insert(0, REPO)
+
+METRIC = "delta-attn layer prefill ms + TFLOP/s (%MFMA peak) at 128K, Llama-3.1-8B shape"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--seq", type=int, default=131072)
+    p.add_argument("--gamma", type=int, default=64)
+    p.add_argument("--window", type=int, default=2048)
+    p.add_argument("--sink", type=int, default=128)
+    p.add_argument("--heads", type=int, default=32)
+    p.add_argument("--kv-heads", type=int, default=8)
+    p.add_argument("--batch", type=int, default=1)
+    p.add_argument("--head-dim", type=int, default=128)
+    p.add_argument("--rope-theta", type=float, default=500000.0)
+    p.add_argument("--cpu-budget", type=float, default=15.0,
+                   help="approximate seconds of CPU oracle work for cpu_baseline (0: skip)")
+    p.add_argument("--seed", type=int, default=0)
+    return p.parse_args()
+
+
+def make_inputs(a, device):
+    """Seeded N(0,1) q/k/v drawn in q, k, v order, q * d^-0.5, RoPE on q and k
+    (rotate_half, inv_freq = theta^(-2i/d), fp32 tables), cast to bf16."""
+    import torch
+    from delta_attention.llama import apply_rotary_pos_emb, rope_cos_sin
+
+    g = torch.Generator(device=device).manual_seed(a.seed)
+    B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
+    q = torch.empty(B, H, S, D, device=device, dtype=torch.bfloat16)
+    k = torch.empty(B, Hkv, S, D, device=device, dtype=torch.bfloat16)
+    v = torch.empty(B, Hkv, S, D, device=device, dtype=torch.bfloat16)
+    pos = torch.arange(S, device=device)[None]
+    cos, sin = rope_cos_sin(pos, D, a.rope_theta, torch.float32)
+    CH = 8192
+    for c0 in range(0, S, CH):
+        c1 = min(S, c0 + CH)
+        qc = torch.randn(B, H, c1 - c0, D, device=device, generator=g) * D ** -0.5
+        kc = torch.randn(B, Hkv, c1 - c0, D, device=device, generator=g)
+        qc, kc = apply_rotary_pos_emb(qc, kc, cos[:, c0:c1], sin[:, c0:c1])
+        q[:, :, c0:c1] = qc.to(torch.bfloat16)
+        k[:, :, c0:c1] = kc.to(torch.bfloat16)
+        v[:, :, c0:c1] = torch.randn(B, Hkv, c1 - c0, D, device=device, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+def cpu_baseline(a, q, k, v, flops_layer):
+    """The CPU oracle (numpy, BLAS threads) on a bounded sample of the same
+    workload: the key-sparse pass for a block of rows and the dense pass for
+    the longest anchor rows, both on the heads of one kv group."""
+    import numpy as np
+    from oracle import delta_oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        cores = 1
+    G = a.heads // a.kv_heads
+    S, D = a.seq, a.head_dim
+    scale = D ** -0.5
+    qh = q[:, :G].float().cpu().numpy()
+    kh = k[:, :1].float().cpu().numpy()
+    vh = v[:, :1].float().cpu().numpy()
+    anchors, tail, s_p, _ = O.anchor_layout(S, a.gamma)
+    flops = 0.0
+    t0 = time.perf_counter()
+    n_rows = 0
+    # key-sparse rows from the middle of the sequence, 1024 at a time
+    r0 = S // 2
+    while time.perf_counter() - t0 < a.cpu_budget / 2 and r0 + 1024 <= S:
+        rows = np.arange(r0, r0 + 1024)
+        O.sparse_attention(qh, kh, vh, a.window, a.sink, scale, rows=rows)
+        flops += 4.0 * D * G * O.sparse_row_counts(S, a.window, a.sink)[rows].sum()
+        n_rows += 1024
+        r0 += 1024
+    t1 = time.perf_counter()
+    # the longest dense anchor rows, 8 at a time
+    n_dense = 0
+    i = len(anchors)
+    while time.perf_counter() - t1 < a.cpu_budget / 2 and i >= 8:
+        rows = anchors[i - 8:i]
+        O.qsparse_attention(qh[:, :, rows], kh, vh, rows, scale)
+        flops += 4.0 * D * G * float((rows + 1).sum())
+        n_dense += 8
+        i -= 8
+    dt = time.perf_counter() - t0
+    tflops = flops / dt / 1e12
+    return {
+        "value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(cores), "kind": "port",
+        "sample": (f"oracle/delta_oracle.py (numpy fp32, BLAS) on heads 0-{G - 1} (kv group 0): "
+                   f"key-sparse pass over {n_rows} rows from row {S // 2} plus the dense pass over "
+                   f"the last {n_dense} anchor rows; {flops / 1e9:.1f} GFLOP in {dt:.1f} s; "
+                   f"full-layer time at this rate {flops_layer / (tflops * 1e12):.0f} s"),
+    }
+
+
+def load_traffic(name):
+    """HBM bytes per launch of `name` from the committed rocprofv3 PMC summary."""
+    path = os.path.join(REPO, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+        return rec.get(name, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {a.gpus}); the delta-attention path "
+              "is not sharded across GPUs in this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from delta_attention import ops
+    from delta_attention import _lib as L
+    from oracle import delta_oracle as O
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    L.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
+    scale = D ** -0.5
+    q, k, v = make_inputs(a, dev)
+
+    cut_n, s_p, n_anchor = ops.anchor_layout(S, a.gamma)
+    idx = ops.selected_rows(S, a.gamma, str(dev))
+    n_sel = idx.numel()
+    out = torch.empty(B, S, H, D, device=dev, dtype=torch.bfloat16)
+    delta = torch.empty(B, n_anchor, H, D, device=dev, dtype=torch.bfloat16)
+    ws = ops.qsparse_workspace(B, H, Hkv, n_sel, S, D, dev)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record()
+        ops.sparse_attention(q, k, v, window=a.window, sink=a.sink, sm_scale=scale, out=out)
+        if ev is not None:
+            ev[1].record()
+        ops.qsparse_attention(q, k, v, idx, scale, q_rows=idx, epi=L.DA_EPI_DELTA, out=out,
+                              n_anchor=n_anchor, delta=delta, workspace=ws)
+        if ev is not None:
+            ev[2].record()
+        ops.delta_add(out, s_p=s_p, out=out, delta=delta, gamma=a.gamma)
+        if ev is not None:
+            ev[3].record()
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` layer prefills
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / a.steps * 1e3
+
+    # per-kernel durations from HIP events on the launch stream (separate pass)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    k_ms = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / a.steps for i in range(3)]
+
+    f_sparse = O.flops_sparse(B, H, D, S, a.window, a.sink)
+    f_q = O.flops_qsparse(B, H, D, idx.cpu().numpy())
+    bytes_add = B * H * D * 2 * (2 * s_p + n_anchor)
+    tflops = (f_sparse + f_q) / (ms * 1e-3) / 1e12
+    kernels = {
+        "sparse_attn": {"ms": round(k_ms[0], 4), "tflops": round(f_sparse / k_ms[0] / 1e9, 2),
+                        "frac_mfma": round(f_sparse / k_ms[0] / 1e9 / PEAK_BF16_TFLOPS, 4),
+                        "flop": f_sparse},
+        "qsparse_attn": {"ms": round(k_ms[1], 4), "tflops": round(f_q / k_ms[1] / 1e9, 2),
+                         "frac_mfma": round(f_q / k_ms[1] / 1e9 / PEAK_BF16_TFLOPS, 4),
+                         "flop": f_q, "rows": n_sel},
+        "delta_add": {"ms": round(k_ms[2], 4), "gbs": round(bytes_add / k_ms[2] / 1e6, 1),
+                      "frac_hbm": round(bytes_add / k_ms[2] / 1e6 / PEAK_HBM_GBS, 4),
+                      "bytes": bytes_add},
+    }
+    dom = "sparse_attn" if k_ms[0] >= k_ms[1] else "qsparse_attn"
+    achieved = kernels[dom]["tflops"]
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": load_traffic(dom)}
+
+    cpu = None
+    if a.cpu_budget > 0:
+        cpu = cpu_baseline(a, q, k, v, f_sparse + f_q)
+
+    line = {
+        "metric": METRIC, "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, q*d^-0.5, RoPE theta 5e5, bf16)",
+        "config": {"workload": "llama-3.1-8b-shaped delta-attention layer prefill",
+                   "batch": B, "seq_len": S, "q_heads": H, "kv_heads": Hkv, "head_dim": D,
+                   "window": a.window, "sink": a.sink, "gamma": a.gamma,
+                   "selected_rows": n_sel, "parallelism": "none (1 GPU)"},
+        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,653 @@
+// Attention kernels of the delta-attention prefill path on gfx950:
+//   kernel (1)  da_sparse_attn_fwd   sink + block-anchored sliding window
+//   kernel (2)  da_qsparse_attn_fwd  selected query rows against all causal keys,
+//                                    split over the key axis, merged by
+//                                    qsparse_merge_kernel, which also runs the
+//                                    delta epilogue.
+//
+// Tiling (one workgroup = 4 waves = 256 threads):
+//   * M tile: BM = 128 flattened (query row, head-in-group) pairs. The G query
+//     heads that share one key/value head are packed into the same tile, so
+//     K/V tiles are read once per group (no repeat_kv copies).
+//   * Each wave owns 32 flattened rows. Scores are formed transposed,
+//     S^T = K * Q^T, with v_mfma_f32_32x32x16 (A = 32 keys x 16 dims from LDS,
+//     B = Q^T fragment kept in registers). In the 32x32 accumulator layout a
+//     lane holds one query row (lane % 32) and 16 of its keys, so the softmax
+//     row max/sum is in-lane plus one permlane32 swap.
+//   * O^T = V^T * P^T: the probabilities leave the score accumulator directly
+//     as the B operand, and the O^T accumulator again keeps one query row per
+//     lane, so the online-softmax rescale is a per-lane scalar.
+//   * K rows are staged to LDS in a row order (sigma) that makes each lane's 8
+//     keys per PV step contiguous; V is staged transposed (V^T) during the
+//     global->LDS copy. Both use XOR chunk swizzles so the 16-byte LDS reads
+//     and writes are bank-conflict free. Two LDS stages double-buffer the K/V
+//     tiles; the next tile's global loads are in flight during the MFMAs.
+//   * Lazy rescale: the running max only moves when a row's tile max exceeds
+//     it by more than 2^8, so most tiles skip the O rescale.
+#include "device_common.h"
+#include "capi_common.h"
+
+namespace da {
+
+constexpr int BM = 128;   // flattened (row, head) pairs per workgroup
+constexpr int BN = 64;    // keys per tile
+constexpr int NTHR = 256;
+constexpr float RESCALE_THRESH = 8.0f;   // log2 domain
+constexpr float NEG_BIG = -1.0e30f;      // finite "minus infinity" for the running max
+
+enum { MODE_SPARSE = 0, MODE_QSPARSE = 1 };
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t qs_b, qs_h, qs_s;
+  int64_t ks_b, ks_h, ks_s;
+  int64_t vs_b, vs_h, vs_s;
+  void* o;
+  int64_t os_b, os_h, os_s;
+  int B, Hq, Hkv, G;
+  int n_rows;       // query rows per (batch, head)
+  int n_q;          // rows of q (selected rows index into it)
+  int n_kv;         // keys
+  int n_mtiles;     // ceil(n_rows * G / BM)
+  int n_items;      // work items before padding the grid to a multiple of 8
+  float scale_log2; // sm_scale * log2(e)
+  int window, sink, q_block;
+  const int64_t* q_rows;
+  const int64_t* row_last;
+  int64_t rl_b;
+  int chunk;        // keys per split (multiple of BN)
+  int n_splits;
+  float* part_o;    // [item][BM][D]
+  float* part_ml;   // [item][2][BM]  (running max, row sum)
+};
+
+// sigma: LDS row order of a 32-key half-tile (swap bits 2 and 3). Row
+// sigma(r) of the A operand lands in accumulator row r, which puts keys
+// 8*g .. 8*g+7 (g = lane / 32) in accumulator elements 0..7 of every lane.
+__device__ __forceinline__ int sigma32(int r) {
+  return (r & 0x13) | ((r & 4) << 1) | ((r & 8) >> 1);
+}
+// XOR swizzle of the 16-byte chunk index of K row `row` (row-major K tile).
+__device__ __forceinline__ int k_swz(int row) { return (row & 3) | ((row >> 1) & 4); }
+// XOR swizzle of the 16-byte chunk index of V^T row `d`.
+__device__ __forceinline__ int v_swz(int d) { return (d + (d >> 3)) & 7; }
+
+template <int D>
+struct Smem {
+  static constexpr int DCH = D / 8;        // 16-byte chunks per K row
+  u32x4 k[2][BN * DCH];                    // [stage][key row][chunk]
+  u32x4 v[2][D * (BN / 8)];                // [stage][d row][key chunk]  (V^T)
+  int red[4][4];
+};
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
+  constexpr int DCH = D / 8;
+  constexpr int NDS = D / 16;              // MFMA k-steps of Q.K^T
+  constexpr int NDT = D / 32;              // 32-row tiles of O^T
+  constexpr int KCH = BN * DCH / NTHR;     // K chunks loaded per thread
+  constexpr int DPT = D / 32;              // V dims per thread (8 keys x DPT dims)
+  using E = Elt<T>;
+
+  __shared__ Smem<D> sm;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int ln = lane & 31;
+  const int lg = lane >> 5;
+
+  // ---- work item (XCD-aware: each XCD walks a contiguous range) ----
+  const int per_xcd = gridDim.x >> 3;
+  const int w = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (w >= a.n_items) return;
+  int mt, split = 0, bh;
+  if (MODE == MODE_SPARSE) {
+    mt = w % a.n_mtiles;
+    bh = w / a.n_mtiles;
+  } else {
+    mt = w % a.n_mtiles;
+    const int t = w / a.n_mtiles;
+    split = t % a.n_splits;
+    bh = t / a.n_splits;
+  }
+  const int hk = bh % a.Hkv;
+  const int b = bh / a.Hkv;
+  const int G = a.G;
+
+  // ---- this lane's query row ----
+  const int mflat = mt * BM + wave * 32 + ln;
+  const bool valid = mflat < a.n_rows * G;
+  const int i = valid ? mflat / G : 0;
+  const int h = hk * G + (valid ? mflat % G : 0);
+  int qrow, lo, hi;
+  if (MODE == MODE_SPARSE) {
+    qrow = i;
+    hi = valid ? i : -1;
+    lo = (i / a.q_block) * a.q_block + a.q_block - a.window;
+  } else {
+    qrow = a.q_rows ? (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1)) : i;
+    int64_t lim = a.row_last[(int64_t)b * a.rl_b + i];
+    if (lim > a.n_kv - 1) lim = a.n_kv - 1;
+    hi = valid ? (int)(lim < -1 ? -1 : lim) : -1;
+    lo = 0;
+  }
+  const int sink = (MODE == MODE_SPARSE) ? a.sink : 0;
+
+  // ---- tile-wide bounds (valid rows only) ----
+  {
+    int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
+    int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      v_hmin = min(v_hmin, __shfl_xor(v_hmin, off));
+      v_hmax = max(v_hmax, __shfl_xor(v_hmax, off));
+      v_lmin = min(v_lmin, __shfl_xor(v_lmin, off));
+      v_lmax = max(v_lmax, __shfl_xor(v_lmax, off));
+    }
+    if (lane == 0) {
+      sm.red[0][wave] = v_hmin;
+      sm.red[1][wave] = v_hmax;
+      sm.red[2][wave] = v_lmin;
+      sm.red[3][wave] = v_lmax;
+    }
+  }
+  __syncthreads();
+  const int hi_min = min(min(sm.red[0][0], sm.red[0][1]), min(sm.red[0][2], sm.red[0][3]));
+  const int hi_max = max(max(sm.red[1][0], sm.red[1][1]), max(sm.red[1][2], sm.red[1][3]));
+  const int lo_min = min(min(sm.red[2][0], sm.red[2][1]), min(sm.red[2][2], sm.red[2][3]));
+  const int lo_max = max(max(sm.red[3][0], sm.red[3][1]), max(sm.red[3][2], sm.red[3][3]));
+
+  // ---- key tiles to visit ----
+  int n_first, first_t0, n_second, second_t0;
+  if (MODE == MODE_SPARSE) {
+    // sink tiles [0, ceil(min(sink, lo_min, hi_max + 1) / BN)), then window
+    // tiles from the tile holding lo_min up to the tile holding hi_max.
+    int sink_end = min(min(sink, lo_min), hi_max + 1);
+    if (sink_end < 0) sink_end = 0;
+    n_first = (sink_end + BN - 1) / BN;
+    first_t0 = 0;
+    second_t0 = max(max(lo_min, 0) / BN, n_first);
+    n_second = hi_max >= 0 ? max(0, hi_max / BN - second_t0 + 1) : 0;
+  } else {
+    const int c0 = split * a.chunk;
+    if (c0 > hi_max) return;   // nothing visible: the merge skips this split
+    const int c1 = min(c0 + a.chunk, hi_max + 1);
+    n_first = 0;
+    first_t0 = 0;
+    second_t0 = c0 / BN;
+    n_second = (c1 - 1) / BN - second_t0 + 1;
+  }
+  const int nt = n_first + n_second;
+
+  const size_t esz = sizeof(T);
+  const char* kbase = (const char*)a.k + ((int64_t)b * a.ks_b + (int64_t)hk * a.ks_h) * esz;
+  const char* vbase = (const char*)a.v + ((int64_t)b * a.vs_b + (int64_t)hk * a.vs_h) * esz;
+
+  // ---- Q^T fragments (registers for the whole kernel) ----
+  u32x4 qf[NDS];
+  {
+    const char* qp = (const char*)a.q +
+                     ((int64_t)b * a.qs_b + (int64_t)h * a.qs_h + (int64_t)qrow * a.qs_s) * esz;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+      qf[ds] = valid ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
+  }
+
+  // ---- global -> register -> LDS staging of one K/V tile ----
+  u32x4 kreg[KCH];
+  uint32_t vreg[8][DPT / 2];
+  const int v_kc = tid >> 5;   // keys 8*v_kc .. 8*v_kc+7
+  const int v_dq = tid & 31;   // dims DPT*v_dq .. +DPT-1
+
+  auto tile_n0 = [&](int t) -> int {
+    return (t < n_first ? first_t0 + t : second_t0 + (t - n_first)) * BN;
+  };
+  auto gload = [&](int n0) {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int id = c * NTHR + tid;
+      const int row = id / DCH, ch = id % DCH;
+      const int key = n0 + row;
+      kreg[c] = key < a.n_kv ? *(const u32x4*)(kbase + ((int64_t)key * a.ks_s + ch * 8) * esz)
+                             : (u32x4){0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = n0 + 8 * v_kc + e;
+      const char* p = vbase + ((int64_t)key * a.vs_s + DPT * v_dq) * esz;
+      if constexpr (DPT == 4) {
+        u32x2 x = key < a.n_kv ? *(const u32x2*)p : (u32x2){0, 0};
+        vreg[e][0] = x[0];
+        vreg[e][1] = x[1];
+      } else {
+        vreg[e][0] = key < a.n_kv ? *(const uint32_t*)p : 0u;
+      }
+    }
+  };
+  auto lstore = [&](int st) {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int id = c * NTHR + tid;
+      const int row = id / DCH, ch = id % DCH;
+      sm.k[st][row * DCH + (ch ^ k_swz(row))] = kreg[c];
+    }
+#pragma unroll
+    for (int x = 0; x < DPT; ++x) {
+      const int wsel = x >> 1;
+      const bool odd = x & 1;
+      u32x4 out;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const uint32_t a0 = vreg[2 * jj][wsel], a1 = vreg[2 * jj + 1][wsel];
+        out[jj] = odd ? ((a0 >> 16) | (a1 & 0xffff0000u)) : ((a0 & 0xffffu) | (a1 << 16));
+      }
+      const int d = DPT * v_dq + x;
+      sm.v[st][d * 8 + (v_kc ^ v_swz(d))] = out;
+    }
+  };
+
+  f32x16 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+  float m_i = NEG_BIG, l_i = 0.f;
+
+  const int krow0 = sigma32(ln);
+  const int kx = ln & 7;   // k_swz(krow0 + 32 * kt)
+  int vx[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) vx[dt] = v_swz(32 * dt + ln);
+
+  if (nt > 0) {
+    gload(tile_n0(0));
+    lstore(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < nt; ++t) {
+    const int st = t & 1;
+    const int n0 = tile_n0(t);
+    if (t + 1 < nt) gload(tile_n0(t + 1));
+
+    // S^T for keys n0 .. n0+31 (s0) and n0+32 .. n0+63 (s1)
+    f32x16 s0, s1;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) { s0[j] = 0.f; s1[j] = 0.f; }
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      const int ch = (2 * ds + lg) ^ kx;
+      const u32x4 ka = sm.k[st][krow0 * DCH + ch];
+      const u32x4 kb = sm.k[st][(krow0 + 32) * DCH + ch];
+      s0 = E::mfma(ka, qf[ds], s0);
+      s1 = E::mfma(kb, qf[ds], s1);
+    }
+
+    // scale (log2 domain) and mask; key of element j: n0 + 32*half + 16*(j/8) + 8*lg + j%8
+    const int n1 = n0 + BN - 1;
+    const bool full = (n1 <= hi_min) && (n1 < a.n_kv) && (n1 < sink || n0 >= lo_max);
+    float mx = NEG_BIG;
+    if (full) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        s0[j] *= a.scale_log2;
+        s1[j] *= a.scale_log2;
+        mx = fmaxf(mx, fmaxf(s0[j], s1[j]));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key0 = n0 + 16 * (j >> 3) + 8 * lg + (j & 7);
+        const int key1 = key0 + 32;
+        const bool v0 = key0 <= hi && (key0 < sink || key0 >= lo);
+        const bool v1 = key1 <= hi && (key1 < sink || key1 >= lo);
+        s0[j] = v0 ? s0[j] * a.scale_log2 : -INFINITY;
+        s1[j] = v1 ? s1[j] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, fmaxf(s0[j], s1[j]));
+      }
+    }
+    mx = max32(mx);
+    if (__any(mx > m_i + RESCALE_THRESH)) {
+      const float m_new = fmaxf(m_i, mx);
+      const float alpha = fast_exp2(m_i - m_new);
+      m_i = m_new;
+      l_i *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+    }
+    float rs = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      s0[j] = fast_exp2(s0[j] - m_i);
+      s1[j] = fast_exp2(s1[j] - m_i);
+      rs += s0[j] + s1[j];
+    }
+    l_i += rs;
+
+    // O^T += V^T * P^T, 16 keys per step
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f32x16& sp = (ks < 2) ? s0 : s1;
+      const int jb = 8 * (ks & 1);
+      u32x4 pf;
+      pf[0] = E::pack2(sp[jb + 0], sp[jb + 1]);
+      pf[1] = E::pack2(sp[jb + 2], sp[jb + 3]);
+      pf[2] = E::pack2(sp[jb + 4], sp[jb + 5]);
+      pf[3] = E::pack2(sp[jb + 6], sp[jb + 7]);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const u32x4 va = sm.v[st][(32 * dt + ln) * 8 + ((2 * ks + lg) ^ vx[dt])];
+        acc[dt] = E::mfma(va, pf, acc[dt]);
+      }
+    }
+
+    if (t + 1 < nt) lstore(st ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----
+  const float l_tot = sum32(l_i);
+  if (MODE == MODE_SPARSE) {
+    if (!valid) return;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)h * a.os_h + (int64_t)qrow * a.os_s) * esz;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const int d = 32 * dt + 8 * jq + 4 * lg;
+        u32x2 pk;
+        pk[0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
+        pk[1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+        *(u32x2*)(op + d * esz) = pk;
+      }
+  } else {
+    const int r = wave * 32 + ln;
+    float* po = a.part_o + ((int64_t)w * BM + r) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const int d = 32 * dt + 8 * jq + 4 * lg;
+        *(f32x4*)(po + d) = (f32x4){acc[dt][4 * jq + 0], acc[dt][4 * jq + 1],
+                                     acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]};
+      }
+    if (lg == 0) {
+      a.part_ml[(int64_t)w * 2 * BM + r] = m_i;
+      a.part_ml[(int64_t)w * 2 * BM + BM + r] = l_tot;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV merge + epilogue of kernel (2). One workgroup per (b, kv head,
+// m tile); 256 threads cover BM rows x D/8 column chunks.
+struct MergeArgs {
+  const int64_t* q_rows;
+  const int64_t* row_last;
+  int64_t rl_b;
+  int n_rows, G, Hkv, n_kv, n_mtiles, n_splits, chunk;
+  const float* part_o;
+  const float* part_ml;
+  int epi, n_anchor, n_q;
+  void* o;
+  int64_t os_b, os_h, os_s;
+  void* delta;
+  int64_t ds_b, ds_h, ds_a;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(NTHR) void qsparse_merge_kernel(MergeArgs a) {
+  using E = Elt<T>;
+  constexpr int CPR = D / 8;   // 8-column chunks per row
+  __shared__ int s_hmax[4];
+  const int tile = blockIdx.x;
+  const int mt = tile % a.n_mtiles;
+  const int bh = tile / a.n_mtiles;
+  const int hk = bh % a.Hkv;
+  const int b = bh / a.Hkv;
+  const int tid = threadIdx.x;
+  const int G = a.G;
+
+  // Same hi_max as the split kernel saw, hence the same set of written splits.
+  int my_hmax = -1;
+  if (tid < BM) {
+    const int mflat = mt * BM + tid;
+    if (mflat < a.n_rows * G) {
+      int64_t lim = a.row_last[(int64_t)b * a.rl_b + mflat / G];
+      if (lim > a.n_kv - 1) lim = a.n_kv - 1;
+      my_hmax = (int)(lim < -1 ? -1 : lim);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) my_hmax = max(my_hmax, __shfl_xor(my_hmax, off));
+  if ((tid & 63) == 0) s_hmax[tid >> 6] = my_hmax;
+  __syncthreads();
+  const int hi_max = max(max(s_hmax[0], s_hmax[1]), max(s_hmax[2], s_hmax[3]));
+  const int nsv = hi_max >= 0 ? hi_max / a.chunk + 1 : 0;
+
+  const size_t esz = sizeof(T);
+  for (int task = tid; task < BM * CPR; task += NTHR) {
+    const int r = task / CPR;
+    const int c = task % CPR;
+    const int mflat = mt * BM + r;
+    if (mflat >= a.n_rows * G) continue;
+    const int i = mflat / G;
+    const int h = hk * G + mflat % G;
+
+    float M = NEG_BIG;
+    for (int s = 0; s < nsv; ++s) {
+      const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
+      M = fmaxf(M, a.part_ml[w * 2 * BM + r]);
+    }
+    float L = 0.f;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    for (int s = 0; s < nsv; ++s) {
+      const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
+      const float sc = fast_exp2(a.part_ml[w * 2 * BM + r] - M);
+      L += sc * a.part_ml[w * 2 * BM + BM + r];
+      const f32x4* po = (const f32x4*)(a.part_o + (w * BM + r) * D + 8 * c);
+      const f32x4 x0 = po[0], x1 = po[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[e] += sc * x0[e];
+        acc[4 + e] += sc * x1[e];
+      }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= inv;
+
+    const int qrow = a.q_rows ? (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1)) : i;
+    if (a.epi == DA_EPI_OUTPUT) {
+      char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)h * a.os_h + (int64_t)i * a.os_s + 8 * c) * esz;
+      u32x4 pk = {E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3]),
+                  E::pack2(acc[4], acc[5]), E::pack2(acc[6], acc[7])};
+      *(u32x4*)op = pk;
+    } else {
+      char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)h * a.os_h + (int64_t)qrow * a.os_s + 8 * c) * esz;
+      const u32x4 pk = {E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3]),
+                        E::pack2(acc[4], acc[5]), E::pack2(acc[6], acc[7])};
+      if (a.epi == DA_EPI_DELTA && i < a.n_anchor) {
+        // delta = rnd(rnd(dense) - sparse): the reference's bf16 subtraction.
+        const u32x4 sp = *(const u32x4*)op;
+        u32x4 dl;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          dl[e] = E::pack2(E::lo(pk[e]) - E::lo(sp[e]), E::hi(pk[e]) - E::hi(sp[e]));
+        char* dp = (char*)a.delta +
+                   ((int64_t)b * a.ds_b + (int64_t)h * a.ds_h + (int64_t)i * a.ds_a + 8 * c) * esz;
+        *(u32x4*)dp = dl;
+      } else {
+        *(u32x4*)op = pk;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+
+struct QsparsePlan {
+  int n_mtiles, n_splits, chunk, n_items;
+  size_t ws_bytes;
+};
+
+static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int Skv, int D) {
+  QsparsePlan p;
+  const int G = Hq / Hkv;
+  p.n_mtiles = (int)(((int64_t)n * G + BM - 1) / BM);
+  const int64_t base = (int64_t)B * Hkv * p.n_mtiles;
+  const int nkt = (Skv + BN - 1) / BN;
+  // Aim for ~4096 split items (about half of them are empty for a causal row
+  // set), i.e. several equal-sized items per CU.
+  int64_t want = (4096 + base - 1) / base;
+  if (want < 1) want = 1;
+  if (want > nkt) want = nkt;
+  const int chunk_tiles = (int)((nkt + want - 1) / want);
+  p.chunk = chunk_tiles * BN;
+  p.n_splits = (nkt + chunk_tiles - 1) / chunk_tiles;
+  p.n_items = (int)(base * p.n_splits);
+  p.ws_bytes = (size_t)p.n_items * BM * (D + 2) * sizeof(float);
+  return p;
+}
+
+template <typename T, int D, int MODE>
+static void launch_attn(const AttnArgs& a, hipStream_t stream) {
+  const int grid = (a.n_items + 7) / 8 * 8;
+  hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE>), dim3(grid), dim3(NTHR), 0, stream, a);
+}
+
+template <int MODE>
+static void dispatch_attn(const AttnArgs& a, int D, int dtype, hipStream_t s) {
+  if (dtype == DA_BF16) {
+    if (D == 128) launch_attn<__bf16, 128, MODE>(a, s);
+    else launch_attn<__bf16, 64, MODE>(a, s);
+  } else {
+    if (D == 128) launch_attn<_Float16, 128, MODE>(a, s);
+    else launch_attn<_Float16, 64, MODE>(a, s);
+  }
+}
+
+template <typename T, int D>
+static void launch_merge(const MergeArgs& m, int n_tiles, hipStream_t s) {
+  hipLaunchKernelGGL((qsparse_merge_kernel<T, D>), dim3(n_tiles), dim3(NTHR), 0, s, m);
+}
+
+}  // namespace da
+
+using namespace da;
+
+extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                                  int B, int Hq, int Hkv, int S, int D,
+                                  const int64_t q_str[3], const int64_t k_str[3],
+                                  const int64_t v_str[3], const int64_t o_str[3],
+                                  int window, int sink, int q_block, float sm_scale,
+                                  int dtype, void* stream) {
+  int rc;
+  if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
+  if (S < 0 || window < 0 || sink < 0 || q_block < 1) return DA_ERR_INVALID_ARG;
+  if (!q_str || !k_str || !v_str || !o_str) return DA_ERR_INVALID_ARG;
+  if (S == 0) return DA_OK;
+  if (!q || !k || !v || !out) return DA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
+      !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
+    return DA_ERR_ALIGNMENT;
+  AttnArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.o = out;
+  a.qs_b = q_str[0]; a.qs_h = q_str[1]; a.qs_s = q_str[2];
+  a.ks_b = k_str[0]; a.ks_h = k_str[1]; a.ks_s = k_str[2];
+  a.vs_b = v_str[0]; a.vs_h = v_str[1]; a.vs_s = v_str[2];
+  a.os_b = o_str[0]; a.os_h = o_str[1]; a.os_s = o_str[2];
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv;
+  a.n_rows = S; a.n_q = S; a.n_kv = S;
+  a.n_mtiles = (int)(((int64_t)S * a.G + BM - 1) / BM);
+  const int64_t items = (int64_t)B * Hkv * a.n_mtiles;
+  if (items > 0x7fffff00LL) return DA_ERR_INVALID_ARG;
+  a.n_items = (int)items;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.window = window; a.sink = sink; a.q_block = q_block;
+  (void)hipGetLastError();
+  dispatch_attn<MODE_SPARSE>(a, D, dtype, (hipStream_t)stream);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}
+
+extern "C" size_t da_qsparse_workspace_bytes(int B, int Hq, int Hkv, int n, int Skv, int D) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n < 1 || Skv < 1 || (D != 64 && D != 128))
+    return 0;
+  return plan_qsparse(B, Hq, Hkv, n, Skv, D).ws_bytes;
+}
+
+extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
+                                   const int64_t* q_rows, const int64_t* row_last, int64_t rl_bstride,
+                                   int n, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                                   const int64_t q_str[3], const int64_t k_str[3], const int64_t v_str[3],
+                                   void* o, const int64_t o_str[3],
+                                   int epi, int n_anchor, void* delta, const int64_t d_str[3],
+                                   float sm_scale, void* workspace, size_t workspace_bytes,
+                                   int dtype, void* stream) {
+  int rc;
+  if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
+  if (n < 0 || Sq < 0 || Skv < 0 || rl_bstride < 0) return DA_ERR_INVALID_ARG;
+  if (epi != DA_EPI_OUTPUT && epi != DA_EPI_DELTA && epi != DA_EPI_SCATTER) return DA_ERR_INVALID_ARG;
+  if (!q_str || !k_str || !v_str || !o_str) return DA_ERR_INVALID_ARG;
+  if (n == 0) return DA_OK;
+  if (!q || !k || !v || !o || !row_last || Sq < 1 || Skv < 1) return DA_ERR_INVALID_ARG;
+  if (q_rows == nullptr && n > Sq) return DA_ERR_INVALID_ARG;
+  if (epi == DA_EPI_DELTA) {
+    if (n_anchor < 0 || n_anchor > n) return DA_ERR_INVALID_ARG;
+    if (n_anchor > 0 && (!delta || !d_str)) return DA_ERR_INVALID_ARG;
+    if (n_anchor > 0 && (!aligned16(delta) || !strides8(d_str))) return DA_ERR_ALIGNMENT;
+  }
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) ||
+      !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
+    return DA_ERR_ALIGNMENT;
+  const QsparsePlan p = plan_qsparse(B, Hq, Hkv, n, Skv, D);
+  if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
+
+  AttnArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.o = nullptr;
+  a.qs_b = q_str[0]; a.qs_h = q_str[1]; a.qs_s = q_str[2];
+  a.ks_b = k_str[0]; a.ks_h = k_str[1]; a.ks_s = k_str[2];
+  a.vs_b = v_str[0]; a.vs_h = v_str[1]; a.vs_s = v_str[2];
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv;
+  a.n_rows = n; a.n_q = Sq; a.n_kv = Skv;
+  a.n_mtiles = p.n_mtiles;
+  a.n_items = p.n_items;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.q_rows = q_rows; a.row_last = row_last; a.rl_b = rl_bstride;
+  a.chunk = p.chunk; a.n_splits = p.n_splits;
+  a.part_o = (float*)workspace;
+  a.part_ml = (float*)workspace + (size_t)p.n_items * BM * D;
+
+  MergeArgs m = {};
+  m.q_rows = q_rows; m.row_last = row_last; m.rl_b = rl_bstride;
+  m.n_rows = n; m.n_q = Sq; m.G = a.G; m.Hkv = Hkv; m.n_kv = Skv; m.n_mtiles = p.n_mtiles;
+  m.n_splits = p.n_splits; m.chunk = p.chunk;
+  m.part_o = a.part_o; m.part_ml = a.part_ml;
+  m.epi = epi; m.n_anchor = (epi == DA_EPI_DELTA) ? n_anchor : 0;
+  m.o = o; m.os_b = o_str[0]; m.os_h = o_str[1]; m.os_s = o_str[2];
+  m.delta = delta;
+  if (d_str) { m.ds_b = d_str[0]; m.ds_h = d_str[1]; m.ds_a = d_str[2]; }
+
+  hipStream_t s = (hipStream_t)stream;
+  (void)hipGetLastError();
+  dispatch_attn<MODE_QSPARSE>(a, D, dtype, s);
+  const int n_tiles = B * Hkv * p.n_mtiles;
+  if (dtype == DA_BF16) {
+    if (D == 128) launch_merge<__bf16, 128>(m, n_tiles, s);
+    else launch_merge<__bf16, 64>(m, n_tiles, s);
+  } else {
+    if (D == 128) launch_merge<_Float16, 128>(m, n_tiles, s);
+    else launch_merge<_Float16, 64>(m, n_tiles, s);
+  }
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}

@@ -1,0 +1,172 @@
+// Kernel (3): delta broadcast-add (HBM-bound).
+//
+// One workgroup per (anchor group, batch): the group's delta row is read once
+// (from the delta buffer, or formed from the dense and sparse anchor rows) and
+// kept in registers while the threads stream the group's rows through
+// 16-byte loads and stores; consecutive threads cover consecutive 16-byte
+// chunks of one token row, so every row access is fully coalesced.
+#include "device_common.h"
+#include "capi_common.h"
+
+namespace da {
+
+struct DeltaArgs {
+  const void* sparse;
+  int64_t sp_b, sp_h, sp_s;
+  void* out;
+  int64_t o_b, o_h, o_s;
+  const void* delta;
+  int64_t d_b, d_h, d_a;
+  const void* dense;
+  int64_t ds_b, ds_h, ds_a;
+  const int64_t* anchors;
+  int n_anchor, gamma, s_p, H, D;
+};
+
+constexpr int DA_ROWS_UNROLL = 4;
+
+template <typename T, bool FROM_DENSE>
+__global__ __launch_bounds__(256) void delta_add_kernel(DeltaArgs a) {
+  using E = Elt<T>;
+  const int b = blockIdx.y;
+  int r0, r1, aidx;
+  if (a.anchors) {
+    // block 0 covers rows before anchors[0]; they take the last anchor's
+    // delta (searchsorted(..., right=True) - 1 == -1 picks the last entry).
+    const int g = (int)blockIdx.x - 1;
+    if (g < 0) {
+      r0 = 0;
+      r1 = (int)a.anchors[0];
+      aidx = a.n_anchor - 1;
+    } else {
+      r0 = (int)a.anchors[g];
+      r1 = g + 1 < a.n_anchor ? (int)a.anchors[g + 1] : a.s_p;
+      aidx = g;
+    }
+  } else {
+    aidx = blockIdx.x;
+    r0 = aidx * a.gamma;
+    r1 = r0 + a.gamma;
+  }
+  if (r0 < 0) r0 = 0;
+  if (r1 > a.s_p) r1 = a.s_p;
+  if (r0 >= r1) return;
+
+  const size_t esz = sizeof(T);
+  const int cpr = a.D / 8;
+  const int ncol = a.H * cpr;
+  const char* sp_base = (const char*)a.sparse + (int64_t)b * a.sp_b * esz;
+  char* o_base = (char*)a.out + (int64_t)b * a.o_b * esz;
+
+  for (int c = threadIdx.x; c < ncol; c += blockDim.x) {
+    const int h = c / cpr;
+    const int off8 = (c - h * cpr) * 8;
+    float dv[8];
+    if constexpr (FROM_DENSE) {
+      // anchors outside [0, s_p) are clamped so the read stays inside the rows
+      const int arow = (int)min(max(a.anchors[aidx], (int64_t)0), (int64_t)(a.s_p - 1));
+      const u32x4 dn = *(const u32x4*)((const char*)a.dense +
+          ((int64_t)b * a.ds_b + (int64_t)h * a.ds_h + (int64_t)aidx * a.ds_a + off8) * esz);
+      const u32x4 sa = *(const u32x4*)(sp_base + ((int64_t)h * a.sp_h + (int64_t)arow * a.sp_s + off8) * esz);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = E::pack2(E::lo(dn[e]) - E::lo(sa[e]), E::hi(dn[e]) - E::hi(sa[e]));
+        dv[2 * e] = E::lo(w);
+        dv[2 * e + 1] = E::hi(w);
+      }
+    } else {
+      const u32x4 dl = *(const u32x4*)((const char*)a.delta +
+          ((int64_t)b * a.d_b + (int64_t)h * a.d_h + (int64_t)aidx * a.d_a + off8) * esz);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dv[2 * e] = E::lo(dl[e]);
+        dv[2 * e + 1] = E::hi(dl[e]);
+      }
+    }
+    const int64_t sp_col = (int64_t)h * a.sp_h + off8;
+    const int64_t o_col = (int64_t)h * a.o_h + off8;
+    int r = r0;
+    for (; r + DA_ROWS_UNROLL <= r1; r += DA_ROWS_UNROLL) {
+      u32x4 x[DA_ROWS_UNROLL];
+#pragma unroll
+      for (int u = 0; u < DA_ROWS_UNROLL; ++u)
+        x[u] = *(const u32x4*)(sp_base + (sp_col + (int64_t)(r + u) * a.sp_s) * esz);
+#pragma unroll
+      for (int u = 0; u < DA_ROWS_UNROLL; ++u) {
+        u32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = E::pack2(E::lo(x[u][e]) + dv[2 * e], E::hi(x[u][e]) + dv[2 * e + 1]);
+        *(u32x4*)(o_base + (o_col + (int64_t)(r + u) * a.o_s) * esz) = y;
+      }
+    }
+    for (; r < r1; ++r) {
+      const u32x4 x = *(const u32x4*)(sp_base + (sp_col + (int64_t)r * a.sp_s) * esz);
+      u32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y[e] = E::pack2(E::lo(x[e]) + dv[2 * e], E::hi(x[e]) + dv[2 * e + 1]);
+      *(u32x4*)(o_base + (o_col + (int64_t)r * a.o_s) * esz) = y;
+    }
+  }
+}
+
+template <typename T>
+static void launch_delta(const DeltaArgs& a, dim3 grid, bool from_dense, hipStream_t s) {
+  if (from_dense)
+    hipLaunchKernelGGL((delta_add_kernel<T, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((delta_add_kernel<T, false>), grid, dim3(256), 0, s, a);
+}
+
+}  // namespace da
+
+using namespace da;
+
+extern "C" int da_delta_add(const void* sparse, const int64_t sp_str[3],
+                            void* out, const int64_t o_str[3],
+                            const void* delta, const int64_t d_str[3],
+                            const void* dense_sel, const int64_t ds_str[3],
+                            const int64_t* anchors, int n_anchor, int gamma, int s_p,
+                            int B, int H, int D, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_common(B, H, H, D, dtype)) != DA_OK) return rc;
+  if (s_p < 0 || n_anchor < 0 || !sp_str || !o_str) return DA_ERR_INVALID_ARG;
+  if (s_p == 0) return DA_OK;
+  if (!sparse || !out || n_anchor < 1) return DA_ERR_INVALID_ARG;
+  const bool from_dense = (delta == nullptr);
+  if (from_dense) {
+    if (!dense_sel || !ds_str || !anchors) return DA_ERR_INVALID_ARG;
+    if (dense_sel == out || sparse == out) return DA_ERR_INVALID_ARG;
+    if (!aligned16(dense_sel) || !strides8(ds_str)) return DA_ERR_ALIGNMENT;
+  } else {
+    if (!d_str) return DA_ERR_INVALID_ARG;
+    if (!aligned16(delta) || !strides8(d_str)) return DA_ERR_ALIGNMENT;
+  }
+  if (!anchors) {
+    if (gamma < 1) return DA_ERR_INVALID_ARG;
+    if ((int64_t)n_anchor * gamma < s_p) return DA_ERR_INVALID_ARG;
+  }
+  if (!aligned16(sparse) || !aligned16(out) || !strides8(sp_str) || !strides8(o_str))
+    return DA_ERR_ALIGNMENT;
+  if (B > 65535) return DA_ERR_INVALID_ARG;
+
+  DeltaArgs a = {};
+  a.sparse = sparse; a.sp_b = sp_str[0]; a.sp_h = sp_str[1]; a.sp_s = sp_str[2];
+  a.out = out; a.o_b = o_str[0]; a.o_h = o_str[1]; a.o_s = o_str[2];
+  a.delta = delta;
+  if (d_str) { a.d_b = d_str[0]; a.d_h = d_str[1]; a.d_a = d_str[2]; }
+  a.dense = dense_sel;
+  if (ds_str) { a.ds_b = ds_str[0]; a.ds_h = ds_str[1]; a.ds_a = ds_str[2]; }
+  a.anchors = anchors;
+  a.n_anchor = n_anchor; a.gamma = gamma; a.s_p = s_p; a.H = H; a.D = D;
+  const int groups = anchors ? n_anchor + 1 : (s_p + gamma - 1) / gamma;
+  const dim3 grid(groups, B);
+  hipStream_t s = (hipStream_t)stream;
+  (void)hipGetLastError();
+  if (dtype == DA_BF16) launch_delta<__bf16>(a, grid, from_dense, s);
+  else launch_delta<_Float16>(a, grid, from_dense, s);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}
+
+extern "C" const char* da_build_target(void) { return "gfx950"; }

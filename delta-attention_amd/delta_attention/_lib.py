@@ -1,0 +1,108 @@
+"""ctypes binding of libdelta_attn.so (the C ABI declared in include/delta_attn.h).
+
+The library is the only compute path: there is no fallback. If it is missing
+or fails to load, every op raises ExtensionMissing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libdelta_attn.so")
+
+DA_OK = 0
+DA_ERR_INVALID_ARG = -1
+DA_ERR_HEAD_DIM = -2
+DA_ERR_DTYPE = -3
+DA_ERR_ALIGNMENT = -4
+DA_ERR_WORKSPACE = -5
+DA_ERR_LAUNCH = -6
+
+DA_BF16 = 0
+DA_FP16 = 1
+
+DA_EPI_OUTPUT = 0
+DA_EPI_DELTA = 1
+DA_EPI_SCATTER = 2
+
+EXPORTS = (
+    "da_sparse_attn_fwd",
+    "da_qsparse_workspace_bytes",
+    "da_qsparse_attn_fwd",
+    "da_delta_add",
+    "da_build_target",
+)
+
+_ERR_TEXT = {
+    DA_ERR_INVALID_ARG: "invalid argument (shape, stride, range or null pointer)",
+    DA_ERR_HEAD_DIM: "unsupported head_dim (64 and 128 are supported)",
+    DA_ERR_DTYPE: "unsupported dtype (bfloat16 and float16 are supported)",
+    DA_ERR_ALIGNMENT: "tensor rows must be 16-byte aligned (strides multiple of 8 elements)",
+    DA_ERR_WORKSPACE: "workspace missing or too small",
+    DA_ERR_LAUNCH: "kernel launch failed",
+}
+
+
+class ExtensionMissing(RuntimeError):
+    """libdelta_attn.so is not built or cannot be loaded."""
+
+
+_lib = None
+
+I64x3 = ctypes.c_int64 * 3
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+_p3 = ctypes.POINTER(ctypes.c_int64)
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once; raise ExtensionMissing if it is not there."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ExtensionMissing(
+            f"{LIB_PATH} is not built: run `python delta-attention_amd/build_lib.py` "
+            "(or __graft_entry__.build()) first")
+    try:
+        L = ctypes.CDLL(LIB_PATH)
+    except OSError as e:  # pragma: no cover - depends on the machine
+        raise ExtensionMissing(f"cannot load {LIB_PATH}: {e}") from e
+    L.da_sparse_attn_fwd.restype = _i
+    L.da_sparse_attn_fwd.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                     _p3, _p3, _p3, _p3, _i, _i, _i, _f, _i, _vp]
+    L.da_qsparse_workspace_bytes.restype = _sz
+    L.da_qsparse_workspace_bytes.argtypes = [_i, _i, _i, _i, _i, _i]
+    L.da_qsparse_attn_fwd.restype = _i
+    L.da_qsparse_attn_fwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64,
+                                      _i, _i, _i, _i, _i, _i, _i,
+                                      _p3, _p3, _p3, _vp, _p3,
+                                      _i, _i, _vp, _p3, _f, _vp, _sz, _i, _vp]
+    L.da_delta_add.restype = _i
+    L.da_delta_add.argtypes = [_vp, _p3, _vp, _p3, _vp, _p3, _vp, _p3, _vp,
+                               _i, _i, _i, _i, _i, _i, _i, _vp]
+    L.da_build_target.restype = ctypes.c_char_p
+    L.da_build_target.argtypes = []
+    _lib = L
+    return L
+
+
+def check(rc: int, what: str) -> None:
+    """Map a DA_ERR_* code to the exception the reference raises for it:
+    argument problems are AssertionError (the reference asserts, e.g.
+    delta_kernel.py:267-268, 287), launch failures RuntimeError."""
+    if rc == DA_OK:
+        return
+    msg = f"{what}: {_ERR_TEXT.get(rc, 'error')} (code {rc})"
+    if rc == DA_ERR_LAUNCH:
+        raise RuntimeError(msg)
+    raise AssertionError(msg)
+
+
+def strides3(*s: int):
+    return I64x3(*[int(x) for x in s])

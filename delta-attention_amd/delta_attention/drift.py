@@ -1,0 +1,60 @@
+"""Prefill drift telemetry over the anchor deltas (delta_attention/drift.py).
+
+The fused path keeps the anchor deltas in a [b, n_anchors, h, d] buffer, the
+same tensor the reference summarises (llama.py:742-746), so the summary runs
+on it directly when `log_drift` is set.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, Iterable, List
+
+HIST_BINS = 40
+HIST_RANGE = (-1.0, 1.0)
+
+
+def drift_summary(dense_sparse_diff, layer_idx: int, gamma: int, seq_len: int) -> Dict[str, Any]:
+    """Cosine between consecutive anchor deltas (per head, over d): mean,
+    p10/p50/p90 and a HIST_BINS histogram over HIST_RANGE (drift.py:23-49)."""
+    import torch
+
+    a = dense_sparse_diff[:, :-1].float()
+    b = dense_sparse_diff[:, 1:].float()
+    flat = torch.nn.functional.cosine_similarity(a, b, dim=-1).flatten()
+    hist = torch.histc(flat, bins=HIST_BINS, min=HIST_RANGE[0], max=HIST_RANGE[1])
+    qs = torch.quantile(flat, torch.tensor([0.1, 0.5, 0.9], device=flat.device))
+    return {
+        "layer": int(layer_idx), "gamma": int(gamma), "seq_len": int(seq_len),
+        "n": int(flat.numel()), "mean": float(flat.mean().item()),
+        "p10": float(qs[0].item()), "p50": float(qs[1].item()), "p90": float(qs[2].item()),
+        "hist_bins": HIST_BINS, "hist_range": list(HIST_RANGE),
+        "hist": [int(x) for x in hist.tolist()],
+    }
+
+
+def aggregate_drift(lines: Iterable[Dict[str, Any]]) -> Dict[int, Dict[str, Any]]:
+    """One entry per layer: n-weighted mean, summed histograms; mismatched bins
+    are an error (drift.py:52-77)."""
+    out: Dict[int, Dict[str, Any]] = {}
+    for s in lines:
+        if s["hist_bins"] != HIST_BINS or list(s["hist_range"]) != list(HIST_RANGE):
+            raise ValueError(
+                f"drift sidecar bins/range {s['hist_bins']}/{s['hist_range']} do not match "
+                f"{HIST_BINS}/{list(HIST_RANGE)} (mixed-version sidecar files)")
+        layer = int(s["layer"])
+        agg = out.setdefault(layer, {"layer": layer, "n": 0, "mean": 0.0, "requests": 0,
+                                     "hist": [0] * HIST_BINS, "hist_bins": HIST_BINS,
+                                     "hist_range": list(HIST_RANGE), "gamma": s["gamma"]})
+        total = agg["n"] + s["n"]
+        if total > 0:
+            agg["mean"] = (agg["mean"] * agg["n"] + s["mean"] * s["n"]) / total
+        agg["n"] = total
+        agg["requests"] += 1
+        agg["hist"] = [x + y for x, y in zip(agg["hist"], s["hist"])]
+    return out
+
+
+def hist_bin_edges() -> List[float]:
+    lo, hi = HIST_RANGE
+    step = (hi - lo) / HIST_BINS
+    return [lo + i * step for i in range(HIST_BINS + 1)]

@@ -1,0 +1,244 @@
+"""Llama attention with the delta-attention prefill path
+(delta_attention/llama.py:60-192, 218-229, 364-496, 659-914 of the reference).
+
+`LlamaAttention.forward` projects q/k/v, applies RoPE and routes
+`config._attn_implementation == "window"` to `delta_forward`, which runs the
+three MI355X kernels: key-sparse attention (kernel 1), query-sparse dense rows
+with the fused delta epilogue (kernel 2) and the delta broadcast-add
+(kernel 3). The module's config object needs the Llama fields
+(hidden_size, num_attention_heads, num_key_value_heads, optional head_dim,
+attention_bias, attention_dropout, rms_norm_eps, _attn_implementation) and the
+pipeline knobs of `config.PIPELINE_FIELDS`.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+from torch import nn
+
+from . import ops
+from .delta_kernel import attention as qsa_kernel
+
+
+class LlamaRMSNorm(nn.Module):
+    """x / sqrt(mean(x^2) + eps) in float32, times the weight, in the input
+    dtype (llama.py:60-74)."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.variance_epsilon = eps
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        dt = hidden_states.dtype
+        x = hidden_states.to(torch.float32)
+        x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
+        return self.weight.to(dt) * x.to(dt)
+
+
+def rope_cos_sin(position_ids: torch.Tensor, head_dim: int, theta: float,
+                 dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Default RoPE tables for position_ids [b, s] -> cos/sin [b, s, head_dim]:
+    inv_freq = theta^(-2i/d), angles in float32, emb = cat(freqs, freqs)
+    (llama.py:129-158)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64,
+                                             device=position_ids.device).float() / head_dim))
+    freqs = position_ids[..., None].float() * inv_freq[None, None, :]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def apply_rotary_pos_emb(q, k, cos, sin, position_ids=None, unsqueeze_dim: int = 1):
+    """q*cos + rotate_half(q)*sin, same for k (llama.py:168-192)."""
+    cos = cos.unsqueeze(unsqueeze_dim)
+    sin = sin.unsqueeze(unsqueeze_dim)
+    return (q * cos) + (rotate_half(q) * sin), (k * cos) + (rotate_half(k) * sin)
+
+
+def repeat_kv(hidden_states: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """[b, hkv, s, d] -> [b, hkv * n_rep, s, d], head h reading kv head h // n_rep
+    (llama.py:218-229). The delta path never needs it: its kernels read the
+    Hkv heads directly."""
+    b, hkv, s, d = hidden_states.shape
+    if n_rep == 1:
+        return hidden_states
+    return hidden_states[:, :, None].expand(b, hkv, n_rep, s, d).reshape(b, hkv * n_rep, s, d)
+
+
+class LlamaAttention(nn.Module):
+
+    def __init__(self, config, layer_idx: int):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.head_dim = getattr(config, "head_dim", None) or config.hidden_size // config.num_attention_heads
+        self.num_key_value_groups = config.num_attention_heads // config.num_key_value_heads
+        self.scaling = self.head_dim ** -0.5
+        self.attention_dropout = getattr(config, "attention_dropout", 0.0)
+        self.is_causal = True
+        bias = getattr(config, "attention_bias", False)
+        self.q_proj = nn.Linear(config.hidden_size, config.num_attention_heads * self.head_dim, bias=bias)
+        self.k_proj = nn.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=bias)
+        self.v_proj = nn.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=bias)
+        self.o_proj = nn.Linear(config.num_attention_heads * self.head_dim, config.hidden_size, bias=bias)
+        self._drift_stats = None
+        self._stride_stats = None
+
+    # -- knobs -------------------------------------------------------------
+    def _sink(self) -> int:
+        return int(getattr(self.config, "sink_tokens", 1024))
+
+    # -- kernel (1) ----------------------------------------------------------
+    def hip_attention_interface(self, module, query, key, value, attention_mask,
+                                dropout: float = 0.0, scaling: Optional[float] = None,
+                                sliding_window: Optional[int] = None, softcap=None,
+                                position_ids=None, output_attentions: bool = False,
+                                use_cache: bool = False, rope_cos=None, rope_sin=None,
+                                out: Optional[torch.Tensor] = None):
+        """Key-sparse (sink + sliding window) attention; returns ([b, s, h, d], None)
+        (llama.py:364-449, "window" branch). fp32 inputs run in bf16 and the
+        result is cast back (llama.py:382-388, 493-494)."""
+        assert self.config._attn_implementation == "window", (
+            f"{self.config._attn_implementation!r}: only the 'window' sparse pass is built")
+        assert softcap is None and not output_attentions
+        original_dtype = query.dtype
+        if query.dtype == torch.float32:
+            query, key, value = query.to(torch.bfloat16), key.to(torch.bfloat16), value.to(torch.bfloat16)
+        assert query.dtype in (torch.bfloat16, torch.float16), query.dtype
+        scaling = self.scaling if scaling is None else scaling
+        window = sliding_window if sliding_window is not None else 1024
+        output = ops.sparse_attention(query, key, value, window=int(window), sink=self._sink(),
+                                      sm_scale=float(scaling), out=out)
+        if output.dtype != original_dtype:
+            output = output.to(original_dtype)
+        return output, None
+
+    # -- the delta composition -------------------------------------------------
+    def delta_forward(self, module, query_states, key_states, value_states,
+                      attention_mask=None, dropout: float = 0.0, scaling: float = 1.0, **kwargs):
+        """Delta attention prefill (llama.py:659-757). q [b, h, s, d] and k/v
+        [b, hkv, s, d] post-RoPE -> ([b, s, h, d], None).
+
+        mode "sparse-only": kernel (1) only. "recompute": kernel (1), then the
+        selected rows (anchors every delta_lambda rows + the cut_n dense tail)
+        are replaced by dense rows. "delta": kernel (2) writes the tail rows and
+        the anchor deltas, kernel (3) adds each delta over its stride group.
+        """
+        cfg = self.config
+        lambd = int(cfg.delta_lambda)
+        window = int(cfg.sliding_window)
+        mode = cfg.mode
+        b, h, s, d = query_states.size()
+        assert h == cfg.num_attention_heads, (h, s)
+
+        if getattr(cfg, "stride_policy", "fixed") == "adaptive" and mode == "delta":
+            sparse, _ = self.hip_attention_interface(self, query_states, key_states, value_states,
+                                                     attention_mask, scaling=scaling,
+                                                     sliding_window=window)
+            cut_n = s % lambd + max(128, lambd)
+            s_p = s - cut_n
+            return self.delta_adaptive_forward(query_states, key_states, value_states, sparse,
+                                               s, s_p, cut_n, scaling), None
+
+        original_dtype = query_states.dtype
+        q, k, v = query_states, key_states, value_states
+        if q.dtype == torch.float32:
+            q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+        log_drift = bool(getattr(cfg, "log_drift", False)) and mode == "delta"
+        out, delta = ops.delta_prefill(q, k, v, gamma=lambd, window=window, sink=self._sink(),
+                                       sm_scale=float(scaling), mode=mode, return_delta=True)
+        if log_drift and delta is not None and delta.shape[1] >= 2:
+            from .drift import drift_summary
+
+            self._drift_stats = drift_summary(delta, self.layer_idx, lambd, s)
+        if out.dtype != original_dtype:
+            out = out.to(original_dtype)
+        return out, None
+
+    def delta_adaptive_forward(self, query_states, key_states, value_states, sparse_attn_output,
+                               s, s_p, cut_n, scaling):
+        """Chunked adaptive anchor placement (llama.py:759-824): anchors at the
+        current stride inside each adapt_chunk rows, stride re-planned from the
+        chunk's mean consecutive-delta cosine, variable-stride broadcast
+        (kernel 3 with an anchor list), dense cut_n tail."""
+        from .stride import (apply_delta_variable, effective_sparsity, interanchor_cos,
+                             next_gamma, next_gamma_relative, plan_chunks)
+
+        cfg = self.config
+        device = query_states.device
+        q, k, v = query_states, key_states, value_states
+        if q.dtype == torch.float32:
+            q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+            sparse_attn_output = sparse_attn_output.to(torch.bfloat16)
+        gamma_c = int(cfg.delta_lambda)
+        trigger = getattr(cfg, "stride_trigger", "absolute")
+        cos_history, idx_parts, dense_parts, chunk_log = [], [], [], []
+        for start, end in plan_chunks(s_p, int(cfg.adapt_chunk)):
+            c_idx = torch.arange(start, end, step=gamma_c, device=device)
+            dense_c = qsa_kernel(q[:, :, c_idx], k, v, c_idx.unsqueeze(0), scaling).transpose(1, 2)
+            cos_mean, cos_min = interanchor_cos(dense_c - sparse_attn_output[:, c_idx])
+            idx_parts.append(c_idx)
+            dense_parts.append(dense_c)
+            chunk_log.append({"start": int(start), "gamma": int(gamma_c), "cos_mean": cos_mean,
+                              "cos_min": cos_min, "n_anchors": int(c_idx.numel())})
+            if trigger == "relative":
+                gamma_c = next_gamma_relative(cos_mean, cos_history, gamma_c,
+                                              k=float(getattr(cfg, "adapt_k", 2.0)),
+                                              gamma_min=int(cfg.gamma_min), gamma_max=int(cfg.gamma_max))
+                cos_history.append(cos_mean)
+            else:
+                gamma_c = next_gamma(cos_mean, gamma_c, threshold=float(cfg.adapt_threshold),
+                                     gamma_min=int(cfg.gamma_min), gamma_max=int(cfg.gamma_max))
+        idx = torch.cat(idx_parts)
+        dense_sel = torch.cat(dense_parts, dim=1).contiguous()
+        corrected = apply_delta_variable(sparse_attn_output[:, :s_p], dense_sel, idx, s_p)
+        tail_idx = torch.arange(s_p, s, device=device)
+        tail_dense = qsa_kernel(q[:, :, tail_idx], k, v, tail_idx.unsqueeze(0), scaling).transpose(1, 2)
+        self._stride_stats = {
+            "kind": "stride", "layer": int(self.layer_idx), "seq_len": int(s),
+            "effective_sparsity": effective_sparsity(torch.cat((idx, tail_idx)), s,
+                                                     int(cfg.sliding_window), self._sink()),
+            "n_anchors": int(idx.numel()), "chunks": chunk_log,
+        }
+        out = torch.cat((corrected, tail_dense), dim=1)
+        return out.to(query_states.dtype)
+
+    # -- projections and dispatch -----------------------------------------------
+    def _qkv(self, hidden_states, hidden_shape):
+        q = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        return q, k, v
+
+    def forward(self, hidden_states, position_embeddings, attention_mask=None,
+                past_key_value=None, cache_position=None, **kwargs):
+        """hidden [b, s, hidden] -> (o_proj(attention) [b, s, hidden], None)
+        (llama.py:832-914); `window` routes to delta_forward."""
+        input_shape = hidden_states.shape[:-1]
+        hidden_shape = (*input_shape, -1, self.head_dim)
+        query_states, key_states, value_states = self._qkv(hidden_states, hidden_shape)
+        cos, sin = position_embeddings
+        query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin)
+        if past_key_value is not None:
+            key_states, value_states = past_key_value.update(
+                key_states, value_states, self.layer_idx,
+                {"sin": sin, "cos": cos, "cache_position": cache_position})
+        impl = self.config._attn_implementation
+        if impl != "window":
+            raise NotImplementedError(
+                f"attention implementation {impl!r} is not part of the MI355X delta path "
+                "(use 'window')")
+        attn_output, attn_weights = self.delta_forward(
+            self, query_states, key_states, value_states, attention_mask,
+            dropout=0.0 if not self.training else self.attention_dropout, scaling=self.scaling)
+        assert attn_output.shape[-2] == self.config.num_attention_heads, attn_output.shape
+        b, s, _, _ = attn_output.size()
+        attn_output = attn_output.reshape(b, s, -1)
+        return self.o_proj(attn_output), attn_weights

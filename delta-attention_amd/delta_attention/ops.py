@@ -1,0 +1,257 @@
+"""Torch-tensor entry points over the C ABI.
+
+PyTorch is used here for device memory and the current HIP stream only; all
+attention arithmetic runs in libdelta_attn.so. Every op launches
+asynchronously on torch's current stream of the tensors' device and never
+synchronises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib as L
+
+_DTYPE = {torch.bfloat16: L.DA_BF16, torch.float16: L.DA_FP16}
+Q_BLOCK = 64  # hip-attn's block_sparse_block_size_q (config.py:117, :136)
+
+
+def _code(t: torch.Tensor) -> int:
+    code = _DTYPE.get(t.dtype)
+    assert code is not None, f"dtype {t.dtype} is not supported (bfloat16, float16)"
+    return code
+
+
+def _ready(t: torch.Tensor) -> torch.Tensor:
+    """Rows contiguous and 16-byte aligned, as the kernels read them; other
+    dimensions keep their strides (no copy for the usual transposed views)."""
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+          and all(s % 8 == 0 for s in t.stride()[:-1]))
+    return t if ok else t.contiguous()
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _on_gpu(*ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    for t in ts:
+        assert t.is_cuda, "delta-attention kernels need GPU tensors"
+        assert t.device == dev, "all tensors must be on one device"
+    return dev
+
+
+# ---------------------------------------------------------------------------
+# kernel (1)
+
+def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int,
+                     sink: int, sm_scale: float, q_block: int = Q_BLOCK,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal sink + block-anchored sliding-window attention.
+
+    q [B,H,S,D], k/v [B,Hkv,S,D] (any strides, GQA native) -> out [B,S,H,D].
+    A key k is visible to row r iff k <= r and (k < sink or
+    k + window > floor(r/q_block)*q_block + q_block - 1)
+    (delta_attention/train/flex_delta.py:59-61).
+    """
+    assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    assert k.shape == (B, Hkv, S, D) and v.shape == (B, Hkv, S, D), (q.shape, k.shape, v.shape)
+    assert H % Hkv == 0, (H, Hkv)
+    assert q.dtype == k.dtype == v.dtype
+    dev = _on_gpu(q, k, v)
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    if out is None:
+        out = torch.empty((B, S, H, D), device=dev, dtype=q.dtype)
+    assert out.shape == (B, S, H, D) and out.dtype == q.dtype
+    assert out.stride(-1) == 1 and out.data_ptr() % 16 == 0
+    with torch.cuda.device(dev):
+        rc = L.lib().da_sparse_attn_fwd(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, S, D,
+            L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+            L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+            L.strides3(v.stride(0), v.stride(1), v.stride(2)),
+            L.strides3(out.stride(0), out.stride(2), out.stride(1)),
+            int(window), int(sink), int(q_block), float(sm_scale), _code(q), _stream(dev))
+    L.check(rc, "da_sparse_attn_fwd")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# kernel (2)
+
+def qsparse_workspace(B: int, H: int, Hkv: int, n: int, Skv: int, D: int, device) -> torch.Tensor:
+    nbytes = int(L.lib().da_qsparse_workspace_bytes(B, H, Hkv, n, Skv, D))
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def _row_limits(row_last: torch.Tensor, B: int, n: int) -> Tuple[torch.Tensor, int]:
+    rl = row_last
+    if rl.dim() == 1:
+        rl = rl.unsqueeze(0)
+    assert rl.dim() == 2 and rl.shape[1] == n and rl.shape[0] in (1, B), (row_last.shape, B, n)
+    if rl.dtype != torch.int64:
+        rl = rl.to(torch.int64)
+    rl = rl.contiguous()
+    return rl, (0 if rl.shape[0] == 1 else rl.stride(0))
+
+
+def qsparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      row_last: torch.Tensor, sm_scale: float, *,
+                      q_rows: Optional[torch.Tensor] = None,
+                      epi: int = L.DA_EPI_OUTPUT, out: Optional[torch.Tensor] = None,
+                      n_anchor: int = 0, delta: Optional[torch.Tensor] = None,
+                      workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Query-sparse, key-dense attention: selected row i attends keys
+    0..row_last[i] (inclusive), split over the key axis on the GPU.
+
+    q [B,H,Sq,D]; k/v [B,Hkv,Skv,D] (GQA native, any strides);
+    q_rows: optional [n] int64 rows of q to use (default: rows 0..n-1, n = len(row_last)).
+    epi == DA_EPI_OUTPUT: returns o [B,H,n,D] (new, or `out`).
+    epi == DA_EPI_DELTA / DA_EPI_SCATTER: `out` is the [B,S,H,D] layer output;
+    see include/delta_attn.h.
+    """
+    B, H, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    assert k.shape == (B, Hkv, Skv, D) and v.shape == k.shape, (q.shape, k.shape, v.shape)
+    assert H % Hkv == 0 and q.dtype == k.dtype == v.dtype
+    n = row_last.shape[-1]
+    dev = _on_gpu(q, k, v, row_last)
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    rl, rl_b = _row_limits(row_last, B, n)
+    if q_rows is not None:
+        assert q_rows.numel() == n
+        q_rows = q_rows.reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
+    else:
+        assert n <= Sq, (n, Sq)
+    if epi == L.DA_EPI_OUTPUT:
+        if out is None:
+            out = torch.empty((B, H, n, D), device=dev, dtype=q.dtype)
+        assert out.shape == (B, H, n, D)
+        o_str = L.strides3(out.stride(0), out.stride(1), out.stride(2))
+    else:
+        assert out is not None and out.dim() == 4 and out.shape[0] == B and out.shape[2] == H
+        o_str = L.strides3(out.stride(0), out.stride(2), out.stride(1))
+    assert out.dtype == q.dtype and out.stride(-1) == 1
+    d_str = None
+    if epi == L.DA_EPI_DELTA and n_anchor > 0:
+        assert delta is not None and delta.shape == (B, n_anchor, H, D) and delta.dtype == q.dtype
+        d_str = L.strides3(delta.stride(0), delta.stride(2), delta.stride(1))
+    if workspace is None:
+        workspace = qsparse_workspace(B, H, Hkv, n, Skv, D, dev)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_qsparse_attn_fwd(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(q_rows), _ptr(rl), int(rl_b),
+            n, B, H, Hkv, Sq, Skv, D,
+            L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+            L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+            L.strides3(v.stride(0), v.stride(1), v.stride(2)),
+            _ptr(out), o_str, int(epi), int(n_anchor), _ptr(delta), d_str,
+            float(sm_scale), _ptr(workspace), workspace.numel(), _code(q), _stream(dev))
+    L.check(rc, "da_qsparse_attn_fwd")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# kernel (3)
+
+def delta_add(sparse: torch.Tensor, *, s_p: int, out: Optional[torch.Tensor] = None,
+              delta: Optional[torch.Tensor] = None, dense_sel: Optional[torch.Tensor] = None,
+              anchors: Optional[torch.Tensor] = None, gamma: int = 0) -> torch.Tensor:
+    """out[:, r] = sparse[:, r] + delta[:, owner(r)] for r < s_p ([B,S,H,D] tensors).
+
+    owner(r) = r // gamma (anchors None) or the last anchor <= r. The delta is
+    `delta` [B,n,H,D], or rnd(dense_sel - sparse[:, anchors]) when `delta` is None.
+    `out` defaults to a new [B,s_p,H,D] tensor; out=sparse runs in place
+    (allowed with a precomputed delta only).
+    """
+    B, _, H, D = sparse.shape
+    dev = _on_gpu(sparse)
+    if out is None:
+        out = torch.empty((B, s_p, H, D), device=dev, dtype=sparse.dtype)
+    assert out.dtype == sparse.dtype and out.shape[0] == B and out.shape[2:] == (H, D)
+    if delta is not None:
+        n = delta.shape[1]
+        d_str = L.strides3(delta.stride(0), delta.stride(2), delta.stride(1))
+        ds_str = None
+    else:
+        assert dense_sel is not None and anchors is not None
+        n = dense_sel.shape[1]
+        d_str = None
+        ds_str = L.strides3(dense_sel.stride(0), dense_sel.stride(2), dense_sel.stride(1))
+    if anchors is not None:
+        anchors = anchors.reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
+        assert anchors.numel() == n
+    with torch.cuda.device(dev):
+        rc = L.lib().da_delta_add(
+            _ptr(sparse), L.strides3(sparse.stride(0), sparse.stride(2), sparse.stride(1)),
+            _ptr(out), L.strides3(out.stride(0), out.stride(2), out.stride(1)),
+            _ptr(delta), d_str, _ptr(dense_sel), ds_str, _ptr(anchors),
+            int(n), int(gamma), int(s_p), B, H, D, _code(sparse), _stream(dev))
+    L.check(rc, "da_delta_add")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# the composed layer prefill (kernels 1 -> 2 -> 3)
+
+def anchor_layout(s: int, gamma: int) -> Tuple[int, int, int]:
+    """(cut_n, s_p, n_anchor) of delta_forward's fixed-stride layout
+    (llama.py:692-693, 711-714): cut_n = s % gamma + max(128, gamma)."""
+    cut_n = s % gamma + max(128, gamma)
+    s_p = s - cut_n
+    n_anchor = -(-s_p // gamma) if s_p > 0 else 0
+    return cut_n, s_p, n_anchor
+
+
+@functools.lru_cache(maxsize=64)
+def selected_rows(s: int, gamma: int, device: str) -> torch.Tensor:
+    """Anchor rows 0, gamma, ... < s_p followed by the dense tail s_p .. s-1
+    (int64, on `device`)."""
+    _, s_p, _ = anchor_layout(s, gamma)
+    s_p = max(s_p, 0)
+    return torch.cat([torch.arange(0, s_p, gamma, dtype=torch.int64),
+                      torch.arange(s_p, s, dtype=torch.int64)]).to(device)
+
+
+def delta_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, gamma: int,
+                  window: int, sink: int, sm_scale: float, mode: str = "delta",
+                  out: Optional[torch.Tensor] = None,
+                  return_delta: bool = False):
+    """One delta-attention layer prefill: q [B,H,s,D], k/v [B,Hkv,s,D] (post-RoPE)
+    -> [B,s,H,D] (llama.py:659-757).
+
+    mode "sparse-only": the key-sparse output; "recompute": sparse rows with
+    the selected rows replaced by dense ones; "delta": sparse + the delta of
+    the anchor at or before each row, dense tail rows.
+    When s <= cut_n there are no anchors and every row is computed densely.
+    return_delta: also return the [B,n_anchor,H,D] anchor deltas (drift telemetry).
+    """
+    assert mode in ("delta", "recompute", "sparse-only"), mode
+    assert gamma >= 1
+    B, H, s, D = q.shape
+    out = sparse_attention(q, k, v, window=window, sink=sink, sm_scale=sm_scale, out=out)
+    if mode == "sparse-only":
+        return (out, None) if return_delta else out
+    cut_n, s_p, n_anchor = anchor_layout(s, gamma)
+    idx = selected_rows(s, gamma, str(q.device))
+    ws = qsparse_workspace(B, H, k.shape[1], idx.numel(), s, D, q.device)
+    if mode == "recompute" or s_p <= 0:
+        qsparse_attention(q, k, v, idx, sm_scale, q_rows=idx, epi=L.DA_EPI_SCATTER,
+                          out=out, workspace=ws)
+        return (out, None) if return_delta else out
+    delta = torch.empty((B, n_anchor, H, D), device=q.device, dtype=q.dtype)
+    qsparse_attention(q, k, v, idx, sm_scale, q_rows=idx, epi=L.DA_EPI_DELTA, out=out,
+                      n_anchor=n_anchor, delta=delta, workspace=ws)
+    delta_add(out, s_p=s_p, out=out, delta=delta, gamma=gamma)
+    return (out, delta) if return_delta else out

@@ -1,0 +1,142 @@
+/*
+ * delta_attn.h -- C ABI of the MI355X (gfx950) Delta Attention prefill path.
+ *
+ * Three kernels make up one delta-attention layer prefill:
+ *   (1) key-sparse attention: causal sliding window + sink tokens, with the
+ *       window anchored at the last row of each q_block-row query block;
+ *   (2) query-sparse / key-dense attention: a chosen set of query rows, each
+ *       attending every key up to its own inclusive limit, optionally fused
+ *       with the delta epilogue (delta = dense - sparse at anchor rows,
+ *       dense rows scattered straight into the layer output);
+ *   (3) delta broadcast-add: every row gets the delta of the nearest
+ *       anchor at or before it.
+ *
+ * Conventions shared by every entry point:
+ *   - Tensors are device pointers. The last (head_dim) dimension is
+ *     contiguous; every other dimension is described by an element stride
+ *     (not a byte stride). Rows must be 16-byte aligned: base pointers
+ *     16-byte aligned and every stride a multiple of 8 elements.
+ *   - dtype is DA_BF16 or DA_FP16; compute is fp32 accumulate on MFMA.
+ *   - Everything is asynchronous on `stream` (a hipStream_t; NULL = default
+ *     stream). No entry point synchronises, allocates or frees; the caller
+ *     owns all memory, including workspaces.
+ *   - Return 0 on success or a negative DA_ERR_* code. No entry point keeps
+ *     a pointer after it returns and there is no mutable global state, so
+ *     calls are re-entrant.
+ */
+#ifndef DELTA_ATTN_H
+#define DELTA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DA_OK 0
+#define DA_ERR_INVALID_ARG (-1)      /* shape, stride, range or null-pointer error */
+#define DA_ERR_HEAD_DIM (-2)         /* head_dim not supported (64 and 128 are) */
+#define DA_ERR_DTYPE (-3)            /* dtype not DA_BF16 / DA_FP16 */
+#define DA_ERR_ALIGNMENT (-4)        /* pointer or stride breaks 16-byte row alignment */
+#define DA_ERR_WORKSPACE (-5)        /* workspace missing or smaller than required */
+#define DA_ERR_LAUNCH (-6)           /* hipGetLastError reported a launch failure */
+
+#define DA_BF16 0
+#define DA_FP16 1
+
+/* Epilogue modes of da_qsparse_attn_fwd. */
+#define DA_EPI_OUTPUT 0    /* o[b, h, i, :] = attention row i (the plain kernel) */
+#define DA_EPI_DELTA 1     /* rows i < n_anchor: delta[b, i, h, :] = dense - sparse[b, q_rows[i], h, :];
+                              rows i >= n_anchor: out[b, q_rows[i], h, :] = dense */
+#define DA_EPI_SCATTER 2   /* out[b, q_rows[i], h, :] = dense for every row (mode "recompute") */
+
+/*
+ * Kernel (1): key-sparse attention (sink + block-anchored sliding window).
+ * Replaces hip-attn `block_sparse_attention` as called from
+ * delta_attention/llama.py:407-449 (LlamaAttention.hip_attention_interface,
+ * "window" branch); visibility follows delta_attention/train/flex_delta.py:59-61:
+ *   key k is visible to row r  iff  k <= r  and  (k < sink  or
+ *   k + window > floor(r / q_block) * q_block + q_block - 1).
+ * q [B, Hq, S, D] (strides q_str = {batch, head, seq}), k/v [B, Hkv, S, D],
+ * out [B, S, Hq, D] layout given by o_str = {batch, head, seq}; Hq % Hkv == 0
+ * (GQA: query head h reads key/value head h / (Hq / Hkv)).
+ * sm_scale multiplies q.k before the softmax.
+ */
+int da_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                       int B, int Hq, int Hkv, int S, int D,
+                       const int64_t q_str[3], const int64_t k_str[3],
+                       const int64_t v_str[3], const int64_t o_str[3],
+                       int window, int sink, int q_block, float sm_scale,
+                       int dtype, void* stream);
+
+/*
+ * Workspace (bytes) that da_qsparse_attn_fwd needs for these sizes; 0 is a
+ * valid answer. n = number of selected query rows, Skv = number of keys.
+ */
+size_t da_qsparse_workspace_bytes(int B, int Hq, int Hkv, int n, int Skv, int D);
+
+/*
+ * Kernel (2): query-sparse / key-dense attention with split-KV.
+ * Replaces the Triton `_attn_fwd` behind delta_attention/delta_kernel.py:262-329
+ * (`attention(q, k, v, mask, sm_scale)`), called at llama.py:720 / :786 / :814.
+ * Row i of the selection reads query row q_rows[i] (q_rows == NULL: row i) of q
+ * and attends keys 0 .. row_last[b * rl_bstride + i] inclusive (limits need not
+ * be sorted; rl_bstride 0 shares one limit vector over the batch). Limits are
+ * clamped to Skv - 1; a negative limit gives an all-zero row; q_rows values
+ * are clamped into [0, Sq).
+ * q [B, Hq, Sq, D]; k/v [B, Hkv, Skv, D].
+ *   epi == DA_EPI_OUTPUT : o [B, Hq, n, D] with o_str = {batch, head, row}.
+ *   epi == DA_EPI_DELTA  : `o` is the layer output [B, S, Hq, D] (o_str =
+ *       {batch, head, seq}) holding the sparse rows; `delta` is
+ *       [B, n_anchor, Hq, D] in `dtype` with d_str = {batch, head, anchor}.
+ *       Rounding follows the reference's bf16 composition
+ *       (delta_attention/llama.py:740): delta = rnd(rnd(dense) - sparse).
+ *   epi == DA_EPI_SCATTER: `o` as for DA_EPI_DELTA, every row written.
+ * workspace must hold da_qsparse_workspace_bytes(...) bytes.
+ */
+int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
+                        const int64_t* q_rows, const int64_t* row_last, int64_t rl_bstride,
+                        int n, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                        const int64_t q_str[3], const int64_t k_str[3], const int64_t v_str[3],
+                        void* o, const int64_t o_str[3],
+                        int epi, int n_anchor, void* delta, const int64_t d_str[3],
+                        float sm_scale, void* workspace, size_t workspace_bytes,
+                        int dtype, void* stream);
+
+/*
+ * Kernel (3): delta broadcast-add over rows 0 .. s_p-1.
+ * Replaces the torch broadcast at delta_attention/llama.py:740-755 (uniform
+ * stride) and delta_attention/stride.py:26-40 (`apply_delta_variable`).
+ * out[b, r, h, :] = sparse[b, r, h, :] + delta_of(owner(r))[b, h, :]
+ * where owner(r) = r / gamma when anchors == NULL, else the index of the last
+ * anchor <= r (rows before anchors[0] take the last anchor, matching the
+ * reference's searchsorted(...) - 1 == -1 indexing).
+ * The delta comes from `delta` ([B, n_anchor, H, D] in `dtype`, d_str) when it
+ * is non-NULL, else it is formed as rnd(dense_sel[b, a, h, :] -
+ * sparse[b, anchors[a], h, :]) (dense_sel [B, n_anchor, H, D] with ds_str;
+ * requires anchors). Arithmetic is fp32 with one rounding to `dtype` per
+ * operation, the same sequence as the reference's torch ops, so results are
+ * bit-identical to them on the same inputs.
+ * sparse/out are [B, >=s_p, H, D] (strides {batch, head, seq}). With a
+ * precomputed `delta`, out may alias sparse (in-place); when the delta is
+ * formed from dense_sel, out must not alias sparse. With anchors == NULL,
+ * n_anchor must be at least ceil(s_p / gamma); with anchors, they must be
+ * ascending (values outside [0, s_p) are clamped into it when the delta is
+ * formed from dense_sel).
+ */
+int da_delta_add(const void* sparse, const int64_t sp_str[3],
+                 void* out, const int64_t o_str[3],
+                 const void* delta, const int64_t d_str[3],
+                 const void* dense_sel, const int64_t ds_str[3],
+                 const int64_t* anchors, int n_anchor, int gamma, int s_p,
+                 int B, int H, int D, int dtype, void* stream);
+
+/* Library identification: the gfx target the code objects were built for. */
+const char* da_build_target(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DELTA_ATTN_H */

@@ -1,0 +1,108 @@
+"""The C-ABI library: it builds, loads, exports every declared symbol, and
+rejects bad arguments with the documented codes before touching the GPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+import conftest  # noqa: F401  (paths)
+from delta_attention import _lib as L
+
+HEADER = os.path.join(conftest.REPO, "include", "delta_attn.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(L.LIB_PATH):
+        import build_lib
+        build_lib.build()
+    return L.lib()
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^[a-z][\w\s\*]*?\b(da_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_symbols() == sorted(L.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.da_build_target() == b"gfx950"
+    blob = open(L.LIB_PATH, "rb").read()
+    assert b"gfx950" in blob
+
+
+def _s3(*v):
+    return L.strides3(*v)
+
+
+def _sparse(lib, **kw):
+    a = dict(q=16, k=16, v=16, out=16, B=1, Hq=8, Hkv=2, S=128, D=128,
+             qs=(8 * 128 * 128, 128 * 128, 128), ks=(2 * 128 * 128, 128 * 128, 128),
+             os_=(128 * 8 * 128, 128, 8 * 128), window=64, sink=4, qb=64, dtype=L.DA_BF16)
+    a.update(kw)
+    return lib.da_sparse_attn_fwd(ctypes.c_void_p(a["q"]), ctypes.c_void_p(a["k"]),
+                                  ctypes.c_void_p(a["v"]), ctypes.c_void_p(a["out"]),
+                                  a["B"], a["Hq"], a["Hkv"], a["S"], a["D"],
+                                  _s3(*a["qs"]), _s3(*a["ks"]), _s3(*a["ks"]), _s3(*a["os_"]),
+                                  a["window"], a["sink"], a["qb"], 0.1, a["dtype"], None)
+
+
+def test_sparse_rejects_bad_arguments(lib):
+    assert _sparse(lib, dtype=7) == L.DA_ERR_DTYPE
+    assert _sparse(lib, D=96) == L.DA_ERR_HEAD_DIM
+    assert _sparse(lib, D=256) == L.DA_ERR_HEAD_DIM
+    assert _sparse(lib, Hq=6, Hkv=4) == L.DA_ERR_INVALID_ARG
+    assert _sparse(lib, q=0) == L.DA_ERR_INVALID_ARG
+    assert _sparse(lib, q=24) == L.DA_ERR_ALIGNMENT
+    assert _sparse(lib, qs=(8 * 128 * 128, 128 * 128, 132)) == L.DA_ERR_ALIGNMENT
+    assert _sparse(lib, window=-1) == L.DA_ERR_INVALID_ARG
+    assert _sparse(lib, qb=0) == L.DA_ERR_INVALID_ARG
+    assert _sparse(lib, S=0) == L.DA_OK          # nothing to do, nothing launched
+
+
+def test_qsparse_workspace_and_checks(lib):
+    ws = lib.da_qsparse_workspace_bytes
+    assert ws(1, 32, 8, 2174, 131072, 128) > 0
+    assert ws(1, 32, 8, 2174, 131072, 128) >= ws(1, 32, 8, 100, 131072, 128)
+    assert ws(1, 32, 8, 10, 100, 96) == 0
+    assert ws(1, 6, 4, 10, 100, 128) == 0
+    need = ws(1, 8, 2, 64, 1024, 128)
+    s3 = _s3(8 * 1024 * 128, 1024 * 128, 128)
+
+    def call(workspace=4096, nbytes=None, epi=L.DA_EPI_OUTPUT, D=128, row_last=16, n_anchor=0, delta=0):
+        return lib.da_qsparse_attn_fwd(
+            ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), None,
+            ctypes.c_void_p(row_last), 0, 64, 1, 8, 2, 1024, 1024, D, s3, s3, s3,
+            ctypes.c_void_p(16), s3, epi, n_anchor, ctypes.c_void_p(delta), s3, 0.1,
+            ctypes.c_void_p(workspace), need if nbytes is None else nbytes, L.DA_BF16, None)
+
+    assert call(nbytes=need - 1) == L.DA_ERR_WORKSPACE
+    assert call(workspace=0) == L.DA_ERR_WORKSPACE
+    assert call(epi=9) == L.DA_ERR_INVALID_ARG
+    assert call(D=80) == L.DA_ERR_HEAD_DIM
+    assert call(row_last=0) == L.DA_ERR_INVALID_ARG
+    assert call(epi=L.DA_EPI_DELTA, n_anchor=65, delta=16) == L.DA_ERR_INVALID_ARG
+    assert call(epi=L.DA_EPI_DELTA, n_anchor=4, delta=0) == L.DA_ERR_INVALID_ARG
+
+
+def test_delta_add_checks(lib):
+    s3 = _s3(4096 * 32 * 128, 128, 32 * 128)
+
+    def call(delta=16, dense=0, anchors=0, n=64, gamma=64, s_p=4096, sparse=16, out=32):
+        return lib.da_delta_add(ctypes.c_void_p(sparse), s3, ctypes.c_void_p(out), s3,
+                                ctypes.c_void_p(delta), s3, ctypes.c_void_p(dense), s3,
+                                ctypes.c_void_p(anchors), n, gamma, s_p, 1, 32, 128, L.DA_BF16, None)
+
+    assert call(n=63) == L.DA_ERR_INVALID_ARG                 # too few deltas for s_p / gamma
+    assert call(gamma=0) == L.DA_ERR_INVALID_ARG
+    assert call(delta=0, dense=16, anchors=0) == L.DA_ERR_INVALID_ARG    # dense form needs anchors
+    assert call(delta=0, dense=16, anchors=16, out=16) == L.DA_ERR_INVALID_ARG  # no aliasing
+    assert call(delta=8) == L.DA_ERR_ALIGNMENT
+    assert call(s_p=0) == L.DA_OK

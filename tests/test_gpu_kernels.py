@@ -1,0 +1,154 @@
+"""GPU parity of the three kernels against the oracle on identical seeded
+inputs (the oracle runs in float64 on the bf16/fp16-rounded values).
+
+Tolerance (the reference's T1 gate, tests/test_math_identities.py:85-89, and
+the north-star bar): per-row cosine > 0.999 and max |diff| < 2e-2 for the
+attention kernels; the delta-add kernel is bit-exact against the reference's
+bf16 elementwise arithmetic.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, gen_qkv, np64
+from oracle import delta_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _sparse_case(B, H, Hkv, S, D, window, sink, qb=64, dtype=torch.bfloat16, seed=0,
+                 model_layout=False, scale=None):
+    from delta_attention import ops
+    q, k, v = gen_qkv(B, H, Hkv, S, D, seed=seed, dtype=dtype, model_layout=model_layout)
+    scale = D ** -0.5 if scale is None else scale
+    out = ops.sparse_attention(q, k, v, window=window, sink=sink, sm_scale=scale, q_block=qb)
+    torch.cuda.synchronize()
+    ref = O.sparse_attention(np64(q), np64(k), np64(v), window, sink, scale, q_block=qb)
+    assert_close(np64(out), ref, what=f"sparse B{B} H{H}/{Hkv} S{S} D{D} w{window} sink{sink} qb{qb}")
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,window,sink", [
+    (1, 8, 2, 1024, 64, 256, 64),      # CPU-config geometry, shortened
+    (1, 8, 2, 2048, 128, 512, 128),    # Llama geometry (GQA 4)
+    (2, 4, 1, 700, 128, 128, 20),      # batch 2, S and sink not multiples of 64
+    (1, 10, 2, 512, 128, 200, 7),      # Qwen3 GQA ratio 5
+    (1, 2, 2, 300, 64, 96, 0),         # MHA, no sink
+    (1, 4, 4, 256, 128, 40, 3),        # window < q_block: rows with few keys
+    (1, 4, 2, 384, 128, 4096, 0),      # window covers everything: causal
+    (1, 4, 2, 384, 64, 8, 1000),       # sinks cover everything: causal
+])
+def test_sparse_attention_parity(gpu, B, H, Hkv, S, D, window, sink):
+    _sparse_case(B, H, Hkv, S, D, window, sink)
+
+
+def test_sparse_attention_fp16_and_q_block(gpu):
+    _sparse_case(1, 8, 2, 640, 128, 160, 16, qb=32, dtype=torch.float16)
+    _sparse_case(1, 4, 1, 256, 64, 64, 8, qb=1)
+
+
+def test_sparse_attention_model_layout(gpu):
+    # q/k/v as transposed views of [B,S,H,D] storage (no copies on the way in)
+    _sparse_case(1, 8, 2, 1024, 128, 256, 64, model_layout=True, seed=3)
+
+
+def _qsa(q, k, v, mask, scale):
+    from delta_attention.delta_kernel import attention
+    out = attention(q, k, v, mask, scale)
+    torch.cuda.synchronize()
+    return out
+
+
+def test_qsparse_t1(gpu):
+    # tests/test_math_identities.py:61-89: 37 sorted rows incl. both ends
+    b, h, s, d = 1, 32, 4096, 128
+    q, k, v = gen_qkv(b, h, h, s, d, seed=0)
+    mid = torch.randperm(s - 2, generator=torch.Generator().manual_seed(1))[:35] + 1
+    idx = torch.cat([torch.tensor([0, s - 1]), mid]).unique().sort().values
+    out = _qsa(q[:, :, idx.cuda()], k, v, idx.cuda().unsqueeze(0), d ** -0.5)
+    ref = O.qsparse_attention(np64(q)[:, :, idx.numpy()], np64(k), np64(v), idx.numpy(), d ** -0.5)
+    assert_close(np64(out), ref, what="T1")
+
+
+@pytest.mark.parametrize("kind", ["rectangle", "irregular", "causal"])
+def test_qsparse_reference_kernel_tests(gpu, kind):
+    # delta_kernel.py:332-469: Z=1, H=2, N_CTX=1024, D=64, std 0.5, seed 20, atol 1e-2
+    n = 1024
+    N = {"rectangle": 2 * n, "irregular": 4 * n, "causal": n}[kind]
+    q, k, v = gen_qkv(1, 2, 2, n, 64, seed=20, std=0.5, N=N)
+    g = torch.Generator().manual_seed(20)
+    mask = {"rectangle": torch.randint(0, N, (1, n), generator=g),
+            "irregular": torch.randperm(n, generator=g).unsqueeze(0),
+            "causal": torch.arange(n).unsqueeze(0)}[kind]
+    out = _qsa(q, k, v, mask.cuda(), 64 ** -0.5)
+    ref = O.qsparse_attention(np64(q), np64(k), np64(v), mask[0].numpy(), 64 ** -0.5)
+    assert_close(np64(out), ref, atol=1e-2, what=f"qsa {kind}")
+
+
+def test_qsparse_gqa_native_equals_expanded(gpu):
+    from delta_attention.llama import repeat_kv
+    q, k, v = gen_qkv(2, 8, 2, 1500, 128, seed=4)
+    rows = torch.tensor([0, 1, 63, 64, 500, 1000, 1499], device="cuda")
+    a = _qsa(q[:, :, rows], k, v, rows.unsqueeze(0), 0.1)
+    b = _qsa(q[:, :, rows], repeat_kv(k, 4), repeat_kv(v, 4), rows.unsqueeze(0), 0.1)
+    assert torch.equal(a, b)
+    ref = O.qsparse_attention(np64(q)[:, :, rows.cpu().numpy()], np64(k), np64(v), rows.cpu().numpy(), 0.1)
+    assert_close(np64(a), ref, what="qsa GQA")
+
+
+def test_qsparse_edge_limits(gpu):
+    from delta_attention import ops
+    q, k, v = gen_qkv(2, 4, 2, 64, 128, seed=5, N=300)
+    # per-batch limits, a negative limit (empty row -> zeros) and one beyond the keys (clamped)
+    lim = torch.tensor([[5, -1, 299, 1000] * 16, [0, 63, 128, 7] * 16], device="cuda")
+    out = ops.qsparse_attention(q, k, v, lim, 0.2)
+    torch.cuda.synchronize()
+    for b in range(2):
+        l = np.minimum(lim[b].cpu().numpy(), 299)
+        ref = O.qsparse_attention(np64(q)[b:b + 1], np64(k)[b:b + 1], np64(v)[b:b + 1], l, 0.2)
+        assert_close(np64(out)[b:b + 1], ref, what=f"edge b{b}")
+    assert torch.count_nonzero(out[0, :, 1::4]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_delta_add_bit_exact(gpu, dtype):
+    from delta_attention import ops
+    B, S, H, D, g = 2, 1280, 8, 128, 64
+    gen = torch.Generator().manual_seed(6)
+    sparse = torch.randn(B, S, H, D, generator=gen).to(dtype)
+    _, _, s_p, _ = O.anchor_layout(S, g)
+    n = s_p // g
+    dense = torch.randn(B, n, H, D, generator=gen).to(dtype)
+    anchors = torch.arange(0, s_p, g)
+    # delta precomputed the way kernel (2) writes it, then the in-place uniform add
+    delta = (dense - sparse[:, anchors])
+    out = sparse.clone().cuda()
+    ops.delta_add(out, s_p=s_p, out=out, delta=delta.cuda(), gamma=g)
+    torch.cuda.synchronize()
+    if dtype == torch.bfloat16:
+        ref = O.compose_uniform(np64(sparse).astype(np.float32),
+                                np.concatenate([np64(dense), np64(sparse)[:, s_p:]], 1).astype(np.float32),
+                                S, g, bf16=True)
+        np.testing.assert_array_equal(out.float().cpu().numpy(), ref)
+    ref_t = sparse.clone()
+    ref_t[:, :s_p] = (sparse[:, :s_p].reshape(B, n, g, H, D) + delta.reshape(B, n, 1, H, D)).reshape(B, s_p, H, D)
+    assert torch.equal(out.cpu(), ref_t)
+
+
+def test_apply_delta_variable_bit_exact(gpu):
+    from delta_attention.stride import apply_delta_variable
+    B, S, H, D = 1, 2000, 4, 64
+    gen = torch.Generator().manual_seed(7)
+    sparse = torch.randn(B, S, H, D, generator=gen).to(torch.bfloat16)
+    idx = torch.tensor([5, 17, 18, 100, 640, 641, 1500])       # variable stride, first row != 0
+    dense = torch.randn(B, len(idx), H, D, generator=gen).to(torch.bfloat16)
+    s_p = 1900
+    got = apply_delta_variable(sparse.cuda(), dense.cuda(), idx.cuda(), s_p)
+    torch.cuda.synchronize()
+    ref = O.apply_delta_variable(np64(sparse).astype(np.float32), np64(dense).astype(np.float32),
+                                 idx.numpy(), s_p, bf16=True)
+    np.testing.assert_array_equal(got.float().cpu().numpy(), ref)
+    # the reference's own torch ops on the same bf16 tensors (stride.py:38-40)
+    deltas = dense - sparse[:, idx]
+    owner = torch.searchsorted(idx, torch.arange(s_p), right=True) - 1
+    assert torch.equal(got.cpu(), sparse[:, :s_p] + deltas[:, owner])

@@ -1,0 +1,167 @@
+"""GPU parity of the composed layer prefill (kernels 1 -> 2 -> 3) and of the
+attention modules, against the oracle's delta_forward (llama.py:659-757) on
+identical seeded inputs, plus the reference's identities T2-T4 on the GPU path.
+"""
+
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, gen_qkv, np64
+from oracle import delta_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(B, H, Hkv, S, D, gamma, window, sink, mode="delta", seed=0, dtype=torch.bfloat16):
+    from delta_attention import ops
+    q, k, v = gen_qkv(B, H, Hkv, S, D, seed=seed, dtype=dtype)
+    scale = D ** -0.5
+    out = ops.delta_prefill(q, k, v, gamma=gamma, window=window, sink=sink, sm_scale=scale, mode=mode)
+    torch.cuda.synchronize()
+    qn, kn, vn = np64(q), np64(k), np64(v)
+    ref = O.delta_forward(qn, kn, vn, gamma, window, sink, scale, mode=mode)
+    return np64(out), ref, (qn, kn, vn)
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,gamma,window,sink", [
+    (1, 8, 2, 4096, 64, 16, 512, 64),     # the CPU configuration's shape (bf16 on the GPU path)
+    (1, 8, 2, 2048, 128, 64, 512, 128),   # Llama geometry, shortened
+    (2, 10, 2, 1024, 128, 64, 256, 64),   # Qwen3 geometry (GQA 5, batch 2), shortened
+    (1, 4, 4, 1200, 128, 32, 128, 8),     # s % gamma != 0
+    (1, 4, 1, 768, 64, 128, 192, 0),      # gamma 128
+])
+def test_delta_prefill_parity(gpu, B, H, Hkv, S, D, gamma, window, sink):
+    got, ref, _ = _layer(B, H, Hkv, S, D, gamma, window, sink)
+    assert_close(got, ref, what=f"delta B{B} H{H}/{Hkv} S{S} D{D} g{gamma} w{window} sink{sink}")
+
+
+@pytest.mark.parametrize("mode", ["sparse-only", "recompute"])
+def test_delta_prefill_modes(gpu, mode):
+    got, ref, _ = _layer(1, 8, 2, 1024, 128, 32, 256, 16, mode=mode)
+    assert_close(got, ref, what=mode)
+
+
+def test_short_sequence_is_all_dense(gpu):
+    # s <= cut_n: the reference crashes (negative s_p); here every row is dense
+    from delta_attention import ops
+    q, k, v = gen_qkv(1, 4, 2, 100, 128, seed=0)
+    out = ops.delta_prefill(q, k, v, gamma=64, window=32, sink=4, sm_scale=128 ** -0.5)
+    torch.cuda.synchronize()
+    dense = O.causal_attention_rows(np64(q), np64(k), np64(v), np.arange(100), 128 ** -0.5)
+    assert_close(np64(out), dense, what="short")
+
+
+def test_t2_anchor_exactness_and_index_set(gpu):
+    s, gamma = 2048, 64
+    got, ref, (q, k, v) = _layer(1, 8, 2, s, 128, gamma, 256, 16, seed=1)
+    anchors, tail, s_p, _ = O.anchor_layout(s, gamma)
+    rows = np.concatenate([anchors, tail])
+    dense = O.causal_attention_rows(q, k, v, rows, 128 ** -0.5)
+    assert_close(got[:, rows], dense, what="T2 anchors+tail")
+    # the rows the GPU path computed densely are exactly the oracle's index set
+    from delta_attention import ops
+    np.testing.assert_array_equal(ops.selected_rows(s, gamma, "cuda").cpu().numpy(), rows)
+
+
+def test_t3_gamma1_is_dense(gpu):
+    s = 1024
+    got, _, (q, k, v) = _layer(1, 4, 2, s, 128, 1, 128, 4, seed=2)
+    dense = O.causal_attention_rows(q, k, v, np.arange(s), 128 ** -0.5)
+    assert_close(got, dense, what="T3")
+
+
+def test_t4_full_window_is_dense(gpu):
+    s = 1024
+    got, _, (q, k, v) = _layer(1, 4, 2, s, 128, 64, s, 0, seed=3)
+    dense = O.causal_attention_rows(q, k, v, np.arange(s), 128 ** -0.5)
+    assert_close(got, dense, what="T4")
+
+
+def _cfg(H, Hkv, D, **kw):
+    base = dict(hidden_size=H * D, num_attention_heads=H, num_key_value_heads=Hkv, head_dim=D,
+                attention_bias=False, attention_dropout=0.0, rms_norm_eps=1e-6,
+                _attn_implementation="window", mode="delta", delta_lambda=64,
+                sliding_window=256, sink_tokens=16, stride_policy="fixed", log_drift=False,
+                adapt_chunk=512, adapt_threshold=0.95, gamma_min=16, gamma_max=256,
+                stride_trigger="absolute", adapt_k=2.0)
+    base.update(kw)
+    return types.SimpleNamespace(**base)
+
+
+def test_module_delta_forward_matches_ops(gpu):
+    from delta_attention import ops
+    from delta_attention.llama import LlamaAttention
+    from delta_attention.validation import anchor_exactness_check
+    cfg = _cfg(8, 2, 128, log_drift=True)
+    m = LlamaAttention(cfg, layer_idx=0).cuda().to(torch.bfloat16)
+    q, k, v = gen_qkv(1, 8, 2, 1536, 128, seed=4, model_layout=True)
+    out, w = m.delta_forward(m, q, k, v, None, scaling=m.scaling)
+    assert w is None
+    ref = ops.delta_prefill(q, k, v, gamma=64, window=256, sink=16, sm_scale=m.scaling)
+    assert torch.equal(out, ref)
+    assert m._drift_stats["n"] == (ops.anchor_layout(1536, 64)[2] - 1) * 8
+    # fp32 inputs run in bf16 and come back as fp32 (llama.py:382-388, 493-494)
+    out32, _ = m.delta_forward(m, q.float(), k.float(), v.float(), None, scaling=m.scaling)
+    assert out32.dtype == torch.float32 and torch.equal(out32.to(torch.bfloat16), out)
+    assert anchor_exactness_check(m, gamma=64, window=256, s=2048) > 0.999
+
+
+def test_module_forward_and_qwen3(gpu):
+    from delta_attention.llama import LlamaAttention, rope_cos_sin
+    from delta_attention.qwen3 import Qwen3DeltaAttention
+    torch.manual_seed(0)
+    for cls, H, Hkv in ((LlamaAttention, 8, 2), (Qwen3DeltaAttention, 10, 2)):
+        cfg = _cfg(H, Hkv, 128)
+        m = cls(cfg, layer_idx=1).cuda().to(torch.bfloat16)
+        for p in m.parameters():
+            torch.nn.init.normal_(p, std=0.02)
+        x = torch.randn(1, 1024, H * 128, device="cuda", dtype=torch.bfloat16)
+        pos = torch.arange(1024, device="cuda")[None]
+        cos, sin = rope_cos_sin(pos, 128, 500000.0, torch.bfloat16)
+        y, _ = m(x, (cos, sin))
+        torch.cuda.synchronize()
+        # oracle: the same prologue in numpy, then delta_forward
+        hs = (1, 1024, -1, 128)
+        qp = np64(m.q_proj(x).view(hs).transpose(1, 2))
+        kp = np64(m.k_proj(x).view(hs).transpose(1, 2))
+        vp = np64(m.v_proj(x).view(hs).transpose(1, 2))
+        if cls is Qwen3DeltaAttention:   # per-head q/k RMSNorm with the (random) norm weights
+            qp = O.rms_norm(qp, 1e-6, np64(m.q_norm.weight)).astype(np.float64)
+            kp = O.rms_norm(kp, 1e-6, np64(m.k_norm.weight)).astype(np.float64)
+        c, s_ = O.rope_cos_sin(1024, 128, 500000.0)
+        qr, kr = O.apply_rope(qp, c, s_), O.apply_rope(kp, c, s_)
+        # the module rounds the post-RoPE q/k to bf16 before the kernels
+        qr, kr = O.round_bf16(qr).astype(np.float64), O.round_bf16(kr).astype(np.float64)
+        vr = O.round_bf16(vp).astype(np.float64)
+        att = O.delta_forward(qr, kr, vr, 64, 256, 16, 128 ** -0.5)
+        y_ref = att.reshape(1, 1024, -1) @ np64(m.o_proj.weight).T
+        assert_close(np64(y)[0], y_ref[0], cos_min=0.99, atol=5e-2, what=f"{cls.__name__} forward")
+
+
+def test_adaptive_stride_path(gpu):
+    from delta_attention.llama import LlamaAttention
+    cfg = _cfg(4, 2, 128, stride_policy="adaptive", adapt_chunk=512, delta_lambda=64,
+               adapt_threshold=0.5, gamma_min=16, gamma_max=128)
+    m = LlamaAttention(cfg, layer_idx=0).cuda().to(torch.bfloat16)
+    s = 2048
+    q, k, v = gen_qkv(1, 4, 2, s, 128, seed=8)
+    out, _ = m.delta_forward(m, q, k, v, None, scaling=m.scaling)
+    torch.cuda.synchronize()
+    st = m._stride_stats
+    idx = []
+    for c in st["chunks"]:
+        end = min(c["start"] + 512, s - 128 - s % 64)
+        idx += list(range(c["start"], end, c["gamma"]))
+    idx = np.array(idx)
+    assert len(idx) == st["n_anchors"]
+    qn, kn, vn = np64(q), np64(k), np64(v)
+    scale = 128 ** -0.5
+    sparse = O.sparse_attention(qn, kn, vn, 256, 16, scale)
+    s_p = s - (s % 64 + 128)
+    dense_sel = O.causal_attention_rows(qn, kn, vn, idx, scale)
+    tail = O.causal_attention_rows(qn, kn, vn, np.arange(s_p, s), scale)
+    ref = np.concatenate([O.apply_delta_variable(sparse, dense_sel, idx, s_p), tail], 1)
+    assert_close(np64(out), ref, what="adaptive")

@@ -1,0 +1,111 @@
+"""Host-side logic of the delta path on the CPU: the exact sampled-row index
+set, knobs, the stride rules / cost model, drift aggregation, and that the
+product ops refuse to run anywhere but on the GPU library."""
+
+import dataclasses
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import conftest  # noqa: F401
+from oracle import delta_oracle as O
+from delta_attention import config as C
+from delta_attention import drift, ops, stride
+from delta_attention.delta_kernel import attention
+from delta_attention.validation import anchor_indices
+
+
+@pytest.mark.parametrize("s,gamma", [(4096, 16), (32768, 64), (131072, 16), (131072, 32),
+                                     (131072, 64), (131072, 128), (65536, 64), (8192, 1),
+                                     (4100, 64), (200, 64), (100, 64)])
+def test_index_set_exact(s, gamma):
+    ref = O.selected_rows(s, gamma)
+    got = ops.selected_rows(s, gamma, "cpu").numpy()
+    np.testing.assert_array_equal(got, ref)
+    cut_n, s_p, n_anchor = ops.anchor_layout(s, gamma)
+    a, t, s_p_o, cut_o = O.anchor_layout(s, gamma)
+    assert (cut_n, s_p) == (cut_o, s_p_o) and n_anchor == len(a)
+    va, vt = anchor_indices(s, gamma)
+    np.testing.assert_array_equal(np.concatenate([va.numpy(), vt.numpy()]), ref)
+
+
+def test_config_knobs():
+    cfg = C.Config()
+    assert cfg.delta_lambda == 64 and cfg.sliding_window == 2048 and cfg.sink_tokens == 1024
+    names = {f.name for f in dataclasses.fields(C.Config)}
+    assert set(C.PIPELINE_FIELDS) <= names and "sink_tokens" in C.PIPELINE_FIELDS
+    cfg2 = C.Config.from_args(["--delta_lambda", "16", "--sink_tokens", "128", "--log_drift",
+                               "--mode", "recompute"])
+    assert (cfg2.delta_lambda, cfg2.sink_tokens, cfg2.log_drift, cfg2.mode) == (16, 128, True, "recompute")
+
+    class M:
+        pass
+    m = M()
+    C.copy_pipeline_fields(cfg2, m)
+    assert all(getattr(m, f) == getattr(cfg2, f) for f in C.PIPELINE_FIELDS)
+
+
+def test_sparse_pass_cost_closed_form():
+    for s, w, sk in [(4096, 2048, 1024), (1000, 2048, 1024), (131072, 2048, 128), (10, 3, 2)]:
+        brute = sum(min(i + 1, w + sk) for i in range(s))
+        assert stride._sparse_pass_cost(s, w, sk) == brute
+
+
+def test_effective_sparsity_uniform_matches_tensor_form():
+    for s, g in [(32768, 64), (8192, 16), (131072, 128)]:
+        idx = torch.from_numpy(O.selected_rows(s, g))
+        assert stride.uniform_effective_sparsity(s, g, 2048, 1024) == pytest.approx(
+            stride.effective_sparsity(idx, s, 2048, 1024), rel=1e-12)
+
+
+def test_next_gamma_rules():
+    kw = dict(threshold=0.9, gamma_min=16, gamma_max=256)
+    assert stride.next_gamma(0.5, 64, **kw) == 32
+    assert stride.next_gamma(0.5, 16, **kw) == 16
+    assert stride.next_gamma(0.91, 64, **kw) == 64           # inside the hysteresis band
+    assert stride.next_gamma(0.93, 64, **kw) == 128
+    assert stride.next_gamma(0.99, 256, **kw) == 256
+    kr = dict(k=1.0, gamma_min=16, gamma_max=256)
+    assert stride.next_gamma_relative(0.1, [0.5], 64, **kr) == 64   # needs >= 2 entries
+    hist = [0.5, 0.7]                                                # mean .6, std .1
+    assert stride.next_gamma_relative(0.45, hist, 64, **kr) == 32
+    assert stride.next_gamma_relative(0.75, hist, 64, **kr) == 128
+    assert stride.next_gamma_relative(0.6, hist, 64, **kr) == 64
+    assert stride.plan_chunks(10000, 4096) == [(0, 4096), (4096, 8192), (8192, 10000)]
+
+
+def test_interanchor_cos_cpu():
+    d = torch.zeros(1, 3, 2, 4)
+    d[0, :, :, 0] = 1.0
+    d[0, 2, 1] = torch.tensor([0.0, 1.0, 0.0, 0.0])
+    mean, mn = stride.interanchor_cos(d)
+    assert mn == pytest.approx(0.0) and mean == pytest.approx(0.75)
+    assert stride.interanchor_cos(d[:, :1]) == (1.0, 1.0)
+
+
+def test_drift_summary_and_aggregate():
+    torch.manual_seed(0)
+    s = drift.drift_summary(torch.randn(1, 9, 4, 16), layer_idx=3, gamma=64, seq_len=640)
+    assert s["n"] == 8 * 4 and sum(s["hist"]) == s["n"] and s["layer"] == 3
+    json.dumps(s)
+    agg = drift.aggregate_drift([s, dict(s, mean=1.0)])
+    assert agg[3]["n"] == 64 and agg[3]["requests"] == 2
+    assert agg[3]["mean"] == pytest.approx((s["mean"] + 1.0) / 2)
+    with pytest.raises(ValueError):
+        drift.aggregate_drift([dict(s, hist_bins=10)])
+    assert len(drift.hist_bin_edges()) == drift.HIST_BINS + 1
+
+
+def test_product_ops_refuse_cpu_tensors():
+    q = torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        ops.sparse_attention(q, q, q, window=32, sink=0, sm_scale=0.1)
+    with pytest.raises(AssertionError):
+        attention(q, q, q, torch.arange(64)[None], 0.1)
+    with pytest.raises(AssertionError):           # head_dim 96 has no kernel
+        attention(torch.zeros(1, 2, 8, 96), torch.zeros(1, 2, 8, 96), torch.zeros(1, 2, 8, 96),
+                  torch.arange(8)[None], 0.1)
+    with pytest.raises(AssertionError):           # mask must be 2-D
+        attention(q, q, q, torch.arange(64), 0.1)

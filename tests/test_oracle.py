@@ -1,0 +1,324 @@
+"""Pins the CPU oracle (oracle/delta_oracle.py) before it is trusted as the
+parity reference: brute force on tiny inputs, library routines (torch SDPA in
+float64) on the special cases that reduce to them, closed forms and the
+reference's own known-answer identities (T1-T4 of
+tests/test_math_identities.py, the delta_kernel.py in-file tests).
+
+The reference ships no numeric fixtures; the integer constants below are the
+sizes of the reference's benchmark configurations derived by hand from the
+formulas in validation.py:224-232 and flex_delta.py:59-61.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import delta_oracle as O
+
+
+def _sdpa64(q, k, v, scale, mask=None, causal=False):
+    """Library reference: torch SDPA in float64 on [B,H,n,d] numpy inputs."""
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).double()
+    H = q.shape[1]
+    kk = np.repeat(k, H // k.shape[1], axis=1)
+    vv = np.repeat(v, H // v.shape[1], axis=1)
+    m = None if mask is None else torch.from_numpy(mask)
+    return F.scaled_dot_product_attention(t(q), t(kk), t(vv), attn_mask=m, is_causal=causal,
+                                          scale=scale).numpy()
+
+
+def _qkv(B, H, Hkv, S, d, seed=0, N=None):
+    rng = np.random.default_rng(seed)
+    N = S if N is None else N
+    return (rng.standard_normal((B, H, S, d)), rng.standard_normal((B, Hkv, N, d)),
+            rng.standard_normal((B, Hkv, N, d)))
+
+
+# ---------------------------------------------------------------------------
+# index layout
+
+@pytest.mark.parametrize("s,gamma,n_anchor,n_sel", [
+    (4096, 16, 248, 376),        # CPU config: s 4096, gamma 16
+    (32768, 64, 510, 638),       # Llama 32K, gamma 64
+    (131072, 16, 8184, 8312),    # Llama 128K gamma sweep
+    (131072, 32, 4092, 4220),
+    (131072, 64, 2046, 2174),
+    (131072, 128, 1023, 1151),
+    (65536, 64, 1022, 1150),     # Qwen3 64K
+    (8192, 64, 126, 254),        # T2 / T13 size
+    (8192, 1, 8064, 8192),       # T3: gamma 1 selects every row
+    (4100, 64, 62, 194),         # s % gamma != 0: cut_n = 4 + 128
+    (4160, 256, 15, 15 + 320),   # gamma > 128: cut_n = 64 + 256
+])
+def test_anchor_layout_sizes(s, gamma, n_anchor, n_sel):
+    anchors, tail, s_p, cut_n = O.anchor_layout(s, gamma)
+    assert len(anchors) == n_anchor and len(anchors) + len(tail) == n_sel
+    assert cut_n == s % gamma + max(128, gamma) and s_p == s - cut_n
+    assert anchors[0] == 0 and np.all(np.diff(anchors) == gamma) and anchors[-1] < s_p
+    assert np.array_equal(tail, np.arange(s_p, s))
+
+
+def test_anchor_layout_reshape_condition():
+    # the reference's reshape (llama.py:748-749) needs gamma | s_p: true for gamma | 128
+    for gamma in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512):
+        for s in (4096, 5000, 131072, 131071):
+            anchors, _, s_p, _ = O.anchor_layout(s, gamma)
+            if s_p > 0:
+                assert s_p % gamma == 0 and len(anchors) * gamma == s_p
+
+
+# ---------------------------------------------------------------------------
+# key-sparse visibility
+
+@pytest.mark.parametrize("s,window,sink,qb", [
+    (200, 64, 10, 64), (300, 100, 0, 64), (257, 31, 5, 64), (130, 500, 3, 64),
+    (190, 48, 200, 64), (128, 16, 4, 1), (96, 0, 7, 32), (333, 70, 64, 16),
+])
+def test_visible_pairs_brute_force(s, window, sink, qb):
+    r = np.arange(s)[:, None]
+    k = np.arange(s)[None, :]
+    # the predicate as flex_delta.py:59-61 writes it
+    block_last = (r // qb) * qb + (qb - 1)
+    brute = (r >= k) & ((k < sink) | (k + window > block_last))
+    assert np.array_equal(brute.sum(1), O.sparse_row_counts(s, window, sink, qb))
+    assert np.array_equal(brute, O.sparse_visible(r, k, window, sink, qb))
+
+
+@pytest.mark.parametrize("s,window,sink,pairs", [
+    (4096, 512, 64, 2082816),
+    (32768, 2048, 128, 67973120),
+    (131072, 2048, 128, 278786048),
+    (65536, 4096, 64, 262045696),
+])
+def test_visible_pairs_config_totals(s, window, sink, pairs):
+    assert O.visible_pairs(s, window, sink) == pairs
+
+
+def test_visible_pairs_closed_forms():
+    # window >= s: full causal, s(s+1)/2
+    assert O.visible_pairs(1000, 5000, 0) == 1000 * 1001 // 2
+    # q_block 1, no sink: a plain band of `window` keys per row
+    s, w = 777, 40
+    assert O.visible_pairs(s, w, 0, q_block=1) == sum(min(i + 1, w) for i in range(s))
+
+
+def test_qsparse_pairs_closed_form():
+    # sum over anchors 0, g, ..., (n-1)g of (i+1) plus the tail
+    for s, g in [(131072, 64), (32768, 64), (4096, 16)]:
+        a, t, s_p, _ = O.anchor_layout(s, g)
+        n = len(a)
+        closed = g * n * (n - 1) // 2 + n + (s * (s + 1) - s_p * (s_p + 1)) // 2
+        assert O.qsparse_pairs(np.concatenate([a, t])) == closed
+
+
+# ---------------------------------------------------------------------------
+# attention
+
+def _brute_sparse(q, k, v, window, sink, scale, qb):
+    """Per-element loops with math.exp on tiny inputs."""
+    B, H, S, d = q.shape
+    G = H // k.shape[1]
+    out = np.zeros((B, S, H, d))
+    for b in range(B):
+        for h in range(H):
+            for r in range(S):
+                last = (r // qb) * qb + qb - 1
+                keys = [j for j in range(S) if j <= r and (j < sink or j + window > last)]
+                if not keys:
+                    continue
+                sc = [scale * float(np.dot(q[b, h, r], k[b, h // G, j])) for j in keys]
+                m = max(sc)
+                w = [math.exp(x - m) for x in sc]
+                tot = sum(w)
+                for wi, j in zip(w, keys):
+                    out[b, r, h] += wi / tot * v[b, h // G, j]
+    return out
+
+
+@pytest.mark.parametrize("S,window,sink,qb", [(130, 40, 3, 64), (70, 20, 0, 16), (96, 64, 70, 32)])
+def test_sparse_attention_brute_force(S, window, sink, qb):
+    q, k, v = _qkv(1, 2, 1, S, 8, seed=S)
+    got = O.sparse_attention(q, k, v, window, sink, 0.3, q_block=qb)
+    ref = _brute_sparse(q, k, v, window, sink, 0.3, qb)
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_sparse_full_window_is_causal_sdpa():
+    q, k, v = _qkv(2, 4, 2, 200, 16, seed=1)
+    got = O.sparse_attention(q, k, v, window=400, sink=0, scale=0.25)
+    ref = _sdpa64(q, k, v, 0.25, causal=True).transpose(0, 2, 1, 3)
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_sparse_all_sinks_is_causal_sdpa():
+    q, k, v = _qkv(1, 2, 2, 150, 16, seed=2)
+    got = O.sparse_attention(q, k, v, window=8, sink=150, scale=0.2)
+    ref = _sdpa64(q, k, v, 0.2, causal=True).transpose(0, 2, 1, 3)
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_sparse_qblock1_is_sliding_window_sdpa():
+    S, w = 160, 24
+    q, k, v = _qkv(1, 2, 1, S, 8, seed=3)
+    band = np.tril(np.ones((S, S), bool)) & np.triu(np.ones((S, S), bool), -(w - 1))
+    got = O.sparse_attention(q, k, v, window=w, sink=0, scale=0.5, q_block=1)
+    ref = _sdpa64(q, k, v, 0.5, mask=band).transpose(0, 2, 1, 3)
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_sparse_gqa_equals_expanded():
+    q, k, v = _qkv(1, 6, 2, 140, 8, seed=4)
+    a = O.sparse_attention(q, k, v, 32, 4, 0.3)
+    b = O.sparse_attention(q, np.repeat(k, 3, 1), np.repeat(v, 3, 1), 32, 4, 0.3)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_sparse_rows_subset_matches_full():
+    q, k, v = _qkv(1, 2, 1, 300, 8, seed=5)
+    full = O.sparse_attention(q, k, v, 100, 8, 0.3)
+    rows = np.array([0, 5, 63, 64, 200, 299])
+    np.testing.assert_allclose(O.sparse_attention(q, k, v, 100, 8, 0.3, rows=rows), full[:, rows],
+                               rtol=1e-12, atol=1e-14)
+
+
+def test_qsparse_causal_rows_is_sdpa():
+    # delta_kernel.py:426-469 (mask = arange) and T1 (sorted subset of rows)
+    S = 300
+    q, k, v = _qkv(1, 4, 4, S, 16, seed=6)
+    got = O.qsparse_attention(q, k, v, np.arange(S), 0.25)
+    np.testing.assert_allclose(got, _sdpa64(q, k, v, 0.25, causal=True), rtol=1e-10, atol=1e-12)
+    idx = np.array([0, 3, 77, 128, 129, 250, 299])
+    m = np.arange(S)[None, :] <= idx[:, None]
+    ref = _sdpa64(q[:, :, idx], k, v, 0.25, mask=m)
+    np.testing.assert_allclose(O.qsparse_attention(q[:, :, idx], k, v, idx, 0.25), ref,
+                               rtol=1e-10, atol=1e-12)
+
+
+def test_qsparse_rectangular_and_unsorted():
+    # delta_kernel.py:332-377 (N_KV = 2N, random limits) and :380-423 (randperm)
+    n, N = 96, 192
+    q, k, v = _qkv(1, 2, 2, n, 16, seed=7, N=N)
+    rng = np.random.default_rng(8)
+    for mask in (rng.integers(0, N, n), rng.permutation(n)):
+        m = np.arange(N)[None, :] <= mask[:, None]
+        np.testing.assert_allclose(O.qsparse_attention(q, k, v, mask, 0.3),
+                                   _sdpa64(q, k, v, 0.3, mask=m), rtol=1e-10, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# composition: T2 / T3 / T4 and the modes
+
+def _dense(q, k, v, scale):
+    return _sdpa64(q, k, v, scale, causal=True).transpose(0, 2, 1, 3)
+
+
+def test_t2_anchor_and_tail_rows_are_dense():
+    s, g = 512, 32
+    q, k, v = _qkv(1, 4, 2, s, 16, seed=9)
+    out = O.delta_forward(q, k, v, g, window=64, sink=4, scale=0.25)
+    dense = _dense(q, k, v, 0.25)
+    anchors, tail, s_p, _ = O.anchor_layout(s, g)
+    np.testing.assert_allclose(out[:, anchors], dense[:, anchors], rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(out[:, tail], dense[:, tail], rtol=1e-9, atol=1e-12)
+    # and the other rows really are corrected sparse rows, not dense
+    assert np.abs(out[:, 1:s_p] - dense[:, 1:s_p]).max() > 1e-3
+
+
+def test_t3_gamma1_is_dense_everywhere():
+    s = 320
+    q, k, v = _qkv(1, 2, 1, s, 16, seed=10)
+    out = O.delta_forward(q, k, v, 1, window=32, sink=0, scale=0.25)
+    np.testing.assert_allclose(out, _dense(q, k, v, 0.25), rtol=1e-9, atol=1e-12)
+
+
+def test_t4_full_window_zero_delta():
+    s = 384
+    q, k, v = _qkv(1, 2, 2, s, 16, seed=11)
+    sparse = O.sparse_attention(q, k, v, window=s, sink=0, scale=0.3)
+    np.testing.assert_allclose(O.delta_forward(q, k, v, 64, s, 0, 0.3, sparse=sparse),
+                               _dense(q, k, v, 0.3), rtol=1e-9, atol=1e-12)
+
+
+def test_modes_sparse_only_and_recompute():
+    s, g = 400, 16
+    q, k, v = _qkv(1, 2, 1, s, 8, seed=12)
+    sparse = O.sparse_attention(q, k, v, 48, 4, 0.3)
+    np.testing.assert_array_equal(O.delta_forward(q, k, v, g, 48, 4, 0.3, mode="sparse-only"), sparse)
+    rec = O.delta_forward(q, k, v, g, 48, 4, 0.3, mode="recompute")
+    dense = _dense(q, k, v, 0.3)
+    idx = O.selected_rows(s, g)
+    other = np.setdiff1d(np.arange(s), idx)
+    np.testing.assert_allclose(rec[:, idx], dense[:, idx], rtol=1e-9, atol=1e-12)
+    np.testing.assert_array_equal(rec[:, other], sparse[:, other])
+
+
+def test_apply_delta_variable_uniform_is_reshape_bitwise():
+    # stride.py:33-34: uniform anchors give the reshape path bit-for-bit (bf16 ops)
+    s, g = 1024, 64
+    rng = np.random.default_rng(13)
+    sparse = O.round_bf16(rng.standard_normal((2, s, 3, 16)).astype(np.float32))
+    a, t, s_p, _ = O.anchor_layout(s, g)
+    dense = O.round_bf16(rng.standard_normal((2, len(a) + len(t), 3, 16)).astype(np.float32))
+    via_reshape = O.compose_uniform(sparse, dense, s, g, bf16=True)[:, :s_p]
+    via_owner = O.apply_delta_variable(sparse, dense[:, :len(a)], a, s_p, bf16=True)
+    np.testing.assert_array_equal(via_reshape, via_owner)
+    # the zero-delta identity: dense == sparse at anchors -> output == sparse
+    zero = O.apply_delta_variable(sparse, sparse[:, a], a, s_p, bf16=True)
+    np.testing.assert_array_equal(zero, sparse[:, :s_p])
+
+
+def test_apply_delta_variable_owner():
+    idx = np.array([3, 10, 11, 40])
+    sp = np.zeros((1, 50, 1, 1))
+    dense = np.array([1.0, 2.0, 3.0, 4.0]).reshape(1, 4, 1, 1)
+    out = O.apply_delta_variable(sp, dense, idx, 50)[0, :, 0, 0]
+    # rows 0-2 precede the first anchor: searchsorted-1 == -1 -> the last anchor
+    expect = [4] * 3 + [1] * 7 + [2] + [3] * 29 + [4] * 10
+    np.testing.assert_array_equal(out, expect)
+
+
+# ---------------------------------------------------------------------------
+# bf16 arithmetic and the input prologue
+
+def test_round_bf16_matches_torch():
+    rng = np.random.default_rng(14)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0 ** rng.integers(-8, 8, 100000),
+                        np.array([0.0, -0.0, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 65504.0], np.float32)])
+    x = x.astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O.round_bf16(x), ref)
+    a, b = O.round_bf16(x[:5000]), O.round_bf16(x[5000:10000])
+    ta, tb = torch.from_numpy(a).to(torch.bfloat16), torch.from_numpy(b).to(torch.bfloat16)
+    np.testing.assert_array_equal(O.sub_bf16(a, b), (ta - tb).float().numpy())
+    np.testing.assert_array_equal(O.add_bf16(a, b), (ta + tb).float().numpy())
+
+
+def test_rope_invariants():
+    s, d = 64, 16
+    cos, sin = O.rope_cos_sin(s, d, 10000.0)
+    rng = np.random.default_rng(15)
+    x = rng.standard_normal((1, 1, s, d)).astype(np.float32)
+    y = O.apply_rope(x, cos, sin)
+    np.testing.assert_allclose(y[:, :, 0], x[:, :, 0], rtol=1e-6)        # position 0: identity
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-5)
+    # relative position: <R_m q, R_n k> depends on m - n only
+    q1 = rng.standard_normal(d).astype(np.float32)
+    k1 = rng.standard_normal(d).astype(np.float32)
+    Q = O.apply_rope(np.broadcast_to(q1, (1, 1, s, d)).copy(), cos, sin)[0, 0]
+    K = O.apply_rope(np.broadcast_to(k1, (1, 1, s, d)).copy(), cos, sin)[0, 0]
+    np.testing.assert_allclose(Q[10] @ K[4], Q[30] @ K[24], rtol=1e-4, atol=1e-4)
+    # pair (i, i + d/2) rotates by angle pos * theta^(-2i/d)
+    ang = 5 * 10000.0 ** (-2 * 3 / d)
+    e = np.zeros(d, np.float32)
+    e[3] = 1.0
+    r = O.apply_rope(np.broadcast_to(e, (1, 1, s, d)).copy(), cos, sin)[0, 0, 5]
+    np.testing.assert_allclose([r[3], r[3 + d // 2]], [math.cos(ang), math.sin(ang)], rtol=1e-5, atol=1e-6)
+
+
+def test_rms_norm_matches_torch():
+    x = np.random.default_rng(16).standard_normal((3, 5, 128)).astype(np.float32)
+    ref = F.rms_norm(torch.from_numpy(x), (128,), eps=1e-6).numpy()
+    np.testing.assert_allclose(O.rms_norm(x, 1e-6), ref, rtol=1e-5, atol=1e-6)
