@@ -48,7 +48,20 @@ def parse():
     p.add_argument("--cpu-budget", type=float, default=15.0,
                    help="approximate seconds of CPU oracle work for cpu_baseline (0: skip)")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
+                        "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return p.parse_args()
+
+
+def copy_calibration():
+    import torch
+    x = torch.ones(1 << 28, dtype=torch.float32, device="cuda")   # 1 GiB
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": x.numel() * 4, "launches": 3}), flush=True)
 
 
 def make_inputs(a, device):
@@ -149,6 +162,9 @@ def main():
     from oracle import delta_oracle as O
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if a.copy_calibration:
+        copy_calibration()
+        return
     L.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

@@ -17,12 +17,16 @@
 //   * O^T = V^T * P^T: the probabilities leave the score accumulator directly
 //     as the B operand, and the O^T accumulator again keeps one query row per
 //     lane, so the online-softmax rescale is a per-lane scalar.
-//   * K rows are staged to LDS in a row order (sigma) that makes each lane's 8
-//     keys per PV step contiguous; V is staged transposed (V^T) during the
-//     global->LDS copy. Both use XOR chunk swizzles so the 16-byte LDS reads
-//     and writes are bank-conflict free. Two LDS stages double-buffer the K/V
-//     tiles; the next tile's global loads are in flight during the MFMAs.
-//   * Lazy rescale: the running max only moves when a row's tile max exceeds
+//   * K/V tiles go global -> LDS by buffer-load DMA (no registers, no VALU
+//     address math: one scalar buffer base per tile, hardware zero-fill past
+//     the last key), double-buffered: the next tile is in flight while the
+//     current one is consumed. XOR chunk swizzles applied on the source side
+//     make the LDS fragment reads bank-conflict free.
+//   * K A-fragments read rows in a bit-permuted order (sigma) so that each
+//     lane's 8 keys per PV step are contiguous; V stays row-major in LDS and
+//     its V^T A-fragments come from transposed reads (ds_read_b64_tr_b16).
+//   * Softmax: one FMA + exp2 per score, row sum by v_dot2 over the packed P.
+//     Lazy rescale: the running max only moves when a row's tile max exceeds
 //     it by more than 2^8, so most tiles skip the O rescale.
 #include "device_common.h"
 #include "capi_common.h"
@@ -63,35 +67,39 @@ struct AttnArgs {
   float* part_ml;   // [item][2][BM]  (running max, row sum)
 };
 
-// sigma: LDS row order of a 32-key half-tile (swap bits 2 and 3). Row
-// sigma(r) of the A operand lands in accumulator row r, which puts keys
-// 8*g .. 8*g+7 (g = lane / 32) in accumulator elements 0..7 of every lane.
+// sigma: swaps bits 2 and 3 of a key index within a 32-key half tile. Using
+// K row sigma(r) as A-operand row r puts keys 8*g .. 8*g+7 (g = lane / 32) in
+// accumulator elements 0..7 of every lane, the order the PV step consumes.
 __device__ __forceinline__ int sigma32(int r) {
   return (r & 0x13) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
-// XOR swizzle of the 16-byte chunk index of K row `row` (row-major K tile).
-__device__ __forceinline__ int k_swz(int row) { return (row & 3) | ((row >> 1) & 4); }
-// XOR swizzle of the 16-byte chunk index of V^T row `d`.
-__device__ __forceinline__ int v_swz(int d) { return (d + (d >> 3)) & 7; }
 
 template <int D>
-struct Smem {
-  static constexpr int DCH = D / 8;        // 16-byte chunks per K row
-  u32x4 k[2][BN * DCH];                    // [stage][key row][chunk]
-  u32x4 v[2][D * (BN / 8)];                // [stage][d row][key chunk]  (V^T)
-  int red[4][4];
+struct Tile {
+  static constexpr int DCH = D / 8;          // 16-byte chunks per row
+  static constexpr int RB = D * 2;           // row bytes
+  static constexpr int BYTES = BN * RB;      // one K or V tile
+  // LDS chunk swizzles (XOR on the chunk index). K rows: sigma(row) & (DCH-1),
+  // so the A-fragment reads (rows sigma(lane)) hit every chunk column once per
+  // 16 lanes. V rows: 4 * (row & 3), so each transposed read of 4 rows x 32
+  // bytes spreads over distinct chunk columns.
+  static __device__ __forceinline__ int kswz(int row) { return sigma32(row & 31) & (DCH - 1); }
+  static __device__ __forceinline__ int vswz(int row) { return (4 * (row & 3)) & (DCH - 1); }
 };
 
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
-  constexpr int DCH = D / 8;
-  constexpr int NDS = D / 16;              // MFMA k-steps of Q.K^T
-  constexpr int NDT = D / 32;              // 32-row tiles of O^T
-  constexpr int KCH = BN * DCH / NTHR;     // K chunks loaded per thread
-  constexpr int DPT = D / 32;              // V dims per thread (8 keys x DPT dims)
+  using TL = Tile<D>;
+  constexpr int DCH = TL::DCH;
+  constexpr int RB = TL::RB;
+  constexpr int NDS = D / 16;                // MFMA k-steps of K.Q^T
+  constexpr int NDT = D / 32;                // 32-row tiles of O^T
+  constexpr int NDMA = TL::BYTES / (NTHR * 16);   // 16-byte DMA chunks per thread per tile
   using E = Elt<T>;
 
-  __shared__ Smem<D> sm;
+  // [stage][K, V][tile bytes]
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];
+  __shared__ int red[4][4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -148,27 +156,26 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
       v_lmax = max(v_lmax, __shfl_xor(v_lmax, off));
     }
     if (lane == 0) {
-      sm.red[0][wave] = v_hmin;
-      sm.red[1][wave] = v_hmax;
-      sm.red[2][wave] = v_lmin;
-      sm.red[3][wave] = v_lmax;
+      red[0][wave] = v_hmin;
+      red[1][wave] = v_hmax;
+      red[2][wave] = v_lmin;
+      red[3][wave] = v_lmax;
     }
   }
   __syncthreads();
-  const int hi_min = min(min(sm.red[0][0], sm.red[0][1]), min(sm.red[0][2], sm.red[0][3]));
-  const int hi_max = max(max(sm.red[1][0], sm.red[1][1]), max(sm.red[1][2], sm.red[1][3]));
-  const int lo_min = min(min(sm.red[2][0], sm.red[2][1]), min(sm.red[2][2], sm.red[2][3]));
-  const int lo_max = max(max(sm.red[3][0], sm.red[3][1]), max(sm.red[3][2], sm.red[3][3]));
+  const int hi_min = min(min(red[0][0], red[0][1]), min(red[0][2], red[0][3]));
+  const int hi_max = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
+  const int lo_min = min(min(red[2][0], red[2][1]), min(red[2][2], red[2][3]));
+  const int lo_max = max(max(red[3][0], red[3][1]), max(red[3][2], red[3][3]));
 
   // ---- key tiles to visit ----
-  int n_first, first_t0, n_second, second_t0;
+  int n_first, n_second, second_t0;
   if (MODE == MODE_SPARSE) {
     // sink tiles [0, ceil(min(sink, lo_min, hi_max + 1) / BN)), then window
     // tiles from the tile holding lo_min up to the tile holding hi_max.
     int sink_end = min(min(sink, lo_min), hi_max + 1);
     if (sink_end < 0) sink_end = 0;
     n_first = (sink_end + BN - 1) / BN;
-    first_t0 = 0;
     second_t0 = max(max(lo_min, 0) / BN, n_first);
     n_second = hi_max >= 0 ? max(0, hi_max / BN - second_t0 + 1) : 0;
   } else {
@@ -176,15 +183,16 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     if (c0 > hi_max) return;   // nothing visible: the merge skips this split
     const int c1 = min(c0 + a.chunk, hi_max + 1);
     n_first = 0;
-    first_t0 = 0;
     second_t0 = c0 / BN;
     n_second = (c1 - 1) / BN - second_t0 + 1;
   }
   const int nt = n_first + n_second;
 
-  const size_t esz = sizeof(T);
+  constexpr size_t esz = sizeof(T);
   const char* kbase = (const char*)a.k + ((int64_t)b * a.ks_b + (int64_t)hk * a.ks_h) * esz;
   const char* vbase = (const char*)a.v + ((int64_t)b * a.vs_b + (int64_t)hk * a.vs_h) * esz;
+  const int64_t krow_b = a.ks_s * (int64_t)esz;
+  const int64_t vrow_b = a.vs_s * (int64_t)esz;
 
   // ---- Q^T fragments (registers for the whole kernel) ----
   u32x4 qf[NDS];
@@ -196,58 +204,54 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
       qf[ds] = valid ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
   }
 
-  // ---- global -> register -> LDS staging of one K/V tile ----
-  u32x4 kreg[KCH];
-  uint32_t vreg[8][DPT / 2];
-  const int v_kc = tid >> 5;   // keys 8*v_kc .. 8*v_kc+7
-  const int v_dq = tid & 31;   // dims DPT*v_dq .. +DPT-1
-
+  // ---- DMA source offsets: wave `wave`, chunk c fills LDS slots
+  //      (c * 4 + wave) * 64 + lane of the tile; slot -> (row, swizzled chunk) ----
+  uint32_t koff[NDMA], voff[NDMA];
+#pragma unroll
+  for (int c = 0; c < NDMA; ++c) {
+    const int slot = (c * 4 + wave) * 64 + lane;
+    const int row = slot / DCH, pc = slot % DCH;
+    koff[c] = (uint32_t)(row * krow_b) + (uint32_t)((pc ^ TL::kswz(row)) * 16);
+    voff[c] = (uint32_t)(row * vrow_b) + (uint32_t)((pc ^ TL::vswz(row)) * 16);
+  }
   auto tile_n0 = [&](int t) -> int {
-    return (t < n_first ? first_t0 + t : second_t0 + (t - n_first)) * BN;
+    return (t < n_first ? t : second_t0 + (t - n_first)) * BN;
   };
-  auto gload = [&](int n0) {
+  auto issue_tile = [&](int t, int st) {
+    const int n0 = tile_n0(t);
+    const int64_t left = (int64_t)(a.n_kv - n0);
+    const int64_t kb64 = left * krow_b, vb64 = left * vrow_b;
+    const uint32_t kbytes = kb64 > 0xffffffffLL ? 0xffffffffu : (uint32_t)kb64;
+    const uint32_t vbytes = vb64 > 0xffffffffLL ? 0xffffffffu : (uint32_t)vb64;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + n0 * krow_b, kbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + n0 * vrow_b, vbytes);
 #pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int id = c * NTHR + tid;
-      const int row = id / DCH, ch = id % DCH;
-      const int key = n0 + row;
-      kreg[c] = key < a.n_kv ? *(const u32x4*)(kbase + ((int64_t)key * a.ks_s + ch * 8) * esz)
-                             : (u32x4){0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int key = n0 + 8 * v_kc + e;
-      const char* p = vbase + ((int64_t)key * a.vs_s + DPT * v_dq) * esz;
-      if constexpr (DPT == 4) {
-        u32x2 x = key < a.n_kv ? *(const u32x2*)p : (u32x2){0, 0};
-        vreg[e][0] = x[0];
-        vreg[e][1] = x[1];
-      } else {
-        vreg[e][0] = key < a.n_kv ? *(const uint32_t*)p : 0u;
-      }
+    for (int c = 0; c < NDMA; ++c) {
+      dma16(rk, (DA_LDS void*)(&smem[st][0][(c * 4 + wave) * 1024]), koff[c]);
+      dma16(rv, (DA_LDS void*)(&smem[st][1][(c * 4 + wave) * 1024]), voff[c]);
     }
   };
-  auto lstore = [&](int st) {
+
+  // ---- LDS read offsets ----
+  // K A-fragment for k-step ds: row sigma(ln) (+32 for keys 32..63), chunk
+  // (2 ds + lg) ^ kswz(row), and kswz(sigma(ln)) == ln & (DCH - 1).
+  int kread[NDS];
 #pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int id = c * NTHR + tid;
-      const int row = id / DCH, ch = id % DCH;
-      sm.k[st][row * DCH + (ch ^ k_swz(row))] = kreg[c];
+  for (int ds = 0; ds < NDS; ++ds)
+    kread[ds] = sigma32(ln) * RB + (((2 * ds + lg) ^ (ln & (DCH - 1))) * 16);
+  // V^T A-fragment via transposed reads: 16-lane group (hh, g) covers d-rows
+  // 32 dt + 16 hh + (0..15) and keys 16 ks + 8 g + 4 rd + (0..3); lane j of the
+  // group points at key row (j / 4), dims 4 (j % 4) .. +3.
+  int vread[NDT];
+  {
+    const int g4 = lane >> 4, hh = g4 & 1, g = g4 >> 1, j = lane & 15;
+    const int row = 8 * g + (j >> 2);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int lc = 4 * dt + 2 * hh + ((j & 3) >> 1);
+      vread[dt] = row * RB + ((lc ^ TL::vswz(row)) * 16) + (j & 1) * 8;
     }
-#pragma unroll
-    for (int x = 0; x < DPT; ++x) {
-      const int wsel = x >> 1;
-      const bool odd = x & 1;
-      u32x4 out;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const uint32_t a0 = vreg[2 * jj][wsel], a1 = vreg[2 * jj + 1][wsel];
-        out[jj] = odd ? ((a0 >> 16) | (a1 & 0xffff0000u)) : ((a0 & 0xffffu) | (a1 << 16));
-      }
-      const int d = DPT * v_dq + x;
-      sm.v[st][d * 8 + (v_kc ^ v_swz(d))] = out;
-    }
-  };
+  }
 
   f32x16 acc[NDT];
 #pragma unroll
@@ -255,61 +259,49 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
   float m_i = NEG_BIG, l_i = 0.f;
+  const float c2 = a.scale_log2;
 
-  const int krow0 = sigma32(ln);
-  const int kx = ln & 7;   // k_swz(krow0 + 32 * kt)
-  int vx[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) vx[dt] = v_swz(32 * dt + ln);
-
-  if (nt > 0) {
-    gload(tile_n0(0));
-    lstore(0);
-  }
+  if (nt > 0) issue_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   for (int t = 0; t < nt; ++t) {
     const int st = t & 1;
     const int n0 = tile_n0(t);
-    if (t + 1 < nt) gload(tile_n0(t + 1));
+    if (t + 1 < nt) issue_tile(t + 1, st ^ 1);
+    const DA_LDS char* ks = (const DA_LDS char*)&smem[st][0][0];
+    const DA_LDS char* vs = (const DA_LDS char*)&smem[st][1][0];
 
-    // S^T for keys n0 .. n0+31 (s0) and n0+32 .. n0+63 (s1)
+    // S^T for keys n0 .. n0+31 (s0) and n0+32 .. n0+63 (s1), raw (unscaled)
     f32x16 s0, s1;
 #pragma unroll
     for (int j = 0; j < 16; ++j) { s0[j] = 0.f; s1[j] = 0.f; }
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) {
-      const int ch = (2 * ds + lg) ^ kx;
-      const u32x4 ka = sm.k[st][krow0 * DCH + ch];
-      const u32x4 kb = sm.k[st][(krow0 + 32) * DCH + ch];
+      const u32x4 ka = *(const DA_LDS u32x4*)(ks + kread[ds]);
+      const u32x4 kb = *(const DA_LDS u32x4*)(ks + kread[ds] + 32 * RB);
       s0 = E::mfma(ka, qf[ds], s0);
       s1 = E::mfma(kb, qf[ds], s1);
     }
 
-    // scale (log2 domain) and mask; key of element j: n0 + 32*half + 16*(j/8) + 8*lg + j%8
+    // mask; key of element j: n0 + 32 * half + 16 * (j / 8) + 8 * lg + j % 8
     const int n1 = n0 + BN - 1;
     const bool full = (n1 <= hi_min) && (n1 < a.n_kv) && (n1 < sink || n0 >= lo_max);
-    float mx = NEG_BIG;
-    if (full) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        s0[j] *= a.scale_log2;
-        s1[j] *= a.scale_log2;
-        mx = fmaxf(mx, fmaxf(s0[j], s1[j]));
-      }
-    } else {
+    if (!full) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int key0 = n0 + 16 * (j >> 3) + 8 * lg + (j & 7);
         const int key1 = key0 + 32;
         const bool v0 = key0 <= hi && (key0 < sink || key0 >= lo);
         const bool v1 = key1 <= hi && (key1 < sink || key1 >= lo);
-        s0[j] = v0 ? s0[j] * a.scale_log2 : -INFINITY;
-        s1[j] = v1 ? s1[j] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, fmaxf(s0[j], s1[j]));
+        s0[j] = v0 ? s0[j] : -INFINITY;
+        s1[j] = v1 ? s1[j] : -INFINITY;
       }
     }
-    mx = max32(mx);
+    float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int j = 1; j < 16; ++j) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s0[j], s1[j]));
+    mx = max32(mx) * c2;          // scaling by c2 > 0 keeps the max
     if (__any(mx > m_i + RESCALE_THRESH)) {
       const float m_new = fmaxf(m_i, mx);
       const float alpha = fast_exp2(m_i - m_new);
@@ -320,33 +312,31 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
     }
-    float rs = 0.f;
+    // p = 2^(c2 s - m), packed to the element type; the row sum is taken over
+    // the packed values (the same P the PV product uses)
+    uint32_t pk[16];
+    const float nm = -m_i;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      s0[j] = fast_exp2(s0[j] - m_i);
-      s1[j] = fast_exp2(s1[j] - m_i);
-      rs += s0[j] + s1[j];
+    for (int j = 0; j < 8; ++j) {
+      pk[j] = E::pack2(fast_exp2(fmaf(s0[2 * j], c2, nm)), fast_exp2(fmaf(s0[2 * j + 1], c2, nm)));
+      pk[8 + j] = E::pack2(fast_exp2(fmaf(s1[2 * j], c2, nm)), fast_exp2(fmaf(s1[2 * j + 1], c2, nm)));
     }
-    l_i += rs;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) l_i = E::add_pair(pk[j], l_i);
 
     // O^T += V^T * P^T, 16 keys per step
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const f32x16& sp = (ks < 2) ? s0 : s1;
-      const int jb = 8 * (ks & 1);
-      u32x4 pf;
-      pf[0] = E::pack2(sp[jb + 0], sp[jb + 1]);
-      pf[1] = E::pack2(sp[jb + 2], sp[jb + 3]);
-      pf[2] = E::pack2(sp[jb + 4], sp[jb + 5]);
-      pf[3] = E::pack2(sp[jb + 6], sp[jb + 7]);
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 pf = {pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]};
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const u32x4 va = sm.v[st][(32 * dt + ln) * 8 + ((2 * ks + lg) ^ vx[dt])];
-        acc[dt] = E::mfma(va, pf, acc[dt]);
+        const u32x2 v0 = read_tr16(vs + vread[dt] + (16 * kk) * RB);
+        const u32x2 v1 = read_tr16(vs + vread[dt] + (16 * kk + 4) * RB);
+        acc[dt] = E::mfma((u32x4){v0[0], v0[1], v1[0], v1[1]}, pf, acc[dt]);
       }
     }
 
-    if (t + 1 < nt) lstore(st ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 
@@ -361,10 +351,10 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
         const int d = 32 * dt + 8 * jq + 4 * lg;
-        u32x2 pk;
-        pk[0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
-        pk[1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
-        *(u32x2*)(op + d * esz) = pk;
+        u32x2 pkd;
+        pkd[0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
+        pkd[1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+        *(u32x2*)(op + d * esz) = pkd;
       }
   } else {
     const int r = wave * 32 + ln;

@@ -33,6 +33,11 @@ template <> struct Elt<__bf16> {
   }
   static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
   static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  // acc + lo(w) + hi(w) in one v_dot2 (products with 1.0 are exact)
+  static __device__ __forceinline__ float add_pair(uint32_t w, float acc) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+  }
 };
 
 template <> struct Elt<_Float16> {
@@ -49,6 +54,10 @@ template <> struct Elt<_Float16> {
   }
   static __device__ __forceinline__ float hi(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  static __device__ __forceinline__ float add_pair(uint32_t w, float acc) {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
   }
 };
 
@@ -72,5 +81,27 @@ __device__ __forceinline__ float sum32(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+#define DA_LDS __attribute__((address_space(3)))
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource over `bytes` bytes from `base` (raw buffer: stride 0, word 3
+// = the gfx9 data-format default). Loads at offsets >= bytes return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane i of the wave
+// writes LDS bytes [lds + 16 i, lds + 16 i + 16). `lds` must be wave-uniform.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, DA_LDS void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
+}
+
+// Transposed 4 x b16 LDS read: within each 16-lane group, lane i gets element
+// (i % 4) of the 8-byte blocks addressed by lanes 4r + i/4, r = 0..3.
+__device__ __forceinline__ u32x2 read_tr16(const DA_LDS void* p) {
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((DA_LDS s16x4*)p);
+  return __builtin_bit_cast(u32x2, v);
+}
 
 }  // namespace da
