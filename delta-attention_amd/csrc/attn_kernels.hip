@@ -6,10 +6,11 @@
 //                                    delta epilogue.
 //
 // Tiling (one workgroup = 4 waves = 256 threads):
-//   * M tile: BM = 128 flattened (query row, head-in-group) pairs. The G query
-//     heads that share one key/value head are packed into the same tile, so
-//     K/V tiles are read once per group (no repeat_kv copies).
-//   * Each wave owns 32 flattened rows. Scores are formed transposed,
+//   * M tile: BM = 128 * RBW flattened (query row, head-in-group) pairs. The G
+//     query heads that share one key/value head are packed into the same
+//     tile, so K/V tiles are read once per group (no repeat_kv copies).
+//   * Each wave owns RBW blocks of 32 flattened rows; every K/V fragment read
+//     from LDS feeds RBW MFMAs. Scores are formed transposed,
 //     S^T = K * Q^T, with v_mfma_f32_32x32x16 (A = 32 keys x 16 dims from LDS,
 //     B = Q^T fragment kept in registers). In the 32x32 accumulator layout a
 //     lane holds one query row (lane % 32) and 16 of its keys, so the softmax
@@ -28,14 +29,28 @@
 //   * Softmax: one FMA + exp2 per score, row sum by v_dot2 over the packed P.
 //     Lazy rescale: the running max only moves when a row's tile max exceeds
 //     it by more than 2^8, so most tiles skip the O rescale.
+#include <type_traits>
+
 #include "device_common.h"
 #include "capi_common.h"
 
 namespace da {
 
-constexpr int BM = 128;   // flattened (row, head) pairs per workgroup
-constexpr int BN = 64;    // keys per tile
+// Row blocks of 32 query rows per wave (each K/V fragment read from LDS feeds
+// RBW MFMAs), LDS stages and DMA prefetch distance (in key tiles).
+#ifndef DA_ROW_BLOCKS
+#define DA_ROW_BLOCKS 1
+#endif
+constexpr int RBW = DA_ROW_BLOCKS;
+constexpr int BM = 128 * RBW;        // flattened (row, head) pairs per workgroup
+constexpr int BN = 64;               // keys per tile
 constexpr int NTHR = 256;
+constexpr int NSTAGE = RBW == 1 ? 2 : 4;
+constexpr int PREF = NSTAGE - 1;     // tiles in flight ahead of the K tile in use
+constexpr int WAVES_PER_EU = RBW == 1 ? 2 : 1;
+// Software pipelining of the score product (S(t+1) formed during the softmax of
+// tile t) doubles the live score registers; it is used with one row block.
+constexpr bool PIPE = RBW == 1;
 constexpr float RESCALE_THRESH = 8.0f;   // log2 domain
 constexpr float NEG_BIG = -1.0e30f;      // finite "minus infinity" for the running max
 
@@ -87,18 +102,39 @@ struct Tile {
   static __device__ __forceinline__ int vswz(int row) { return (4 * (row & 3)) & (DCH - 1); }
 };
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most `vm` vector
+// memory operations are outstanding; LDS and export counters are not waited on.
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(VM >= 0 && VM < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Wait until at most g groups of N DMA loads are outstanding (g <= 4).
+template <int N>
+__device__ __forceinline__ void wait_dma_groups(int g) {
+  switch (g) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<N>(); break;
+    case 2: wait_vmcnt<2 * N>(); break;
+    case 3: wait_vmcnt<3 * N>(); break;
+    default: wait_vmcnt<4 * N>(); break;
+  }
+}
+static_assert(2 * (NSTAGE - 2) <= 4, "wait_dma_groups covers at most 4 groups");
+
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a) {
   using TL = Tile<D>;
   constexpr int DCH = TL::DCH;
   constexpr int RB = TL::RB;
   constexpr int NDS = D / 16;                // MFMA k-steps of K.Q^T
   constexpr int NDT = D / 32;                // 32-row tiles of O^T
-  constexpr int NDMA = TL::BYTES / (NTHR * 16);   // 16-byte DMA chunks per thread per tile
+  constexpr int NDMA = TL::BYTES / (NTHR * 16);   // 16-byte DMA chunks per thread per K (or V) tile
   using E = Elt<T>;
 
   // [stage][K, V][tile bytes]
-  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE][2][TL::BYTES];
   __shared__ int red[4][4];
 
   const int tid = threadIdx.x;
@@ -125,42 +161,50 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   const int b = bh / a.Hkv;
   const int G = a.G;
 
-  // ---- this lane's query row ----
-  const int mflat = mt * BM + wave * 32 + ln;
-  const bool valid = mflat < a.n_rows * G;
-  const int i = valid ? mflat / G : 0;
-  const int h = hk * G + (valid ? mflat % G : 0);
-  int qrow, lo, hi;
-  if (MODE == MODE_SPARSE) {
-    qrow = i;
-    hi = valid ? i : -1;
-    lo = (i / a.q_block) * a.q_block + a.q_block - a.window;
-  } else {
-    qrow = a.q_rows ? (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1)) : i;
-    int64_t lim = a.row_last[(int64_t)b * a.rl_b + i];
-    if (lim > a.n_kv - 1) lim = a.n_kv - 1;
-    hi = valid ? (int)(lim < -1 ? -1 : lim) : -1;
-    lo = 0;
+  // ---- this lane's query rows: row block rb is flattened row
+  //      mt * BM + wave * 32 * RBW + 32 * rb + ln ----
+  bool valid[RBW];
+  int qrow[RBW], lo[RBW], hi[RBW], hrow[RBW];
+  int v_hmin = 0x7fffffff, v_hmax = -1, v_lmin = 0x7fffffff, v_lmax = (int)0x80000000;
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    const int mflat = mt * BM + wave * 32 * RBW + 32 * rb + ln;
+    valid[rb] = mflat < a.n_rows * G;
+    const int i = valid[rb] ? mflat / G : 0;
+    hrow[rb] = hk * G + (valid[rb] ? mflat % G : 0);
+    if (MODE == MODE_SPARSE) {
+      qrow[rb] = i;
+      hi[rb] = valid[rb] ? i : -1;
+      lo[rb] = (i / a.q_block) * a.q_block + a.q_block - a.window;
+    } else {
+      qrow[rb] = a.q_rows ? (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1)) : i;
+      int64_t lim = a.row_last[(int64_t)b * a.rl_b + i];
+      if (lim > a.n_kv - 1) lim = a.n_kv - 1;
+      hi[rb] = valid[rb] ? (int)(lim < -1 ? -1 : lim) : -1;
+      lo[rb] = 0;
+    }
+    if (valid[rb]) {
+      v_hmin = min(v_hmin, hi[rb]);
+      v_hmax = max(v_hmax, hi[rb]);
+      v_lmin = min(v_lmin, lo[rb]);
+      v_lmax = max(v_lmax, lo[rb]);
+    }
   }
   const int sink = (MODE == MODE_SPARSE) ? a.sink : 0;
 
   // ---- tile-wide bounds (valid rows only) ----
-  {
-    int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
-    int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      v_hmin = min(v_hmin, __shfl_xor(v_hmin, off));
-      v_hmax = max(v_hmax, __shfl_xor(v_hmax, off));
-      v_lmin = min(v_lmin, __shfl_xor(v_lmin, off));
-      v_lmax = max(v_lmax, __shfl_xor(v_lmax, off));
-    }
-    if (lane == 0) {
-      red[0][wave] = v_hmin;
-      red[1][wave] = v_hmax;
-      red[2][wave] = v_lmin;
-      red[3][wave] = v_lmax;
-    }
+  for (int off = 32; off >= 1; off >>= 1) {
+    v_hmin = min(v_hmin, __shfl_xor(v_hmin, off));
+    v_hmax = max(v_hmax, __shfl_xor(v_hmax, off));
+    v_lmin = min(v_lmin, __shfl_xor(v_lmin, off));
+    v_lmax = max(v_lmax, __shfl_xor(v_lmax, off));
+  }
+  if (lane == 0) {
+    red[0][wave] = v_hmin;
+    red[1][wave] = v_hmax;
+    red[2][wave] = v_lmin;
+    red[3][wave] = v_lmax;
   }
   __syncthreads();
   const int hi_min = min(min(red[0][0], red[0][1]), min(red[0][2], red[0][3]));
@@ -195,13 +239,14 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   const int64_t vrow_b = a.vs_s * (int64_t)esz;
 
   // ---- Q^T fragments (registers for the whole kernel) ----
-  u32x4 qf[NDS];
-  {
+  u32x4 qf[RBW][NDS];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
     const char* qp = (const char*)a.q +
-                     ((int64_t)b * a.qs_b + (int64_t)h * a.qs_h + (int64_t)qrow * a.qs_s) * esz;
+                     ((int64_t)b * a.qs_b + (int64_t)hrow[rb] * a.qs_h + (int64_t)qrow[rb] * a.qs_s) * esz;
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds)
-      qf[ds] = valid ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
+      qf[rb][ds] = valid[rb] ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
   }
 
   // ---- DMA source offsets: wave `wave`, chunk c fills LDS slots
@@ -217,19 +262,24 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   auto tile_n0 = [&](int t) -> int {
     return (t < n_first ? t : second_t0 + (t - n_first)) * BN;
   };
-  auto issue_tile = [&](int t, int st) {
+  // DMA of key tile t into LDS stage `slot` (K) / (V)
+  auto issue_k = [&](int t, int slot) {
     const int n0 = tile_n0(t);
-    const int64_t left = (int64_t)(a.n_kv - n0);
-    const int64_t kb64 = left * krow_b, vb64 = left * vrow_b;
-    const uint32_t kbytes = kb64 > 0xffffffffLL ? 0xffffffffu : (uint32_t)kb64;
-    const uint32_t vbytes = vb64 > 0xffffffffLL ? 0xffffffffu : (uint32_t)vb64;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + n0 * krow_b, kbytes);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + n0 * vrow_b, vbytes);
+    const int64_t kb64 = (int64_t)(a.n_kv - n0) * krow_b;
+    const __amdgpu_buffer_rsrc_t rk =
+        make_rsrc(kbase + n0 * krow_b, kb64 > 0xffffffffLL ? 0xffffffffu : (uint32_t)kb64);
 #pragma unroll
-    for (int c = 0; c < NDMA; ++c) {
-      dma16(rk, (DA_LDS void*)(&smem[st][0][(c * 4 + wave) * 1024]), koff[c]);
-      dma16(rv, (DA_LDS void*)(&smem[st][1][(c * 4 + wave) * 1024]), voff[c]);
-    }
+    for (int c = 0; c < NDMA; ++c)
+      dma16(rk, (DA_LDS void*)(&smem[slot][0][(c * 4 + wave) * 1024]), koff[c]);
+  };
+  auto issue_v = [&](int t, int slot) {
+    const int n0 = tile_n0(t);
+    const int64_t vb64 = (int64_t)(a.n_kv - n0) * vrow_b;
+    const __amdgpu_buffer_rsrc_t rv =
+        make_rsrc(vbase + n0 * vrow_b, vb64 > 0xffffffffLL ? 0xffffffffu : (uint32_t)vb64);
+#pragma unroll
+    for (int c = 0; c < NDMA; ++c)
+      dma16(rv, (DA_LDS void*)(&smem[slot][1][(c * 4 + wave) * 1024]), voff[c]);
   };
 
   // ---- LDS read offsets ----
@@ -253,123 +303,196 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     }
   }
 
-  f32x16 acc[NDT];
+  f32x16 acc[RBW][NDT];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+  for (int rb = 0; rb < RBW; ++rb)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
-  float m_i = NEG_BIG, l_i = 0.f;
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[rb][dt][j] = 0.f;
+  float m_i[RBW], l_i[RBW];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) { m_i[rb] = NEG_BIG; l_i[rb] = 0.f; }
   const float c2 = a.scale_log2;
 
-  if (nt > 0) issue_tile(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  for (int t = 0; t < nt; ++t) {
-    const int st = t & 1;
-    const int n0 = tile_n0(t);
-    if (t + 1 < nt) issue_tile(t + 1, st ^ 1);
-    const DA_LDS char* ks = (const DA_LDS char*)&smem[st][0][0];
-    const DA_LDS char* vs = (const DA_LDS char*)&smem[st][1][0];
-
-    // S^T for keys n0 .. n0+31 (s0) and n0+32 .. n0+63 (s1), raw (unscaled)
-    f32x16 s0, s1;
+  // S^T = K(stage) Q^T: x[rb][0] keys 0..31, x[rb][1] keys 32..63, raw
+  auto qk = [&](int stage, f32x16 (&x)[RBW][2]) {
+    const DA_LDS char* ks = (const DA_LDS char*)&smem[0][0][0] + stage * (2 * TL::BYTES);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) { s0[j] = 0.f; s1[j] = 0.f; }
+    for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) { x[rb][0][j] = 0.f; x[rb][1][j] = 0.f; }
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) {
       const u32x4 ka = *(const DA_LDS u32x4*)(ks + kread[ds]);
       const u32x4 kb = *(const DA_LDS u32x4*)(ks + kread[ds] + 32 * RB);
-      s0 = E::mfma(ka, qf[ds], s0);
-      s1 = E::mfma(kb, qf[ds], s1);
+#pragma unroll
+      for (int rb = 0; rb < RBW; ++rb) {
+        x[rb][0] = E::mfma(ka, qf[rb][ds], x[rb][0]);
+        x[rb][1] = E::mfma(kb, qf[rb][ds], x[rb][1]);
+      }
     }
+  };
 
-    // mask; key of element j: n0 + 32 * half + 16 * (j / 8) + 8 * lg + j % 8
+  // Loop over key tiles; K(u) and V(u) live in LDS stage u % NSTAGE and are
+  // loaded PREF tiles ahead. Pipelined (PIPE): at the top of step t, S(t) is in
+  // registers, V(t) and K(t+1) are resident, and step t issues K(t+1+PREF) and
+  // V(t+PREF), forms S(t+1) while the softmax of tile t runs, then O += V(t) P(t).
+  // Otherwise step t issues K/V(t+PREF), forms S(t), softmax, O += V(t) P(t).
+  // Every stage written in step t was last read in step t-1, before its
+  // closing barrier.
+  auto step = [&](int t, f32x16 (&cur)[RBW][2], f32x16 (&nxt)[RBW][2]) {
+    const int P = t % NSTAGE;
+    if (PIPE) {
+      if (t + 1 + PREF < nt) issue_k(t + 1 + PREF, (P + 1 + PREF) % NSTAGE);
+    } else {
+      if (t + PREF < nt) issue_k(t + PREF, (P + PREF) % NSTAGE);
+    }
+    if (t + PREF < nt) issue_v(t + PREF, (P + PREF) % NSTAGE);
+    if (!PIPE) qk(P, cur);
+    const int n0 = tile_n0(t);
     const int n1 = n0 + BN - 1;
     const bool full = (n1 <= hi_min) && (n1 < a.n_kv) && (n1 < sink || n0 >= lo_max);
     if (!full) {
+      // key of element j: n0 + 32 * half + 16 * (j / 8) + 8 * lg + j % 8
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key0 = n0 + 16 * (j >> 3) + 8 * lg + (j & 7);
-        const int key1 = key0 + 32;
-        const bool v0 = key0 <= hi && (key0 < sink || key0 >= lo);
-        const bool v1 = key1 <= hi && (key1 < sink || key1 >= lo);
-        s0[j] = v0 ? s0[j] : -INFINITY;
-        s1[j] = v1 ? s1[j] : -INFINITY;
-      }
+      for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key0 = n0 + 16 * (j >> 3) + 8 * lg + (j & 7);
+          const int key1 = key0 + 32;
+          const bool v0 = key0 <= hi[rb] && (key0 < sink || key0 >= lo[rb]);
+          const bool v1 = key1 <= hi[rb] && (key1 < sink || key1 >= lo[rb]);
+          cur[rb][0][j] = v0 ? cur[rb][0][j] : -INFINITY;
+          cur[rb][1][j] = v1 ? cur[rb][1][j] : -INFINITY;
+        }
     }
-    float mx = fmaxf(s0[0], s1[0]);
+    float alpha[RBW];
+    bool up = false;
 #pragma unroll
-    for (int j = 1; j < 16; ++j) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s0[j], s1[j]));
-    mx = max32(mx) * c2;          // scaling by c2 > 0 keeps the max
-    if (__any(mx > m_i + RESCALE_THRESH)) {
-      const float m_new = fmaxf(m_i, mx);
-      const float alpha = fast_exp2(m_i - m_new);
-      m_i = m_new;
-      l_i *= alpha;
+    for (int rb = 0; rb < RBW; ++rb) {
+      float mx = __builtin_fmaxf(cur[rb][0][0], cur[rb][1][0]);
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+      for (int j = 1; j < 16; ++j) mx = __builtin_fmaxf(mx, __builtin_fmaxf(cur[rb][0][j], cur[rb][1][j]));
+      mx = max32(mx) * c2;          // scaling by c2 > 0 keeps the max
+      const bool u = __any(mx > m_i[rb] + RESCALE_THRESH);
+      const float m_new = u ? fmaxf(m_i[rb], mx) : m_i[rb];
+      alpha[rb] = fast_exp2(m_i[rb] - m_new);
+      m_i[rb] = m_new;
+      l_i[rb] *= alpha[rb];
+      up = up || u;
     }
     // p = 2^(c2 s - m), packed to the element type; the row sum is taken over
     // the packed values (the same P the PV product uses)
-    uint32_t pk[16];
-    const float nm = -m_i;
+    uint32_t pk[RBW][16];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      pk[j] = E::pack2(fast_exp2(fmaf(s0[2 * j], c2, nm)), fast_exp2(fmaf(s0[2 * j + 1], c2, nm)));
-      pk[8 + j] = E::pack2(fast_exp2(fmaf(s1[2 * j], c2, nm)), fast_exp2(fmaf(s1[2 * j + 1], c2, nm)));
+    for (int rb = 0; rb < RBW; ++rb) {
+      const float nm = -m_i[rb];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pk[rb][j] = E::pack2(fast_exp2(fmaf(cur[rb][0][2 * j], c2, nm)),
+                             fast_exp2(fmaf(cur[rb][0][2 * j + 1], c2, nm)));
+        pk[rb][8 + j] = E::pack2(fast_exp2(fmaf(cur[rb][1][2 * j], c2, nm)),
+                                 fast_exp2(fmaf(cur[rb][1][2 * j + 1], c2, nm)));
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) l_i[rb] = E::add_pair(pk[rb][j], l_i[rb]);
     }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) l_i = E::add_pair(pk[j], l_i);
 
+    // always formed (the last tile's extra product reads stale LDS and is dropped),
+    // so that these MFMAs share a scheduling region with the exponentials above
+    if (PIPE) qk((P + 1) % NSTAGE, nxt);
+
+    if (up) {
+#pragma unroll
+      for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[rb][dt][j] *= alpha[rb];
+    }
     // O^T += V^T * P^T, 16 keys per step
+    const DA_LDS char* vs = (const DA_LDS char*)&smem[0][1][0] + P * (2 * TL::BYTES);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 pf = {pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]};
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
         const u32x2 v0 = read_tr16(vs + vread[dt] + (16 * kk) * RB);
         const u32x2 v1 = read_tr16(vs + vread[dt] + (16 * kk + 4) * RB);
-        acc[dt] = E::mfma((u32x4){v0[0], v0[1], v1[0], v1[1]}, pf, acc[dt]);
+        const u32x4 va = {v0[0], v0[1], v1[0], v1[1]};
+#pragma unroll
+        for (int rb = 0; rb < RBW; ++rb) {
+          const u32x4 pf = {pk[rb][4 * kk], pk[rb][4 * kk + 1], pk[rb][4 * kk + 2], pk[rb][4 * kk + 3]};
+          acc[rb][dt] = E::mfma(va, pf, acc[rb][dt]);
+        }
       }
     }
-
-    __builtin_amdgcn_s_waitcnt(0);
+    // The tiles the next step reads must have landed: K(t+2) (pipelined) or
+    // K(t+1), and V(t+1). Issued after them (and so allowed to stay in
+    // flight): K(u) for t+3 <= u <= t+1+PREF (pipelined) or t+2 <= u <= t+PREF,
+    // and V(u) for t+2 <= u <= t+PREF, those with u < nt, NDMA loads each.
+    const int younger = max(0, min(PREF - 1, nt - t - (PIPE ? 3 : 2))) +
+                        max(0, min(PREF - 1, nt - t - 2));
+    wait_dma_groups<NDMA>(younger);
     __syncthreads();
+  };
+
+  f32x16 sa[RBW][2], sb[RBW][2];
+  if (nt > 0) {
+    // prologue: K(0..PREF) (pipelined) or K(0..PREF-1), and V(0..PREF-1)
+    issue_k(0, 0);
+    issue_v(0, 0);
+#pragma unroll
+    for (int u = 1; u <= PREF; ++u) {
+      if (u < nt && (PIPE || u < PREF)) issue_k(u, u % NSTAGE);
+      if (u < PREF && u < nt) issue_v(u, u % NSTAGE);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (PIPE) {
+      qk(0, sa);
+      __syncthreads();   // every wave is done with K stage 0 before it is refilled
+    }
+  }
+  for (int t = 0; t < nt; t += 2) {
+    step(t, sa, sb);
+    if (t + 1 < nt) step(t + 1, sb, sa);
   }
 
   // ---- epilogue ----
-  const float l_tot = sum32(l_i);
-  if (MODE == MODE_SPARSE) {
-    if (!valid) return;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)h * a.os_h + (int64_t)qrow * a.os_s) * esz;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+  for (int rb = 0; rb < RBW; ++rb) {
+    const float l_tot = sum32(l_i[rb]);
+    if (MODE == MODE_SPARSE) {
+      if (!valid[rb]) continue;
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow[rb] * a.os_h +
+                               (int64_t)qrow[rb] * a.os_s) * esz;
 #pragma unroll
-      for (int jq = 0; jq < 4; ++jq) {
-        const int d = 32 * dt + 8 * jq + 4 * lg;
-        u32x2 pkd;
-        pkd[0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
-        pkd[1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
-        *(u32x2*)(op + d * esz) = pkd;
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          const int d = 32 * dt + 8 * jq + 4 * lg;
+          u32x2 pkd;
+          pkd[0] = E::pack2(acc[rb][dt][4 * jq + 0] * inv, acc[rb][dt][4 * jq + 1] * inv);
+          pkd[1] = E::pack2(acc[rb][dt][4 * jq + 2] * inv, acc[rb][dt][4 * jq + 3] * inv);
+          *(u32x2*)(op + d * esz) = pkd;
+        }
+    } else {
+      const int r = wave * 32 * RBW + 32 * rb + ln;
+      float* po = a.part_o + ((int64_t)w * BM + r) * D;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          const int d = 32 * dt + 8 * jq + 4 * lg;
+          *(f32x4*)(po + d) = (f32x4){acc[rb][dt][4 * jq + 0], acc[rb][dt][4 * jq + 1],
+                                       acc[rb][dt][4 * jq + 2], acc[rb][dt][4 * jq + 3]};
+        }
+      if (lg == 0) {
+        a.part_ml[(int64_t)w * 2 * BM + r] = m_i[rb];
+        a.part_ml[(int64_t)w * 2 * BM + BM + r] = l_tot;
       }
-  } else {
-    const int r = wave * 32 + ln;
-    float* po = a.part_o + ((int64_t)w * BM + r) * D;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq) {
-        const int d = 32 * dt + 8 * jq + 4 * lg;
-        *(f32x4*)(po + d) = (f32x4){acc[dt][4 * jq + 0], acc[dt][4 * jq + 1],
-                                     acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]};
-      }
-    if (lg == 0) {
-      a.part_ml[(int64_t)w * 2 * BM + r] = m_i;
-      a.part_ml[(int64_t)w * 2 * BM + BM + r] = l_tot;
     }
   }
 }
