@@ -227,6 +227,8 @@ def main():
                       "frac_hbm": round(bytes_add / k_ms[2] / 1e6 / PEAK_HBM_GBS, 4),
                       "bytes": bytes_add},
     }
+    for name in kernels:
+        kernels[name]["traffic"] = load_traffic(name)
     dom = "sparse_attn" if k_ms[0] >= k_ms[1] else "qsparse_attn"
     achieved = kernels[dom]["tflops"]
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
