@@ -48,6 +48,10 @@ def parse():
     p.add_argument("--cpu-budget", type=float, default=15.0,
                    help="approximate seconds of CPU oracle work for cpu_baseline (0: skip)")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--gamma-sweep", type=str, default="",
+                   help="comma-separated gammas: print one JSON line per gamma (layer time, "
+                        "TFLOP/s, row cosine to full causal attention on sampled rows) "
+                        "instead of the headline line")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -139,6 +143,47 @@ def cpu_baseline(a, q, k, v, flops_layer):
     }
 
 
+def gamma_sweep(a, q, k, v, gammas):
+    """Per gamma: layer prefill time and the correction quality, i.e. the
+    per-row cosine (over heads x dims) between the delta output and full causal
+    attention at 512 sampled rows (dense rows from the query-sparse kernel)."""
+    import torch
+    from delta_attention import ops
+    from oracle import delta_oracle as O
+    B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
+    scale = D ** -0.5
+    g = torch.Generator().manual_seed(1)
+    rows = torch.randperm(S, generator=g)[:512].sort().values.cuda()
+    dense = ops.qsparse_attention(q, k, v, rows, scale, q_rows=rows).transpose(1, 2)
+    sparse = ops.delta_prefill(q, k, v, gamma=64, window=a.window, sink=a.sink, sm_scale=scale,
+                               mode="sparse-only")
+    cs = torch.nn.functional.cosine_similarity(sparse[:, rows].reshape(B, 512, -1).float(),
+                                               dense.reshape(B, 512, -1).float(), dim=-1)
+    del sparse
+    f_sparse = O.flops_sparse(B, H, D, S, a.window, a.sink)
+    for gm in gammas:
+        fn = lambda: ops.delta_prefill(q, k, v, gamma=gm, window=a.window, sink=a.sink, sm_scale=scale)
+        for _ in range(a.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            out = fn()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / a.steps * 1e3
+        cos = torch.nn.functional.cosine_similarity(out[:, rows].reshape(B, 512, -1).float(),
+                                                    dense.reshape(B, 512, -1).float(), dim=-1)
+        f_q = O.flops_qsparse(B, H, D, O.selected_rows(S, gm))
+        print(json.dumps({
+            "gamma": gm, "ms_per_layer": round(ms, 4),
+            "tflops": round((f_sparse + f_q) / (ms * 1e-3) / 1e12, 2),
+            "flop_sparse": f_sparse, "flop_qsparse": f_q,
+            "selected_rows": int(len(O.selected_rows(S, gm))),
+            "cos_to_full_mean": round(cos.mean().item(), 6), "cos_to_full_min": round(cos.min().item(), 6),
+            "sparse_only_cos_mean": round(cs.mean().item(), 6), "sparse_only_cos_min": round(cs.min().item(), 6),
+            "seq_len": S, "window": a.window, "sink": a.sink}), flush=True)
+
+
 def load_traffic(name):
     """HBM bytes per launch of `name` from the committed rocprofv3 PMC summary."""
     path = os.path.join(REPO, "profiles", "hbm_traffic.json")
@@ -171,6 +216,10 @@ def main():
     B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
     scale = D ** -0.5
     q, k, v = make_inputs(a, dev)
+
+    if a.gamma_sweep:
+        gamma_sweep(a, q, k, v, [int(x) for x in a.gamma_sweep.split(",")])
+        return
 
     cut_n, s_p, n_anchor = ops.anchor_layout(S, a.gamma)
     idx = ops.selected_rows(S, a.gamma, str(dev))

@@ -341,7 +341,8 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
   // Otherwise step t issues K/V(t+PREF), forms S(t), softmax, O += V(t) P(t).
   // Every stage written in step t was last read in step t-1, before its
   // closing barrier.
-  auto step = [&](int t, f32x16 (&cur)[RBW][2], f32x16 (&nxt)[RBW][2]) {
+  auto step = [&](int t, auto last_tag, f32x16 (&cur)[RBW][2], f32x16 (&nxt)[RBW][2]) {
+    constexpr bool LAST = decltype(last_tag)::value;   // t == nt - 1
     const int P = t % NSTAGE;
     if (PIPE) {
       if (t + 1 + PREF < nt) issue_k(t + 1 + PREF, (P + 1 + PREF) % NSTAGE);
@@ -399,9 +400,9 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
       for (int j = 0; j < 16; ++j) l_i[rb] = E::add_pair(pk[rb][j], l_i[rb]);
     }
 
-    // always formed (the last tile's extra product reads stale LDS and is dropped),
-    // so that these MFMAs share a scheduling region with the exponentials above
-    if (PIPE) qk((P + 1) % NSTAGE, nxt);
+    // no branch around it, so that these MFMAs share a scheduling region with
+    // the exponentials above; the last step is a separate instantiation
+    if (PIPE && !LAST) qk((P + 1) % NSTAGE, nxt);
 
     if (up) {
 #pragma unroll
@@ -454,9 +455,18 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
       __syncthreads();   // every wave is done with K stage 0 before it is refilled
     }
   }
-  for (int t = 0; t < nt; t += 2) {
-    step(t, sa, sb);
-    if (t + 1 < nt) step(t + 1, sb, sa);
+  using NotLast = std::integral_constant<bool, false>;
+  using Last = std::integral_constant<bool, true>;
+  int t = 0;
+  for (; t + 2 < nt; t += 2) {
+    step(t, NotLast(), sa, sb);
+    step(t + 1, NotLast(), sb, sa);
+  }
+  if (t + 1 < nt) {          // two tiles left
+    step(t, NotLast(), sa, sb);
+    step(t + 1, Last(), sb, sa);
+  } else if (t < nt) {       // one tile left
+    step(t, Last(), sa, sb);
   }
 
   // ---- epilogue ----

@@ -157,12 +157,15 @@ def masked_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, allowed: np.nd
 
 
 def sparse_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, window: int, sink: int,
-                     scale: float, q_block: int = Q_BLOCK, rows: Optional[np.ndarray] = None) -> np.ndarray:
+                     scale: float, q_block: int = Q_BLOCK, rows: Optional[np.ndarray] = None,
+                     q_is_rows: bool = False) -> np.ndarray:
     """Key-sparse attention. q [B,H,S,d], k/v [B,Hkv,S,d] -> [B,S,H,d]
     (the layout hip_attention_interface returns, llama.py:394-449).
     Computed per q_block row block on the union of its sink and window keys.
-    rows: optional subset of rows (sorted); the result then has len(rows) rows."""
-    B, H, S, d = q.shape
+    rows: optional subset of rows (sorted); the result then has len(rows) rows.
+    q_is_rows: q already holds only those rows ([B,H,len(rows),d])."""
+    B, H, _, d = q.shape
+    S = k.shape[2]
     kk, vv = _expand_kv(k, H), _expand_kv(v, H)
     all_rows = np.arange(S) if rows is None else np.asarray(rows, dtype=np.int64)
     out = np.zeros((B, len(all_rows), H, d), dtype=q.dtype)
@@ -174,7 +177,8 @@ def sparse_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, window: int, s
         keys = np.unique(np.concatenate([np.arange(min(sink, S)), np.arange(ws, int(r.max()) + 1)]))
         keys = keys[keys < S]
         allowed = sparse_visible(r[:, None], keys[None, :], window, sink, q_block)
-        sc = np.matmul(q[:, :, r], kk[:, :, keys].swapaxes(-1, -2)) * scale
+        qr = q[:, :, sel] if q_is_rows else q[:, :, r]
+        sc = np.matmul(qr, kk[:, :, keys].swapaxes(-1, -2)) * scale
         sc = np.where(allowed[None, None], sc, -np.inf)
         o = np.matmul(_softmax_rows(sc), vv[:, :, keys])
         out[:, sel] = o.transpose(0, 2, 1, 3)
