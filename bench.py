@@ -52,6 +52,11 @@ def parse():
                    help="comma-separated gammas: print one JSON line per gamma (layer time, "
                         "TFLOP/s, row cosine to full causal attention on sampled rows) "
                         "instead of the headline line")
+    p.add_argument("--prologue", action="store_true",
+                   help="time only the fused RoPE (+ optional per-head q/k RMSNorm with "
+                        "--qk-norm) prologue kernel on the workload's [B,S,H,D] q/k projection "
+                        "outputs and print one JSON line with its HBM roofline")
+    p.add_argument("--qk-norm", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -184,6 +189,42 @@ def gamma_sweep(a, q, k, v, gammas):
             "seq_len": S, "window": a.window, "sink": a.sink}), flush=True)
 
 
+def prologue(a, dev):
+    """The fused prologue kernel (da_rope_qk) in place on a packed projection
+    buffer [B, S, (Hq + 2 Hkv) D]: algorithmic bytes = read + write of every q
+    and k element, plus the bf16 cos/sin rows once per token."""
+    import torch
+    from delta_attention import ops
+    from delta_attention.llama import rope_cos_sin
+    B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
+    buf = torch.randn(B, S, (H + 2 * Hkv) * D, device=dev, dtype=torch.bfloat16)
+    q = buf[..., :H * D].view(B, S, H, D)
+    k = buf[..., H * D:(H + Hkv) * D].view(B, S, Hkv, D)
+    cos, sin = rope_cos_sin(torch.arange(S, device=dev)[None], D, a.rope_theta, torch.bfloat16)
+    w = torch.ones(D, device=dev, dtype=torch.bfloat16) if a.qk_norm else None
+    fn = lambda: ops.rope_qk(q, k, cos, sin, q_norm_w=w, k_norm_w=w)
+    for _ in range(a.warmup):
+        fn()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(a.steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / a.steps
+    nbytes = 2 * B * S * (H + Hkv) * D * 2 + 2 * S * D * 2 + (4 * D if a.qk_norm else 0)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "fused RoPE prologue (da_rope_qk, 2 launches: q then k)", "value": round(gbs, 1),
+        "unit": "GB/s", "ms_per_call": round(ms, 4), "steps": a.steps, "warmup": a.warmup,
+        "qk_norm": bool(a.qk_norm), "bytes_per_call": nbytes,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)},
+        "config": {"batch": B, "seq_len": S, "heads": H, "kv_heads": Hkv, "head_dim": D}}), flush=True)
+
+
 def load_traffic(name):
     """HBM bytes per launch of `name` from the committed rocprofv3 PMC summary."""
     path = os.path.join(REPO, "profiles", "hbm_traffic.json")
@@ -213,6 +254,9 @@ def main():
     L.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if a.prologue:
+        prologue(a, dev)
+        return
     B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
     scale = D ** -0.5
     q, k, v = make_inputs(a, dev)

@@ -41,16 +41,27 @@ namespace da {
 #ifndef DA_ROW_BLOCKS
 #define DA_ROW_BLOCKS 1
 #endif
+#ifndef DA_BLOCK_N
+#define DA_BLOCK_N 64
+#endif
+#ifndef DA_WAVES_PER_EU
+#define DA_WAVES_PER_EU (DA_ROW_BLOCKS == 1 ? 2 : 1)
+#endif
+// Software pipelining of the score product (S(t+1) formed during the softmax of
+// tile t) doubles the live score registers; it is used with one row block.
+#ifndef DA_PIPELINE
+#define DA_PIPELINE (DA_ROW_BLOCKS == 1)
+#endif
 constexpr int RBW = DA_ROW_BLOCKS;
 constexpr int BM = 128 * RBW;        // flattened (row, head) pairs per workgroup
-constexpr int BN = 64;               // keys per tile
+constexpr int BN = DA_BLOCK_N;       // keys per tile (32 or 64)
+constexpr int NH = BN / 32;          // 32-key halves per tile
 constexpr int NTHR = 256;
 constexpr int NSTAGE = RBW == 1 ? 2 : 4;
 constexpr int PREF = NSTAGE - 1;     // tiles in flight ahead of the K tile in use
-constexpr int WAVES_PER_EU = RBW == 1 ? 2 : 1;
-// Software pipelining of the score product (S(t+1) formed during the softmax of
-// tile t) doubles the live score registers; it is used with one row block.
-constexpr bool PIPE = RBW == 1;
+constexpr int WAVES_PER_EU = DA_WAVES_PER_EU;
+constexpr bool PIPE = DA_PIPELINE;
+static_assert(BN == 32 || BN == 64, "key tile is 32 or 64 keys");
 constexpr float RESCALE_THRESH = 8.0f;   // log2 domain
 constexpr float NEG_BIG = -1.0e30f;      // finite "minus infinity" for the running max
 
@@ -315,21 +326,22 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
   for (int rb = 0; rb < RBW; ++rb) { m_i[rb] = NEG_BIG; l_i[rb] = 0.f; }
   const float c2 = a.scale_log2;
 
-  // S^T = K(stage) Q^T: x[rb][0] keys 0..31, x[rb][1] keys 32..63, raw
-  auto qk = [&](int stage, f32x16 (&x)[RBW][2]) {
+  // S^T = K(stage) Q^T: x[rb][hf] holds keys 32 hf .. 32 hf + 31 of the tile, raw
+  auto qk = [&](int stage, f32x16 (&x)[RBW][NH]) {
     const DA_LDS char* ks = (const DA_LDS char*)&smem[0][0][0] + stage * (2 * TL::BYTES);
 #pragma unroll
     for (int rb = 0; rb < RBW; ++rb)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) { x[rb][0][j] = 0.f; x[rb][1][j] = 0.f; }
+      for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) x[rb][hf][j] = 0.f;
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) {
-      const u32x4 ka = *(const DA_LDS u32x4*)(ks + kread[ds]);
-      const u32x4 kb = *(const DA_LDS u32x4*)(ks + kread[ds] + 32 * RB);
 #pragma unroll
-      for (int rb = 0; rb < RBW; ++rb) {
-        x[rb][0] = E::mfma(ka, qf[rb][ds], x[rb][0]);
-        x[rb][1] = E::mfma(kb, qf[rb][ds], x[rb][1]);
+      for (int hf = 0; hf < NH; ++hf) {
+        const u32x4 ka = *(const DA_LDS u32x4*)(ks + kread[ds] + 32 * hf * RB);
+#pragma unroll
+        for (int rb = 0; rb < RBW; ++rb) x[rb][hf] = E::mfma(ka, qf[rb][ds], x[rb][hf]);
       }
     }
   };
@@ -341,7 +353,7 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
   // Otherwise step t issues K/V(t+PREF), forms S(t), softmax, O += V(t) P(t).
   // Every stage written in step t was last read in step t-1, before its
   // closing barrier.
-  auto step = [&](int t, auto last_tag, f32x16 (&cur)[RBW][2], f32x16 (&nxt)[RBW][2]) {
+  auto step = [&](int t, auto last_tag, f32x16 (&cur)[RBW][NH], f32x16 (&nxt)[RBW][NH]) {
     constexpr bool LAST = decltype(last_tag)::value;   // t == nt - 1
     const int P = t % NSTAGE;
     if (PIPE) {
@@ -355,26 +367,27 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
     const int n1 = n0 + BN - 1;
     const bool full = (n1 <= hi_min) && (n1 < a.n_kv) && (n1 < sink || n0 >= lo_max);
     if (!full) {
-      // key of element j: n0 + 32 * half + 16 * (j / 8) + 8 * lg + j % 8
+      // key of element j of half hf: n0 + 32 hf + 16 (j / 8) + 8 lg + j % 8
 #pragma unroll
       for (int rb = 0; rb < RBW; ++rb)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key0 = n0 + 16 * (j >> 3) + 8 * lg + (j & 7);
-          const int key1 = key0 + 32;
-          const bool v0 = key0 <= hi[rb] && (key0 < sink || key0 >= lo[rb]);
-          const bool v1 = key1 <= hi[rb] && (key1 < sink || key1 >= lo[rb]);
-          cur[rb][0][j] = v0 ? cur[rb][0][j] : -INFINITY;
-          cur[rb][1][j] = v1 ? cur[rb][1][j] : -INFINITY;
-        }
+        for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int key = n0 + 32 * hf + 16 * (j >> 3) + 8 * lg + (j & 7);
+            const bool vis = key <= hi[rb] && (key < sink || key >= lo[rb]);
+            cur[rb][hf][j] = vis ? cur[rb][hf][j] : -INFINITY;
+          }
     }
     float alpha[RBW];
     bool up = false;
 #pragma unroll
     for (int rb = 0; rb < RBW; ++rb) {
-      float mx = __builtin_fmaxf(cur[rb][0][0], cur[rb][1][0]);
+      float mx = cur[rb][0][0];
 #pragma unroll
-      for (int j = 1; j < 16; ++j) mx = __builtin_fmaxf(mx, __builtin_fmaxf(cur[rb][0][j], cur[rb][1][j]));
+      for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mx = __builtin_fmaxf(mx, cur[rb][hf][j]);
       mx = max32(mx) * c2;          // scaling by c2 > 0 keeps the max
       const bool u = __any(mx > m_i[rb] + RESCALE_THRESH);
       const float m_new = u ? fmaxf(m_i[rb], mx) : m_i[rb];
@@ -385,19 +398,18 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
     }
     // p = 2^(c2 s - m), packed to the element type; the row sum is taken over
     // the packed values (the same P the PV product uses)
-    uint32_t pk[RBW][16];
+    uint32_t pk[RBW][8 * NH];
 #pragma unroll
     for (int rb = 0; rb < RBW; ++rb) {
       const float nm = -m_i[rb];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pk[rb][j] = E::pack2(fast_exp2(fmaf(cur[rb][0][2 * j], c2, nm)),
-                             fast_exp2(fmaf(cur[rb][0][2 * j + 1], c2, nm)));
-        pk[rb][8 + j] = E::pack2(fast_exp2(fmaf(cur[rb][1][2 * j], c2, nm)),
-                                 fast_exp2(fmaf(cur[rb][1][2 * j + 1], c2, nm)));
-      }
+      for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) l_i[rb] = E::add_pair(pk[rb][j], l_i[rb]);
+        for (int j = 0; j < 8; ++j)
+          pk[rb][8 * hf + j] = E::pack2(fast_exp2(fmaf(cur[rb][hf][2 * j], c2, nm)),
+                                        fast_exp2(fmaf(cur[rb][hf][2 * j + 1], c2, nm)));
+#pragma unroll
+      for (int j = 0; j < 8 * NH; ++j) l_i[rb] = E::add_pair(pk[rb][j], l_i[rb]);
     }
 
     // no branch around it, so that these MFMAs share a scheduling region with
@@ -415,7 +427,7 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
     // O^T += V^T * P^T, 16 keys per step
     const DA_LDS char* vs = (const DA_LDS char*)&smem[0][1][0] + P * (2 * TL::BYTES);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < 2 * NH; ++kk) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
         const u32x2 v0 = read_tr16(vs + vread[dt] + (16 * kk) * RB);
@@ -438,7 +450,7 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
     __syncthreads();
   };
 
-  f32x16 sa[RBW][2], sb[RBW][2];
+  f32x16 sa[RBW][NH], sb[RBW][NH];
   if (nt > 0) {
     // prologue: K(0..PREF) (pipelined) or K(0..PREF-1), and V(0..PREF-1)
     issue_k(0, 0);

@@ -1,0 +1,170 @@
+// Fused attention prologue: optional per-head RMSNorm (Qwen3) and rotary
+// position embedding, in place on the q and k projection outputs, in the
+// layout the attention kernels read directly ([B, S, H, D] storage).
+//
+// Arithmetic follows the reference's torch ops element by element
+// (delta_attention/llama.py:69-74 RMSNorm, :161-192 RoPE with bf16/fp16 cos/sin
+// tables), one rounding to the element type per tensor op:
+//   norm:  y = rnd(w * rnd(x * rsqrt(mean(x^2) + eps)))          (fp32 inside)
+//   rope:  out[i]       = rnd(rnd(y[i] * cos[i])       - rnd(y[i+D/2] * sin[i]))
+//          out[i + D/2] = rnd(rnd(y[i+D/2] * cos[i+D/2]) + rnd(y[i] * sin[i+D/2]))
+// HBM-bound: each row is read once and written once with 16-byte accesses;
+// 8 consecutive threads own one (token, head) row (8 + 8 elements each for D=128).
+#include "device_common.h"
+#include "capi_common.h"
+
+namespace da {
+
+struct RopeArgs {
+  void* x;                 // [B, S, H, D] (strides b, s, h in elements)
+  int64_t xs_b, xs_s, xs_h;
+  int H;
+  const void* cos;         // [Bc, S, D], Bc in {1, B}
+  const void* sin;
+  int64_t cs_b, cs_s;
+  const void* w;           // [D] norm weight or nullptr
+  float eps;
+  int B, S, D;
+  int64_t rows;            // B * S * H
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+  using E = Elt<T>;
+  constexpr int TPR = 8;              // threads per row
+  constexpr int HALF = D / 2;
+  constexpr int EPT = HALF / TPR;     // elements per thread in each half (8 for D=128)
+  static_assert(EPT == 8 || EPT == 4, "D must be 64 or 128");
+  const int64_t gtid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gtid / TPR;
+  const int part = (int)(gtid % TPR);
+  const bool live = row < a.rows;
+  const int64_t rr = live ? row : 0;
+  const int h = (int)(rr % a.H);
+  const int64_t bs = rr / a.H;
+  const int s = (int)(bs % a.S);
+  const int b = (int)(bs / a.S);
+  constexpr size_t esz = sizeof(T);
+  char* xp = (char*)a.x + ((int64_t)b * a.xs_b + (int64_t)s * a.xs_s + (int64_t)h * a.xs_h) * esz;
+  const int i0 = part * EPT;          // first element of this thread in the low half
+
+  float lo[EPT], hi[EPT];
+  auto load8 = [&](const char* p, float* dst) {
+    if constexpr (EPT == 8) {
+      const u32x4 v = *(const u32x4*)p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { dst[2 * e] = E::lo(v[e]); dst[2 * e + 1] = E::hi(v[e]); }
+    } else {
+      const u32x2 v = *(const u32x2*)p;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) { dst[2 * e] = E::lo(v[e]); dst[2 * e + 1] = E::hi(v[e]); }
+    }
+  };
+  if (live) {
+    load8(xp + i0 * esz, lo);
+    load8(xp + (HALF + i0) * esz, hi);
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) { lo[e] = 0.f; hi[e] = 0.f; }
+  }
+
+  if (a.w) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
+#pragma unroll
+    for (int off = 1; off < TPR; off <<= 1) ss += __shfl_xor(ss, off);
+    const float r = rsqrtf(ss / (float)D + a.eps);
+    float wl[EPT], wh[EPT];
+    load8((const char*)a.w + i0 * esz, wl);
+    load8((const char*)a.w + (HALF + i0) * esz, wh);
+#pragma unroll
+    for (int e = 0; e < EPT; e += 2) {
+      uint32_t p = E::pack2(lo[e] * r, lo[e + 1] * r);            // x * rsqrt(...) -> dtype
+      p = E::pack2(wl[e] * E::lo(p), wl[e + 1] * E::hi(p));      // weight * x -> dtype
+      lo[e] = E::lo(p); lo[e + 1] = E::hi(p);
+      uint32_t q = E::pack2(hi[e] * r, hi[e + 1] * r);
+      q = E::pack2(wh[e] * E::lo(q), wh[e + 1] * E::hi(q));
+      hi[e] = E::lo(q); hi[e + 1] = E::hi(q);
+    }
+  }
+
+  const char* cp = (const char*)a.cos + ((int64_t)(a.cs_b ? b : 0) * a.cs_b + (int64_t)s * a.cs_s) * esz;
+  const char* sp = (const char*)a.sin + ((int64_t)(a.cs_b ? b : 0) * a.cs_b + (int64_t)s * a.cs_s) * esz;
+  float cl[EPT], ch[EPT], sl[EPT], sh[EPT];
+  load8(cp + i0 * esz, cl);
+  load8(cp + (HALF + i0) * esz, ch);
+  load8(sp + i0 * esz, sl);
+  load8(sp + (HALF + i0) * esz, sh);
+
+  uint32_t olo[EPT / 2], ohi[EPT / 2];
+#pragma unroll
+  for (int e = 0; e < EPT; e += 2) {
+    // low half: x*cos + (-x_hi)*sin ; high half: x_hi*cos + x_lo*sin
+    const uint32_t a1 = E::pack2(lo[e] * cl[e], lo[e + 1] * cl[e + 1]);
+    const uint32_t a2 = E::pack2(-hi[e] * sl[e], -hi[e + 1] * sl[e + 1]);
+    olo[e / 2] = E::pack2(E::lo(a1) + E::lo(a2), E::hi(a1) + E::hi(a2));
+    const uint32_t b1 = E::pack2(hi[e] * ch[e], hi[e + 1] * ch[e + 1]);
+    const uint32_t b2 = E::pack2(lo[e] * sh[e], lo[e + 1] * sh[e + 1]);
+    ohi[e / 2] = E::pack2(E::lo(b1) + E::lo(b2), E::hi(b1) + E::hi(b2));
+  }
+  if (!live) return;
+  if constexpr (EPT == 8) {
+    *(u32x4*)(xp + i0 * esz) = (u32x4){olo[0], olo[1], olo[2], olo[3]};
+    *(u32x4*)(xp + (HALF + i0) * esz) = (u32x4){ohi[0], ohi[1], ohi[2], ohi[3]};
+  } else {
+    *(u32x2*)(xp + i0 * esz) = (u32x2){olo[0], olo[1]};
+    *(u32x2*)(xp + (HALF + i0) * esz) = (u32x2){ohi[0], ohi[1]};
+  }
+}
+
+template <typename T>
+static void launch_rope(const RopeArgs& a, hipStream_t s) {
+  const int64_t threads = a.rows * 8;
+  const int grid = (int)((threads + 255) / 256);
+  if (a.D == 128) hipLaunchKernelGGL((rope_kernel<T, 128>), dim3(grid), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((rope_kernel<T, 64>), dim3(grid), dim3(256), 0, s, a);
+}
+
+}  // namespace da
+
+using namespace da;
+
+static int rope_one(void* x, const int64_t x_str[3], int H, int B, int S, int D,
+                    const void* cos, const void* sin, const int64_t cs_str[2], const void* w,
+                    float eps, int dtype, hipStream_t s) {
+  if (!x || !x_str || H < 1) return DA_ERR_INVALID_ARG;
+  if (!aligned16(x) || !strides8(x_str)) return DA_ERR_ALIGNMENT;
+  if (w && !aligned16(w)) return DA_ERR_ALIGNMENT;
+  RopeArgs a = {};
+  a.x = x; a.xs_b = x_str[0]; a.xs_s = x_str[1]; a.xs_h = x_str[2];
+  a.H = H; a.cos = cos; a.sin = sin; a.cs_b = cs_str[0]; a.cs_s = cs_str[1];
+  a.w = w; a.eps = eps; a.B = B; a.S = S; a.D = D;
+  a.rows = (int64_t)B * S * H;
+  if (a.rows * 8 / 256 > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
+  if (dtype == DA_BF16) launch_rope<__bf16>(a, s);
+  else launch_rope<_Float16>(a, s);
+  return DA_OK;
+}
+
+extern "C" int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
+                          void* k, const int64_t k_str[3], int Hkv,
+                          int B, int S, int D,
+                          const void* cos, const void* sin, const int64_t cs_str[2],
+                          const void* q_norm_w, const void* k_norm_w, float eps,
+                          int dtype, void* stream) {
+  if (dtype != DA_BF16 && dtype != DA_FP16) return DA_ERR_DTYPE;
+  if (D != 64 && D != 128) return DA_ERR_HEAD_DIM;
+  if (B < 1 || S < 0) return DA_ERR_INVALID_ARG;
+  if (S == 0) return DA_OK;
+  if (!cos || !sin || !cs_str || cs_str[0] < 0 || cs_str[1] < D) return DA_ERR_INVALID_ARG;
+  if (!aligned16(cos) || !aligned16(sin) || cs_str[0] % 8 || cs_str[1] % 8) return DA_ERR_ALIGNMENT;
+  hipStream_t s = (hipStream_t)stream;
+  (void)hipGetLastError();
+  int rc;
+  if (q && (rc = rope_one(q, q_str, Hq, B, S, D, cos, sin, cs_str, q_norm_w, eps, dtype, s)) != DA_OK)
+    return rc;
+  if (k && (rc = rope_one(k, k_str, Hkv, B, S, D, cos, sin, cs_str, k_norm_w, eps, dtype, s)) != DA_OK)
+    return rc;
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}

@@ -32,6 +32,7 @@ EXPORTS = (
     "da_qsparse_workspace_bytes",
     "da_qsparse_attn_fwd",
     "da_delta_add",
+    "da_rope_qk",
     "da_build_target",
 )
 
@@ -86,6 +87,9 @@ def lib() -> ctypes.CDLL:
     L.da_delta_add.restype = _i
     L.da_delta_add.argtypes = [_vp, _p3, _vp, _p3, _vp, _p3, _vp, _p3, _vp,
                                _i, _i, _i, _i, _i, _i, _i, _vp]
+    L.da_rope_qk.restype = _i
+    L.da_rope_qk.argtypes = [_vp, _p3, _i, _vp, _p3, _i, _i, _i, _i, _vp, _vp,
+                             ctypes.POINTER(ctypes.c_int64), _vp, _vp, _f, _i, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
     _lib = L

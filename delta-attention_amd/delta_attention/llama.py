@@ -212,10 +212,33 @@ class LlamaAttention(nn.Module):
 
     # -- projections and dispatch -----------------------------------------------
     def _qkv(self, hidden_states, hidden_shape):
+        """The reference's model-family hook (llama.py:826-830): projected q/k/v
+        as [b, h, s, d] views, before RoPE (torch ops)."""
         q = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         return q, k, v
+
+    def _qk_norm(self):
+        """(q_norm weight, k_norm weight, eps) applied before RoPE, or Nones."""
+        return None, None, 1e-6
+
+    def _qkv_rope(self, hidden_states, hidden_shape, cos, sin):
+        """Projections, then the fused prologue kernel (optional per-head q/k
+        RMSNorm + RoPE) in place on the [b, s, h, d] projection outputs; returns
+        [b, h, s, d] views, the layout the attention kernels read without copies."""
+        if hidden_states.dtype not in (torch.bfloat16, torch.float16):
+            # float32 models keep the reference's float32 RoPE (torch ops); the
+            # attention kernels then run in bf16 as delta_forward casts
+            q, k, v = self._qkv(hidden_states, hidden_shape)
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            return q, k, v
+        q = self.q_proj(hidden_states).view(hidden_shape)
+        k = self.k_proj(hidden_states).view(hidden_shape)
+        v = self.v_proj(hidden_states).view(hidden_shape)
+        qw, kw, eps = self._qk_norm()
+        ops.rope_qk(q, k, cos, sin, q_norm_w=qw, k_norm_w=kw, eps=eps)
+        return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
 
     def forward(self, hidden_states, position_embeddings, attention_mask=None,
                 past_key_value=None, cache_position=None, **kwargs):
@@ -223,9 +246,8 @@ class LlamaAttention(nn.Module):
         (llama.py:832-914); `window` routes to delta_forward."""
         input_shape = hidden_states.shape[:-1]
         hidden_shape = (*input_shape, -1, self.head_dim)
-        query_states, key_states, value_states = self._qkv(hidden_states, hidden_shape)
         cos, sin = position_embeddings
-        query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin)
+        query_states, key_states, value_states = self._qkv_rope(hidden_states, hidden_shape, cos, sin)
         if past_key_value is not None:
             key_states, value_states = past_key_value.update(
                 key_states, value_states, self.layer_idx,

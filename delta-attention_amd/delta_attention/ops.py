@@ -203,6 +203,46 @@ def delta_add(sparse: torch.Tensor, *, s_p: int, out: Optional[torch.Tensor] = N
 
 
 # ---------------------------------------------------------------------------
+# attention prologue: per-head RMSNorm (optional) + RoPE, in place
+
+def rope_qk(q: Optional[torch.Tensor], k: Optional[torch.Tensor], cos: torch.Tensor,
+            sin: torch.Tensor, *, q_norm_w: Optional[torch.Tensor] = None,
+            k_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6):
+    """In place on q [B,S,Hq,D] and k [B,S,Hkv,D] (projection-output layout, any
+    batch/seq/head strides): optional per-head RMSNorm with the given weights,
+    then rotary embedding with cos/sin [B or 1, S, D] (cast to q's dtype, as the
+    reference does). Returns (q, k)."""
+    x = q if q is not None else k
+    assert x is not None and x.dim() == 4
+    B, S, _, D = x.shape
+    dev = _on_gpu(*[t for t in (q, k) if t is not None])
+    if S == 0:
+        return q, k
+    cos = cos.to(device=dev, dtype=x.dtype)
+    sin = sin.to(device=dev, dtype=x.dtype)
+    if cos.dim() == 2:
+        cos, sin = cos.unsqueeze(0), sin.unsqueeze(0)
+    assert cos.shape[1:] == (S, D) and cos.shape[0] in (1, B) and sin.shape == cos.shape
+    cos, sin = cos.contiguous(), sin.contiguous()
+    for t in (q, k):
+        if t is not None:
+            assert t.shape[0] == B and t.shape[1] == S and t.shape[3] == D and t.dtype == x.dtype
+            assert t.stride(-1) == 1 and t.data_ptr() % 16 == 0, "rope_qk works in place on row-contiguous tensors"
+    ws = [None if w is None else w.to(device=dev, dtype=x.dtype).contiguous() for w in (q_norm_w, k_norm_w)]
+    cs = (ctypes.c_int64 * 2)(0 if cos.shape[0] == 1 else cos.stride(0), cos.stride(1))
+    with torch.cuda.device(dev):
+        rc = L.lib().da_rope_qk(
+            _ptr(q), None if q is None else L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+            0 if q is None else q.shape[2],
+            _ptr(k), None if k is None else L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+            0 if k is None else k.shape[2],
+            B, S, D, _ptr(cos), _ptr(sin), cs, _ptr(ws[0]), _ptr(ws[1]), float(eps),
+            _code(x), _stream(dev))
+    L.check(rc, "da_rope_qk")
+    return q, k
+
+
+# ---------------------------------------------------------------------------
 # the composed layer prefill (kernels 1 -> 2 -> 3)
 
 def anchor_layout(s: int, gamma: int) -> Tuple[int, int, int]:

@@ -132,6 +132,24 @@ int da_delta_add(const void* sparse, const int64_t sp_str[3],
                  const int64_t* anchors, int n_anchor, int gamma, int s_p,
                  int B, int H, int D, int dtype, void* stream);
 
+/*
+ * Attention prologue, in place: optional per-head RMSNorm (weights q_norm_w /
+ * k_norm_w of length D, NULL = no norm; Qwen3, delta_attention/qwen3.py:37-43 and
+ * llama.py:60-74) followed by rotary position embedding (rotate_half
+ * convention, delta_attention/llama.py:161-192) of q [B, S, Hq, D] (strides
+ * q_str = {batch, seq, head}) and k [B, S, Hkv, D] (k_str); either may be NULL.
+ * cos/sin are [Bc, S, D] tables in `dtype` with element strides
+ * cs_str = {batch (0 = shared), seq}. Each tensor op of the reference is
+ * rounded to `dtype` once, as torch does, so the RoPE result is bit-identical
+ * to the reference's ops on the same inputs.
+ */
+int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
+               void* k, const int64_t k_str[3], int Hkv,
+               int B, int S, int D,
+               const void* cos, const void* sin, const int64_t cs_str[2],
+               const void* q_norm_w, const void* k_norm_w, float eps,
+               int dtype, void* stream);
+
 /* Library identification: the gfx target the code objects were built for. */
 const char* da_build_target(void);
 

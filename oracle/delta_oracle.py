@@ -17,7 +17,8 @@ prefill (file:line cite the reference, singhh5050/delta-attention):
   round_bf16, *_bf16     the bf16 elementwise arithmetic of llama.py:740-751 and
                          stride.py:38-40 (fp32 op, one round-to-nearest-even)
   rope / rms_norm        llama.py:129-192 (rotate_half RoPE), llama.py:60-74 (RMSNorm),
-                         qwen3.py:37-43 (per-head q/k norm before RoPE)
+                         qwen3.py:37-43 (per-head q/k norm before RoPE); *_bf16
+                         variants round once per tensor op like the bf16 tensors
   visible_pairs          the algorithmic-work counts (pairs of the sparse pass,
                          sum(i+1) of the query-sparse pass)
 
@@ -294,6 +295,26 @@ def apply_rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     half = x.shape[-1] // 2
     rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
     return x * cos[None, None] + rot * sin[None, None]
+
+
+def mul_bf16(a, b) -> np.ndarray:
+    return round_bf16(np.asarray(a, np.float32) * np.asarray(b, np.float32))
+
+
+def apply_rope_bf16(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """apply_rope with the reference's bf16 tensors (llama.py:190-191): x, cos,
+    sin hold bf16 values; q*cos, rotate_half(q)*sin and their sum each round once."""
+    half = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+    return add_bf16(mul_bf16(x, cos), mul_bf16(rot, sin))
+
+
+def rms_norm_bf16(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """LlamaRMSNorm on bf16 input (llama.py:69-74): float32 normalisation, cast
+    to bf16, then the bf16 product with the bf16 weight."""
+    x32 = np.asarray(x, np.float32)
+    y = round_bf16(x32 / np.sqrt((x32 * x32).mean(axis=-1, keepdims=True) + np.float32(eps)))
+    return mul_bf16(weight, y)
 
 
 def rms_norm(x: np.ndarray, eps: float = 1e-6, weight: Optional[np.ndarray] = None) -> np.ndarray:

@@ -106,3 +106,23 @@ def test_delta_add_checks(lib):
     assert call(delta=0, dense=16, anchors=16, out=16) == L.DA_ERR_INVALID_ARG  # no aliasing
     assert call(delta=8) == L.DA_ERR_ALIGNMENT
     assert call(s_p=0) == L.DA_OK
+
+
+def test_rope_checks(lib):
+    s3 = _s3(128 * 8 * 128, 8 * 128, 128)
+    c2 = (ctypes.c_int64 * 2)
+
+    def call(q=16, D=128, dtype=L.DA_BF16, cos=16, cs=(0, 128), S=128, qs=s3, w=0):
+        return lib.da_rope_qk(ctypes.c_void_p(q), qs, 8, None, None, 0, 1, S, D,
+                              ctypes.c_void_p(cos), ctypes.c_void_p(16), c2(*cs),
+                              ctypes.c_void_p(w), None, 1e-6, dtype, None)
+
+    assert call(dtype=5) == L.DA_ERR_DTYPE
+    assert call(D=96) == L.DA_ERR_HEAD_DIM
+    assert call(cos=0) == L.DA_ERR_INVALID_ARG
+    assert call(cs=(0, 64)) == L.DA_ERR_INVALID_ARG          # table rows shorter than D
+    assert call(cos=24) == L.DA_ERR_ALIGNMENT
+    assert call(q=8) == L.DA_ERR_ALIGNMENT
+    assert call(w=8) == L.DA_ERR_ALIGNMENT
+    assert call(qs=_s3(128 * 8 * 128, 8 * 128, 100)) == L.DA_ERR_ALIGNMENT
+    assert call(S=0) == L.DA_OK

@@ -322,3 +322,25 @@ def test_rms_norm_matches_torch():
     x = np.random.default_rng(16).standard_normal((3, 5, 128)).astype(np.float32)
     ref = F.rms_norm(torch.from_numpy(x), (128,), eps=1e-6).numpy()
     np.testing.assert_allclose(O.rms_norm(x, 1e-6), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_bf16_prologue_ops_match_torch():
+    # the bf16 RoPE / RMSNorm restatements against torch's own bf16 tensor ops
+    rng = np.random.default_rng(17)
+    S, D = 40, 128
+    x = O.round_bf16(rng.standard_normal((2, 3, S, D)).astype(np.float32))
+    c32, s32 = O.rope_cos_sin(S, D, 500000.0)
+    c, s = O.round_bf16(c32), O.round_bf16(s32)
+    tx = torch.from_numpy(x).to(torch.bfloat16)
+    tc, ts = torch.from_numpy(c).to(torch.bfloat16), torch.from_numpy(s).to(torch.bfloat16)
+    h = D // 2
+    ref = (tx * tc) + (torch.cat((-tx[..., h:], tx[..., :h]), dim=-1) * ts)
+    np.testing.assert_array_equal(O.apply_rope_bf16(x, c, s), ref.float().numpy())
+    w = O.round_bf16(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    tw = torch.from_numpy(w).to(torch.bfloat16)
+    xf = tx.float()
+    tref = tw * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    got = O.rms_norm_bf16(x, w, 1e-6)
+    diff = np.abs(got - tref.float().numpy())
+    ulp = np.abs(tref.float().numpy()) * 2.0 ** -7
+    assert (diff <= ulp + 1e-30).all() and (diff == 0).mean() > 0.99
