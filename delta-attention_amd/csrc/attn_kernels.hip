@@ -5,12 +5,11 @@
 //                                    qsparse_merge_kernel, which also runs the
 //                                    delta epilogue.
 //
-// Tiling (one workgroup = 4 waves = 256 threads):
-//   * M tile: BM = 128 * RBW flattened (query row, head-in-group) pairs. The G
+// Tiling (one workgroup = 4 waves = 256 threads, two workgroups per CU):
+//   * M tile: BM = 128 flattened (query row, head-in-group) pairs. The G
 //     query heads that share one key/value head are packed into the same
 //     tile, so K/V tiles are read once per group (no repeat_kv copies).
-//   * Each wave owns RBW blocks of 32 flattened rows; every K/V fragment read
-//     from LDS feeds RBW MFMAs. Scores are formed transposed,
+//   * Each wave owns 32 flattened rows. Scores are formed transposed,
 //     S^T = K * Q^T, with v_mfma_f32_32x32x16 (A = 32 keys x 16 dims from LDS,
 //     B = Q^T fragment kept in registers). In the 32x32 accumulator layout a
 //     lane holds one query row (lane % 32) and 16 of its keys, so the softmax
@@ -29,6 +28,9 @@
 //   * Softmax: one FMA + exp2 per score, row sum by v_dot2 over the packed P.
 //     Lazy rescale: the running max only moves when a row's tile max exceeds
 //     it by more than 2^8, so most tiles skip the O rescale.
+//   * Per key tile, 32 MFMAs in one scheduling region keep the matrix pipe
+//     fed: the exponentials of tile t run under the score MFMAs of tile t+1,
+//     then the PV MFMAs of tile t follow with their V reads running ahead.
 #include <type_traits>
 
 #include "device_common.h"
@@ -36,32 +38,27 @@
 
 namespace da {
 
-// Row blocks of 32 query rows per wave (each K/V fragment read from LDS feeds
-// RBW MFMAs), LDS stages and DMA prefetch distance (in key tiles).
-#ifndef DA_ROW_BLOCKS
-#define DA_ROW_BLOCKS 1
+// Build options for controlled experiments (defaults measured fastest):
+// DA_SCHED=1 pins the interleave of MFMAs, LDS fragment reads and VALU work
+// in the key-tile loop with scheduling-group barriers (0: compiler order,
+// 1.5-2 % faster). DA_WAVES=8 makes one 8-wave workgroup per CU share every
+// K/V tile (half the DMA per MFMA); 4-wave workgroups, two per CU, measured
+// faster: the two waves on a SIMD then belong to different workgroups and
+// are not held at the same barrier.
+#ifndef DA_SCHED
+#define DA_SCHED 0
 #endif
-#ifndef DA_BLOCK_N
-#define DA_BLOCK_N 64
+#ifndef DA_WAVES
+#define DA_WAVES 4
 #endif
-#ifndef DA_WAVES_PER_EU
-#define DA_WAVES_PER_EU (DA_ROW_BLOCKS == 1 ? 2 : 1)
-#endif
-// Software pipelining of the score product (S(t+1) formed during the softmax of
-// tile t) doubles the live score registers; it is used with one row block.
-#ifndef DA_PIPELINE
-#define DA_PIPELINE (DA_ROW_BLOCKS == 1)
-#endif
-constexpr int RBW = DA_ROW_BLOCKS;
-constexpr int BM = 128 * RBW;        // flattened (row, head) pairs per workgroup
-constexpr int BN = DA_BLOCK_N;       // keys per tile (32 or 64)
+constexpr int NWAVE = DA_WAVES;
+static_assert(NWAVE == 4 || NWAVE == 8, "4 or 8 waves per workgroup");
+constexpr int NTHR = 64 * NWAVE;
+constexpr int BM = 32 * NWAVE;       // flattened (row, head) pairs per workgroup
+constexpr int BN = 64;               // keys per tile
 constexpr int NH = BN / 32;          // 32-key halves per tile
-constexpr int NTHR = 256;
-constexpr int NSTAGE = RBW == 1 ? 2 : 4;
-constexpr int PREF = NSTAGE - 1;     // tiles in flight ahead of the K tile in use
-constexpr int WAVES_PER_EU = DA_WAVES_PER_EU;
-constexpr bool PIPE = DA_PIPELINE;
-static_assert(BN == 32 || BN == 64, "key tile is 32 or 64 keys");
+constexpr int MTHR = 256;            // threads of the split-merge kernel
+constexpr int NSTAGE = 2;            // LDS stages for K and for V
 constexpr float RESCALE_THRESH = 8.0f;   // log2 domain
 constexpr float NEG_BIG = -1.0e30f;      // finite "minus infinity" for the running max
 
@@ -121,35 +118,31 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Wait until at most g groups of N DMA loads are outstanding (g <= 4).
-template <int N>
-__device__ __forceinline__ void wait_dma_groups(int g) {
-  switch (g) {
-    case 0: wait_vmcnt<0>(); break;
-    case 1: wait_vmcnt<N>(); break;
-    case 2: wait_vmcnt<2 * N>(); break;
-    case 3: wait_vmcnt<3 * N>(); break;
-    default: wait_vmcnt<4 * N>(); break;
-  }
-}
-static_assert(2 * (NSTAGE - 2) <= 4, "wait_dma_groups covers at most 4 groups");
+// Scheduling-group barrier masks (LLVM AMDGPU IGroupLP).
+enum : int { SG_VALU = 0x2, SG_MFMA = 0x8, SG_DS_READ = 0x100 };
 
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   using TL = Tile<D>;
   constexpr int DCH = TL::DCH;
   constexpr int RB = TL::RB;
   constexpr int NDS = D / 16;                // MFMA k-steps of K.Q^T
   constexpr int NDT = D / 32;                // 32-row tiles of O^T
+  constexpr int NQK = NDS * NH;              // MFMAs per score tile
+  [[maybe_unused]] constexpr int NPV = 2 * NH * NDT;   // MFMAs per PV tile
   constexpr int NDMA = TL::BYTES / (NTHR * 16);   // 16-byte DMA chunks per thread per K (or V) tile
   using E = Elt<T>;
 
   // [stage][K, V][tile bytes]
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE][2][TL::BYTES];
-  __shared__ int red[4][4];
+  __shared__ int red[4][NWAVE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  // Kept as a vector value: with a readfirstlane-uniform wave index the
+  // compiler's wait-count pass treats the DMA's LDS destination as aliasing
+  // the fragment reads and inserts a vmcnt(0) wait right after each DMA
+  // issue. The loop orders DMA and reads itself (wait + barrier per tile).
   const int wave = tid >> 6;
   const int ln = lane & 31;
   const int lg = lane >> 5;
@@ -172,35 +165,25 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
   const int b = bh / a.Hkv;
   const int G = a.G;
 
-  // ---- this lane's query rows: row block rb is flattened row
-  //      mt * BM + wave * 32 * RBW + 32 * rb + ln ----
-  bool valid[RBW];
-  int qrow[RBW], lo[RBW], hi[RBW], hrow[RBW];
-  int v_hmin = 0x7fffffff, v_hmax = -1, v_lmin = 0x7fffffff, v_lmax = (int)0x80000000;
-#pragma unroll
-  for (int rb = 0; rb < RBW; ++rb) {
-    const int mflat = mt * BM + wave * 32 * RBW + 32 * rb + ln;
-    valid[rb] = mflat < a.n_rows * G;
-    const int i = valid[rb] ? mflat / G : 0;
-    hrow[rb] = hk * G + (valid[rb] ? mflat % G : 0);
-    if (MODE == MODE_SPARSE) {
-      qrow[rb] = i;
-      hi[rb] = valid[rb] ? i : -1;
-      lo[rb] = (i / a.q_block) * a.q_block + a.q_block - a.window;
-    } else {
-      qrow[rb] = a.q_rows ? (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1)) : i;
-      int64_t lim = a.row_last[(int64_t)b * a.rl_b + i];
-      if (lim > a.n_kv - 1) lim = a.n_kv - 1;
-      hi[rb] = valid[rb] ? (int)(lim < -1 ? -1 : lim) : -1;
-      lo[rb] = 0;
-    }
-    if (valid[rb]) {
-      v_hmin = min(v_hmin, hi[rb]);
-      v_hmax = max(v_hmax, hi[rb]);
-      v_lmin = min(v_lmin, lo[rb]);
-      v_lmax = max(v_lmax, lo[rb]);
-    }
+  // ---- this lane's query row: flattened row mt * BM + 32 * wave + ln ----
+  const int mflat = mt * BM + wave * 32 + ln;
+  const bool valid = mflat < a.n_rows * G;
+  const int irow = valid ? mflat / G : 0;
+  const int hrow = hk * G + (valid ? mflat % G : 0);
+  int qrow, lo, hi;
+  if (MODE == MODE_SPARSE) {
+    qrow = irow;
+    hi = valid ? irow : -1;
+    lo = (irow / a.q_block) * a.q_block + a.q_block - a.window;
+  } else {
+    qrow = a.q_rows ? (int)min(max(a.q_rows[irow], (int64_t)0), (int64_t)(a.n_q - 1)) : irow;
+    int64_t lim = a.row_last[(int64_t)b * a.rl_b + irow];
+    if (lim > a.n_kv - 1) lim = a.n_kv - 1;
+    hi = valid ? (int)(lim < -1 ? -1 : lim) : -1;
+    lo = 0;
   }
+  int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
+  int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
   const int sink = (MODE == MODE_SPARSE) ? a.sink : 0;
 
   // ---- tile-wide bounds (valid rows only) ----
@@ -218,10 +201,14 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
     red[3][wave] = v_lmax;
   }
   __syncthreads();
-  const int hi_min = min(min(red[0][0], red[0][1]), min(red[0][2], red[0][3]));
-  const int hi_max = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
-  const int lo_min = min(min(red[2][0], red[2][1]), min(red[2][2], red[2][3]));
-  const int lo_max = max(max(red[3][0], red[3][1]), max(red[3][2], red[3][3]));
+  int hi_min = red[0][0], hi_max = red[1][0], lo_min = red[2][0], lo_max = red[3][0];
+#pragma unroll
+  for (int i = 1; i < NWAVE; ++i) {
+    hi_min = min(hi_min, red[0][i]);
+    hi_max = max(hi_max, red[1][i]);
+    lo_min = min(lo_min, red[2][i]);
+    lo_max = max(lo_max, red[3][i]);
+  }
 
   // ---- key tiles to visit ----
   int n_first, n_second, second_t0;
@@ -246,51 +233,55 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
   constexpr size_t esz = sizeof(T);
   const char* kbase = (const char*)a.k + ((int64_t)b * a.ks_b + (int64_t)hk * a.ks_h) * esz;
   const char* vbase = (const char*)a.v + ((int64_t)b * a.vs_b + (int64_t)hk * a.vs_h) * esz;
-  const int64_t krow_b = a.ks_s * (int64_t)esz;
-  const int64_t vrow_b = a.vs_s * (int64_t)esz;
+  // row strides in bytes are below 2^24 (checked on the host), so tile
+  // offsets are 32 x 32 -> 64-bit products
+  const uint32_t krow_b = (uint32_t)(a.ks_s * (int64_t)esz);
+  const uint32_t vrow_b = (uint32_t)(a.vs_s * (int64_t)esz);
+  const uint64_t kend = (uint64_t)kbase + (uint64_t)(uint32_t)a.n_kv * krow_b;
+  const uint64_t vend = (uint64_t)vbase + (uint64_t)(uint32_t)a.n_kv * vrow_b;
 
   // ---- Q^T fragments (registers for the whole kernel) ----
-  u32x4 qf[RBW][NDS];
-#pragma unroll
-  for (int rb = 0; rb < RBW; ++rb) {
+  u32x4 qf[NDS];
+  {
     const char* qp = (const char*)a.q +
-                     ((int64_t)b * a.qs_b + (int64_t)hrow[rb] * a.qs_h + (int64_t)qrow[rb] * a.qs_s) * esz;
+                     ((int64_t)b * a.qs_b + (int64_t)hrow * a.qs_h + (int64_t)qrow * a.qs_s) * esz;
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds)
-      qf[rb][ds] = valid[rb] ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
+      qf[ds] = valid ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
   }
 
   // ---- DMA source offsets: wave `wave`, chunk c fills LDS slots
-  //      (c * 4 + wave) * 64 + lane of the tile; slot -> (row, swizzled chunk) ----
+  //      (c * NWAVE + wave) * 64 + lane of the tile; slot -> (row, swizzled chunk) ----
   uint32_t koff[NDMA], voff[NDMA];
 #pragma unroll
   for (int c = 0; c < NDMA; ++c) {
-    const int slot = (c * 4 + wave) * 64 + lane;
+    const int slot = (c * NWAVE + wave) * 64 + lane;
     const int row = slot / DCH, pc = slot % DCH;
-    koff[c] = (uint32_t)(row * krow_b) + (uint32_t)((pc ^ TL::kswz(row)) * 16);
-    voff[c] = (uint32_t)(row * vrow_b) + (uint32_t)((pc ^ TL::vswz(row)) * 16);
+    koff[c] = (uint32_t)row * krow_b + (uint32_t)((pc ^ TL::kswz(row)) * 16);
+    voff[c] = (uint32_t)row * vrow_b + (uint32_t)((pc ^ TL::vswz(row)) * 16);
   }
   auto tile_n0 = [&](int t) -> int {
     return (t < n_first ? t : second_t0 + (t - n_first)) * BN;
   };
-  // DMA of key tile t into LDS stage `slot` (K) / (V)
+  // DMA of key tile t into LDS stage `slot` (K) / (V); the buffer covers the
+  // rows from the tile start to the last key (n0 <= hi_max < n_kv), so the
+  // hardware range check zero-fills keys past the end
+  auto tile_rsrc = [&](const char* base, uint64_t end, uint32_t row_b, int t) {
+    const uint64_t p = (uint64_t)base + (uint64_t)(uint32_t)tile_n0(t) * row_b;
+    const uint64_t rem = end - p;
+    return make_rsrc((const void*)p, (rem >> 32) ? 0xffffffffu : (uint32_t)rem);
+  };
   auto issue_k = [&](int t, int slot) {
-    const int n0 = tile_n0(t);
-    const int64_t kb64 = (int64_t)(a.n_kv - n0) * krow_b;
-    const __amdgpu_buffer_rsrc_t rk =
-        make_rsrc(kbase + n0 * krow_b, kb64 > 0xffffffffLL ? 0xffffffffu : (uint32_t)kb64);
+    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase, kend, krow_b, t);
 #pragma unroll
     for (int c = 0; c < NDMA; ++c)
-      dma16(rk, (DA_LDS void*)(&smem[slot][0][(c * 4 + wave) * 1024]), koff[c]);
+      dma16(rk, (DA_LDS void*)(&smem[slot][0][(c * NWAVE + wave) * 1024]), koff[c]);
   };
   auto issue_v = [&](int t, int slot) {
-    const int n0 = tile_n0(t);
-    const int64_t vb64 = (int64_t)(a.n_kv - n0) * vrow_b;
-    const __amdgpu_buffer_rsrc_t rv =
-        make_rsrc(vbase + n0 * vrow_b, vb64 > 0xffffffffLL ? 0xffffffffu : (uint32_t)vb64);
+    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase, vend, vrow_b, t);
 #pragma unroll
     for (int c = 0; c < NDMA; ++c)
-      dma16(rv, (DA_LDS void*)(&smem[slot][1][(c * 4 + wave) * 1024]), voff[c]);
+      dma16(rv, (DA_LDS void*)(&smem[slot][1][(c * NWAVE + wave) * 1024]), voff[c]);
   };
 
   // ---- LDS read offsets ----
@@ -314,158 +305,161 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
     }
   }
 
-  f32x16 acc[RBW][NDT];
+  f32x16 acc[NDT];
 #pragma unroll
-  for (int rb = 0; rb < RBW; ++rb)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[rb][dt][j] = 0.f;
-  float m_i[RBW], l_i[RBW];
-#pragma unroll
-  for (int rb = 0; rb < RBW; ++rb) { m_i[rb] = NEG_BIG; l_i[rb] = 0.f; }
+    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+  float m_i = NEG_BIG, l_i = 0.f;
   const float c2 = a.scale_log2;
+  const DA_LDS char* lds0 = (const DA_LDS char*)&smem[0][0][0];
 
-  // S^T = K(stage) Q^T: x[rb][hf] holds keys 32 hf .. 32 hf + 31 of the tile, raw
-  auto qk = [&](int stage, f32x16 (&x)[RBW][NH]) {
-    const DA_LDS char* ks = (const DA_LDS char*)&smem[0][0][0] + stage * (2 * TL::BYTES);
+  // S^T = K(stage) Q^T into x (raw scores): x[hf] holds keys 32 hf .. 32 hf + 31
+  // of the tile. MFMA q uses k-step q / NH of half q % NH, so consecutive
+  // MFMAs alternate between the two accumulators.
+  auto qk = [&](int stage, f32x16 (&x)[NH]) {
+    const DA_LDS char* ks = lds0 + stage * (2 * TL::BYTES);
 #pragma unroll
-    for (int rb = 0; rb < RBW; ++rb)
+    for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-      for (int hf = 0; hf < NH; ++hf)
+      for (int j = 0; j < 16; ++j) x[hf][j] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) x[rb][hf][j] = 0.f;
-#pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) {
-#pragma unroll
-      for (int hf = 0; hf < NH; ++hf) {
-        const u32x4 ka = *(const DA_LDS u32x4*)(ks + kread[ds] + 32 * hf * RB);
-#pragma unroll
-        for (int rb = 0; rb < RBW; ++rb) x[rb][hf] = E::mfma(ka, qf[rb][ds], x[rb][hf]);
-      }
+    for (int q = 0; q < NQK; ++q) {
+      const int ds = q / NH, hf = q % NH;
+      const u32x4 ka = *(const DA_LDS u32x4*)(ks + kread[ds] + 32 * hf * RB);
+      x[hf] = E::mfma(ka, qf[ds], x[hf]);
     }
   };
-
-  // Loop over key tiles; K(u) and V(u) live in LDS stage u % NSTAGE and are
-  // loaded PREF tiles ahead. Pipelined (PIPE): at the top of step t, S(t) is in
-  // registers, V(t) and K(t+1) are resident, and step t issues K(t+1+PREF) and
-  // V(t+PREF), forms S(t+1) while the softmax of tile t runs, then O += V(t) P(t).
-  // Otherwise step t issues K/V(t+PREF), forms S(t), softmax, O += V(t) P(t).
-  // Every stage written in step t was last read in step t-1, before its
-  // closing barrier.
-  auto step = [&](int t, auto last_tag, f32x16 (&cur)[RBW][NH], f32x16 (&nxt)[RBW][NH]) {
-    constexpr bool LAST = decltype(last_tag)::value;   // t == nt - 1
-    const int P = t % NSTAGE;
-    if (PIPE) {
-      if (t + 1 + PREF < nt) issue_k(t + 1 + PREF, (P + 1 + PREF) % NSTAGE);
-    } else {
-      if (t + PREF < nt) issue_k(t + PREF, (P + PREF) % NSTAGE);
-    }
-    if (t + PREF < nt) issue_v(t + PREF, (P + PREF) % NSTAGE);
-    if (!PIPE) qk(P, cur);
+  // mask of tile t: element j of half hf is key n0 + 32 hf + 16 (j / 8) + 8 lg + j % 8
+  auto mask = [&](int t, f32x16 (&x)[NH]) {
     const int n0 = tile_n0(t);
     const int n1 = n0 + BN - 1;
     const bool full = (n1 <= hi_min) && (n1 < a.n_kv) && (n1 < sink || n0 >= lo_max);
     if (!full) {
-      // key of element j of half hf: n0 + 32 hf + 16 (j / 8) + 8 lg + j % 8
-#pragma unroll
-      for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-        for (int hf = 0; hf < NH; ++hf)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int key = n0 + 32 * hf + 16 * (j >> 3) + 8 * lg + (j & 7);
-            const bool vis = key <= hi[rb] && (key < sink || key >= lo[rb]);
-            cur[rb][hf][j] = vis ? cur[rb][hf][j] : -INFINITY;
-          }
-    }
-    float alpha[RBW];
-    bool up = false;
-#pragma unroll
-    for (int rb = 0; rb < RBW; ++rb) {
-      float mx = cur[rb][0][0];
 #pragma unroll
       for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) mx = __builtin_fmaxf(mx, cur[rb][hf][j]);
-      mx = max32(mx) * c2;          // scaling by c2 > 0 keeps the max
-      const bool u = __any(mx > m_i[rb] + RESCALE_THRESH);
-      const float m_new = u ? fmaxf(m_i[rb], mx) : m_i[rb];
-      alpha[rb] = fast_exp2(m_i[rb] - m_new);
-      m_i[rb] = m_new;
-      l_i[rb] *= alpha[rb];
-      up = up || u;
+        for (int j = 0; j < 16; ++j) {
+          const int key = n0 + 32 * hf + 16 * (j >> 3) + 8 * lg + (j & 7);
+          const bool vis = key <= hi && (key < sink || key >= lo);
+          x[hf][j] = vis ? x[hf][j] : -INFINITY;
+        }
     }
-    // p = 2^(c2 s - m), packed to the element type; the row sum is taken over
-    // the packed values (the same P the PV product uses)
-    uint32_t pk[RBW][8 * NH];
+  };
+  // scaled row max of a score tile: four independent chains, then one
+  // permlane32 swap (lanes l and l + 32 hold the two key groups of a row)
+  auto rowmax = [&](const f32x16 (&x)[NH]) -> float {
+    float p[4];
 #pragma unroll
-    for (int rb = 0; rb < RBW; ++rb) {
-      const float nm = -m_i[rb];
+    for (int c = 0; c < 4; ++c) {
+      const int hf = c >> 1, j0 = 8 * (c & 1);
+      float m = x[hf][j0];
 #pragma unroll
-      for (int hf = 0; hf < NH; ++hf)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          pk[rb][8 * hf + j] = E::pack2(fast_exp2(fmaf(cur[rb][hf][2 * j], c2, nm)),
-                                        fast_exp2(fmaf(cur[rb][hf][2 * j + 1], c2, nm)));
-#pragma unroll
-      for (int j = 0; j < 8 * NH; ++j) l_i[rb] = E::add_pair(pk[rb][j], l_i[rb]);
+      for (int j = 1; j < 8; ++j) m = __builtin_fmaxf(m, x[hf][j0 + j]);
+      p[c] = m;
     }
+    const float mx = __builtin_fmaxf(__builtin_fmaxf(p[0], p[1]), __builtin_fmaxf(p[2], p[3]));
+    return max32(mx) * c2;          // scaling by c2 > 0 keeps the max
+  };
+  // lazy online-softmax update with the scaled tile max: the running max
+  // moves (and O, l are rescaled) only when some row's tile max exceeds it by
+  // more than 2^RESCALE_THRESH
+  auto update = [&](float mx) {
+    if (__any(mx > m_i + RESCALE_THRESH)) {
+      const float m_new = fmaxf(m_i, mx);
+      const float alpha = fast_exp2(m_i - m_new);
+      m_i = m_new;
+      l_i *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
+    }
+  };
 
-    // no branch around it, so that these MFMAs share a scheduling region with
-    // the exponentials above; the last step is a separate instantiation
-    if (PIPE && !LAST) qk((P + 1) % NSTAGE, nxt);
+  // Step t. On entry: S(t) (masked) is in `cur` and the running max covers it;
+  // K(t+1) and V(t) are resident in LDS stages (t+1) & 1 and t & 1.
+  //   DMA: K(t+2) -> stage t & 1 (K(t) was read in step t-1), V(t+1) -> stage
+  //        (t+1) & 1 (V(t-1) was read in step t-1).
+  //   phase A: P(t) = 2^(c2 S(t) - m) packed, l += rowsum(P(t)), interleaved
+  //            with the score MFMAs of S(t+1) = K(t+1) Q^T.
+  //   phase B: O^T += V(t)^T P(t)^T.
+  //   Both phases are one basic block, so that the exponentials stay under
+  //   the score MFMAs instead of sinking to their use in phase B.
+  //   Then S(t+1) is masked (boundary tiles only), its max taken (overlapping
+  //   the PV MFMAs still in the pipe), the running max moved if needed; wait
+  //   for the DMA, barrier.
+  auto step = [&](int t, auto last_tag, f32x16 (&cur)[NH], f32x16 (&nxt)[NH]) {
+    constexpr bool LAST = decltype(last_tag)::value;   // t == nt - 1
+    const int P = t & 1;
+    if (t + 2 < nt) issue_k(t + 2, P);
+    if (t + 1 < nt) issue_v(t + 1, P ^ 1);
 
-    if (up) {
+    uint32_t pk[8 * NH];
+    const float nm = -m_i;
 #pragma unroll
-      for (int rb = 0; rb < RBW; ++rb)
+    for (int hf = 0; hf < NH; ++hf)
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+      for (int j = 0; j < 8; ++j)
+        pk[8 * hf + j] = E::pack2(fast_exp2(fmaf(cur[hf][2 * j], c2, nm)),
+                                  fast_exp2(fmaf(cur[hf][2 * j + 1], c2, nm)));
 #pragma unroll
-          for (int j = 0; j < 16; ++j) acc[rb][dt][j] *= alpha[rb];
-    }
-    // O^T += V^T * P^T, 16 keys per step
-    const DA_LDS char* vs = (const DA_LDS char*)&smem[0][1][0] + P * (2 * TL::BYTES);
+    for (int j = 0; j < 8 * NH; ++j) l_i = E::add_pair(pk[j], l_i);
+    if (!LAST) qk(P ^ 1, nxt);
+
+    const DA_LDS char* vs = lds0 + TL::BYTES + P * (2 * TL::BYTES);
 #pragma unroll
     for (int kk = 0; kk < 2 * NH; ++kk) {
+      const u32x4 pf = {pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]};
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
         const u32x2 v0 = read_tr16(vs + vread[dt] + (16 * kk) * RB);
         const u32x2 v1 = read_tr16(vs + vread[dt] + (16 * kk + 4) * RB);
         const u32x4 va = {v0[0], v0[1], v1[0], v1[1]};
-#pragma unroll
-        for (int rb = 0; rb < RBW; ++rb) {
-          const u32x4 pf = {pk[rb][4 * kk], pk[rb][4 * kk + 1], pk[rb][4 * kk + 2], pk[rb][4 * kk + 3]};
-          acc[rb][dt] = E::mfma(va, pf, acc[rb][dt]);
-        }
+        acc[dt] = E::mfma(va, pf, acc[dt]);
       }
     }
-    // The tiles the next step reads must have landed: K(t+2) (pipelined) or
-    // K(t+1), and V(t+1). Issued after them (and so allowed to stay in
-    // flight): K(u) for t+3 <= u <= t+1+PREF (pipelined) or t+2 <= u <= t+PREF,
-    // and V(u) for t+2 <= u <= t+PREF, those with u < nt, NDMA loads each.
-    const int younger = max(0, min(PREF - 1, nt - t - (PIPE ? 3 : 2))) +
-                        max(0, min(PREF - 1, nt - t - 2));
-    wait_dma_groups<NDMA>(younger);
-    __syncthreads();
+#if DA_SCHED
+    if (!LAST) {
+      // phase A: K reads run 3 MFMAs ahead, ~6 of the 96 softmax VALU ops
+      // under each score MFMA
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 3, 0);
+#pragma unroll
+      for (int q = 0; q < NQK; ++q) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        if (q + 3 < NQK) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_VALU, 6, 0);
+      }
+    }
+    // phase B: V reads run 2 MFMAs ahead (2 transposed reads per MFMA)
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 0);
+#pragma unroll
+    for (int q = 0; q < NPV; ++q) {
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      if (q + 2 < NPV) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+    }
+#endif
+    if (!LAST) {
+      mask(t + 1, nxt);
+      update(rowmax(nxt));
+      // K(t+2) and V(t+1) must have landed (nothing younger is in flight)
+      wait_vmcnt<0>();
+      __syncthreads();
+    }
   };
 
-  f32x16 sa[RBW][NH], sb[RBW][NH];
+  f32x16 sa[NH], sb[NH];
   if (nt > 0) {
-    // prologue: K(0..PREF) (pipelined) or K(0..PREF-1), and V(0..PREF-1)
+    // prologue: K(0), V(0), K(1); S(0) and its running max
     issue_k(0, 0);
     issue_v(0, 0);
-#pragma unroll
-    for (int u = 1; u <= PREF; ++u) {
-      if (u < nt && (PIPE || u < PREF)) issue_k(u, u % NSTAGE);
-      if (u < PREF && u < nt) issue_v(u, u % NSTAGE);
-    }
+    if (nt > 1) issue_k(1, 1);
     wait_vmcnt<0>();
     __syncthreads();
-    if (PIPE) {
-      qk(0, sa);
-      __syncthreads();   // every wave is done with K stage 0 before it is refilled
-    }
+    qk(0, sa);
+    mask(0, sa);
+    update(rowmax(sa));
+    __syncthreads();   // every wave is done with K stage 0 before it is refilled
   }
   using NotLast = std::integral_constant<bool, false>;
   using Last = std::integral_constant<bool, true>;
@@ -482,46 +476,43 @@ __global__ __launch_bounds__(NTHR, WAVES_PER_EU) void attn_fwd_kernel(AttnArgs a
   }
 
   // ---- epilogue ----
+  const float l_tot = sum32(l_i);
+  if (MODE == MODE_SPARSE) {
+    if (!valid) return;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
+                             (int64_t)qrow * a.os_s) * esz;
 #pragma unroll
-  for (int rb = 0; rb < RBW; ++rb) {
-    const float l_tot = sum32(l_i[rb]);
-    if (MODE == MODE_SPARSE) {
-      if (!valid[rb]) continue;
-      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-      char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow[rb] * a.os_h +
-                               (int64_t)qrow[rb] * a.os_s) * esz;
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq) {
-          const int d = 32 * dt + 8 * jq + 4 * lg;
-          u32x2 pkd;
-          pkd[0] = E::pack2(acc[rb][dt][4 * jq + 0] * inv, acc[rb][dt][4 * jq + 1] * inv);
-          pkd[1] = E::pack2(acc[rb][dt][4 * jq + 2] * inv, acc[rb][dt][4 * jq + 3] * inv);
-          *(u32x2*)(op + d * esz) = pkd;
-        }
-    } else {
-      const int r = wave * 32 * RBW + 32 * rb + ln;
-      float* po = a.part_o + ((int64_t)w * BM + r) * D;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq) {
-          const int d = 32 * dt + 8 * jq + 4 * lg;
-          *(f32x4*)(po + d) = (f32x4){acc[rb][dt][4 * jq + 0], acc[rb][dt][4 * jq + 1],
-                                       acc[rb][dt][4 * jq + 2], acc[rb][dt][4 * jq + 3]};
-        }
-      if (lg == 0) {
-        a.part_ml[(int64_t)w * 2 * BM + r] = m_i[rb];
-        a.part_ml[(int64_t)w * 2 * BM + BM + r] = l_tot;
+      for (int jq = 0; jq < 4; ++jq) {
+        const int d = 32 * dt + 8 * jq + 4 * lg;
+        u32x2 pkd;
+        pkd[0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
+        pkd[1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+        *(u32x2*)(op + d * esz) = pkd;
       }
+  } else {
+    const int r = wave * 32 + ln;
+    float* po = a.part_o + ((int64_t)w * BM + r) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const int d = 32 * dt + 8 * jq + 4 * lg;
+        *(f32x4*)(po + d) = (f32x4){acc[dt][4 * jq + 0], acc[dt][4 * jq + 1],
+                                     acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]};
+      }
+    if (lg == 0) {
+      a.part_ml[(int64_t)w * 2 * BM + r] = m_i;
+      a.part_ml[(int64_t)w * 2 * BM + BM + r] = l_tot;
     }
   }
 }
 
 // ---------------------------------------------------------------------------
 // Split-KV merge + epilogue of kernel (2). One workgroup per (b, kv head,
-// m tile); 256 threads cover BM rows x D/8 column chunks.
+// m tile); MTHR threads cover BM rows x D/8 column chunks.
 struct MergeArgs {
   const int64_t* q_rows;
   const int64_t* row_last;
@@ -537,7 +528,7 @@ struct MergeArgs {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(NTHR) void qsparse_merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   using E = Elt<T>;
   constexpr int CPR = D / 8;   // 8-column chunks per row
   __shared__ int s_hmax[4];
@@ -567,7 +558,7 @@ __global__ __launch_bounds__(NTHR) void qsparse_merge_kernel(MergeArgs a) {
   const int nsv = hi_max >= 0 ? hi_max / a.chunk + 1 : 0;
 
   const size_t esz = sizeof(T);
-  for (int task = tid; task < BM * CPR; task += NTHR) {
+  for (int task = tid; task < BM * CPR; task += MTHR) {
     const int r = task / CPR;
     const int c = task % CPR;
     const int mflat = mt * BM + r;
@@ -673,7 +664,12 @@ static void dispatch_attn(const AttnArgs& a, int D, int dtype, hipStream_t s) {
 
 template <typename T, int D>
 static void launch_merge(const MergeArgs& m, int n_tiles, hipStream_t s) {
-  hipLaunchKernelGGL((qsparse_merge_kernel<T, D>), dim3(n_tiles), dim3(NTHR), 0, s, m);
+  hipLaunchKernelGGL((qsparse_merge_kernel<T, D>), dim3(n_tiles), dim3(MTHR), 0, s, m);
+}
+
+// Key/value row strides (elements) in [0, 2^23): row byte strides below 2^24.
+static bool kv_rows_ok(const int64_t k_str[3], const int64_t v_str[3]) {
+  return k_str[2] >= 0 && k_str[2] < (1 << 23) && v_str[2] >= 0 && v_str[2] < (1 << 23);
 }
 
 }  // namespace da
@@ -695,6 +691,7 @@ extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, v
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
       !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
     return DA_ERR_ALIGNMENT;
+  if (!kv_rows_ok(k_str, v_str)) return DA_ERR_INVALID_ARG;
   AttnArgs a = {};
   a.q = q; a.k = k; a.v = v; a.o = out;
   a.qs_b = q_str[0]; a.qs_h = q_str[1]; a.qs_s = q_str[2];
@@ -744,6 +741,7 @@ extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) ||
       !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
     return DA_ERR_ALIGNMENT;
+  if (!kv_rows_ok(k_str, v_str)) return DA_ERR_INVALID_ARG;
   const QsparsePlan p = plan_qsparse(B, Hq, Hkv, n, Skv, D);
   if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
