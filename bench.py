@@ -268,23 +268,26 @@ def main():
     cut_n, s_p, n_anchor = ops.anchor_layout(S, a.gamma)
     idx = ops.selected_rows(S, a.gamma, str(dev))
     n_sel = idx.numel()
+    rows = ops.fused_delta_rows(H, Hkv)
+    assert rows and rows % a.gamma == 0 and s_p > 0, "this workload runs the fused epilogue"
     out = torch.empty(B, S, H, D, device=dev, dtype=torch.bfloat16)
-    delta = torch.empty(B, n_anchor, H, D, device=dev, dtype=torch.bfloat16)
+    dense_sel = torch.empty(B, n_anchor, H, D, device=dev, dtype=torch.bfloat16)
     ws = ops.qsparse_workspace(B, H, Hkv, n_sel, S, D, dev)
 
+    # one layer prefill: kernel (2) writes the dense tail rows into the output
+    # and the dense anchor rows aside, then kernel (1) runs with kernel (3)
+    # (the delta broadcast-add) fused into its epilogue
     def step(ev=None):
         if ev is not None:
             ev[0].record()
-        ops.sparse_attention(q, k, v, window=a.window, sink=a.sink, sm_scale=scale, out=out)
+        ops.qsparse_attention(q, k, v, idx, scale, q_rows=idx, epi=L.DA_EPI_DENSE, out=out,
+                              n_anchor=n_anchor, delta=dense_sel, workspace=ws)
         if ev is not None:
             ev[1].record()
-        ops.qsparse_attention(q, k, v, idx, scale, q_rows=idx, epi=L.DA_EPI_DELTA, out=out,
-                              n_anchor=n_anchor, delta=delta, workspace=ws)
+        ops.sparse_attention_delta(q, k, v, window=a.window, sink=a.sink, sm_scale=scale,
+                                   dense_sel=dense_sel, gamma=a.gamma, s_p=s_p, out=out)
         if ev is not None:
             ev[2].record()
-        ops.delta_add(out, s_p=s_p, out=out, delta=delta, gamma=a.gamma)
-        if ev is not None:
-            ev[3].record()
 
     for _ in range(a.warmup):
         step()
@@ -299,30 +302,54 @@ def main():
     ms = (time.perf_counter() - t0) / a.steps * 1e3
 
     # per-kernel durations from HIP events on the launch stream (separate pass)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(a.steps)]
     for e in evs:
         step(e)
     torch.cuda.synchronize()
-    k_ms = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / a.steps for i in range(3)]
+    k_ms = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / a.steps for i in range(2)]
 
-    f_sparse = O.flops_sparse(B, H, D, S, a.window, a.sink)
+    # outside the step: the stand-alone kernels (1) and (3) on the same data, the
+    # forms the sparse-only / recompute modes and the variable-stride path use
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(a.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / a.steps
+    sparse_buf = torch.empty_like(out)
+    ms_sparse = timed(lambda: ops.sparse_attention(q, k, v, window=a.window, sink=a.sink,
+                                                   sm_scale=scale, out=sparse_buf))
+    delta = torch.zeros(B, n_anchor, H, D, device=dev, dtype=torch.bfloat16)
+    ms_add = timed(lambda: ops.delta_add(sparse_buf, s_p=s_p, out=sparse_buf, delta=delta,
+                                         gamma=a.gamma))
+    del sparse_buf, delta
+
+    counts = O.sparse_row_counts(S, a.window, a.sink)
+    f_fused = 4.0 * D * H * B * float(counts[:s_p].sum())   # kernel (1) rows < s_p
+    f_sparse = O.flops_sparse(B, H, D, S, a.window, a.sink)  # kernel (1) over every row
     f_q = O.flops_qsparse(B, H, D, idx.cpu().numpy())
     bytes_add = B * H * D * 2 * (2 * s_p + n_anchor)
-    tflops = (f_sparse + f_q) / (ms * 1e-3) / 1e12
+    tflops = (f_fused + f_q) / (ms * 1e-3) / 1e12
+
+    def mf(f, t):
+        return {"ms": round(t, 4), "tflops": round(f / t / 1e9, 2),
+                "frac_mfma": round(f / t / 1e9 / PEAK_BF16_TFLOPS, 4), "flop": f}
     kernels = {
-        "sparse_attn": {"ms": round(k_ms[0], 4), "tflops": round(f_sparse / k_ms[0] / 1e9, 2),
-                        "frac_mfma": round(f_sparse / k_ms[0] / 1e9 / PEAK_BF16_TFLOPS, 4),
-                        "flop": f_sparse},
-        "qsparse_attn": {"ms": round(k_ms[1], 4), "tflops": round(f_q / k_ms[1] / 1e9, 2),
-                         "frac_mfma": round(f_q / k_ms[1] / 1e9 / PEAK_BF16_TFLOPS, 4),
-                         "flop": f_q, "rows": n_sel},
-        "delta_add": {"ms": round(k_ms[2], 4), "gbs": round(bytes_add / k_ms[2] / 1e6, 1),
-                      "frac_hbm": round(bytes_add / k_ms[2] / 1e6 / PEAK_HBM_GBS, 4),
-                      "bytes": bytes_add},
+        "qsparse_attn": dict(mf(f_q, k_ms[0]), rows=n_sel, in_step=True),
+        "sparse_attn_delta": dict(mf(f_fused, k_ms[1]), in_step=True),
+        "sparse_attn": dict(mf(f_sparse, ms_sparse), in_step=False),
+        "delta_add": {"ms": round(ms_add, 4), "gbs": round(bytes_add / ms_add / 1e6, 1),
+                      "frac_hbm": round(bytes_add / ms_add / 1e6 / PEAK_HBM_GBS, 4),
+                      "bytes": bytes_add, "in_step": False},
     }
     for name in kernels:
         kernels[name]["traffic"] = load_traffic(name)
-    dom = "sparse_attn" if k_ms[0] >= k_ms[1] else "qsparse_attn"
+    dom = "sparse_attn_delta" if k_ms[1] >= k_ms[0] else "qsparse_attn"
     achieved = kernels[dom]["tflops"]
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
@@ -330,7 +357,7 @@ def main():
 
     cpu = None
     if a.cpu_budget > 0:
-        cpu = cpu_baseline(a, q, k, v, f_sparse + f_q)
+        cpu = cpu_baseline(a, q, k, v, f_fused + f_q)
 
     line = {
         "metric": METRIC, "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1,

@@ -62,7 +62,8 @@ constexpr int NSTAGE = 2;            // LDS stages for K and for V
 constexpr float RESCALE_THRESH = 8.0f;   // log2 domain
 constexpr float NEG_BIG = -1.0e30f;      // finite "minus infinity" for the running max
 
-enum { MODE_SPARSE = 0, MODE_QSPARSE = 1 };
+// MODE_FUSED is MODE_SPARSE with the delta broadcast-add in its epilogue.
+enum { MODE_SPARSE = 0, MODE_QSPARSE = 1, MODE_FUSED = 2 };
 
 struct AttnArgs {
   const void* q;
@@ -74,6 +75,7 @@ struct AttnArgs {
   void* o;
   int64_t os_b, os_h, os_s;
   int B, Hq, Hkv, G;
+  int Gs, n_hs;     // key-sparse mode: query heads per row tile (Gs | G), G / Gs head splits
   int n_rows;       // query rows per (batch, head)
   int n_q;          // rows of q (selected rows index into it)
   int n_kv;         // keys
@@ -88,7 +90,18 @@ struct AttnArgs {
   int n_splits;
   float* part_o;    // [item][BM][D]
   float* part_ml;   // [item][2][BM]  (running max, row sum)
+  // MODE_FUSED: dense anchor rows [B, n_anchor, Hq, D] (strides batch, head,
+  // anchor), optional delta output (same layout), stride and rows < s_p
+  const void* dsel;
+  int64_t dsel_b, dsel_h, dsel_a;
+  void* dout;
+  int64_t dout_b, dout_h, dout_a;
+  int gamma, s_p, n_anchor;
 };
+
+// Bytes of LDS that hold a fused tile's dense anchor rows, prefetched with the
+// first K/V tiles (tiles with more anchor rows read them in the epilogue).
+constexpr int DPRE_BYTES = 4096;
 
 // sigma: swaps bits 2 and 3 of a key index within a 32-key half tile. Using
 // K row sigma(r) as A-operand row r puts keys 8*g .. 8*g+7 (g = lane / 32) in
@@ -136,6 +149,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   // [stage][K, V][tile bytes]
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE][2][TL::BYTES];
   __shared__ int red[4][NWAVE];
+  __shared__ __attribute__((aligned(16))) char dpre[MODE == MODE_FUSED ? DPRE_BYTES : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -151,10 +165,14 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   const int per_xcd = gridDim.x >> 3;
   const int w = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (w >= a.n_items) return;
-  int mt, split = 0, bh;
-  if (MODE == MODE_SPARSE) {
-    mt = w % a.n_mtiles;
-    bh = w / a.n_mtiles;
+  constexpr bool KSPARSE = MODE != MODE_QSPARSE;
+  int mt, split = 0, bh, hs = 0;
+  if (KSPARSE) {
+    // head split innermost: the tiles of one row block share K/V in L2
+    hs = w % a.n_hs;
+    const int t = w / a.n_hs;
+    mt = t % a.n_mtiles;
+    bh = t / a.n_mtiles;
   } else {
     mt = w % a.n_mtiles;
     const int t = w / a.n_mtiles;
@@ -164,14 +182,20 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   const int hk = bh % a.Hkv;
   const int b = bh / a.Hkv;
   const int G = a.G;
+  const int GT = KSPARSE ? a.Gs : G;   // heads packed in this row tile
+  // Fused epilogue: a tile wholly in the dense tail writes nothing. The other
+  // tiles keep the row grouping of the plain launch (the wave-wide rescale
+  // decisions, hence the rounded results, are the same).
+  if (MODE == MODE_FUSED && mt * (BM / GT) >= a.s_p) return;
 
-  // ---- this lane's query row: flattened row mt * BM + 32 * wave + ln ----
+  // ---- this lane's (query row, head): flattened pair mt * BM + 32 * wave + ln
+  //      of the tile's GT heads hk * G + hs * GT + (0 .. GT-1) ----
   const int mflat = mt * BM + wave * 32 + ln;
-  const bool valid = mflat < a.n_rows * G;
-  const int irow = valid ? mflat / G : 0;
-  const int hrow = hk * G + (valid ? mflat % G : 0);
+  const bool valid = mflat < a.n_rows * GT;
+  const int irow = valid ? mflat / GT : 0;
+  const int hrow = hk * G + hs * GT + (valid ? mflat % GT : 0);
   int qrow, lo, hi;
-  if (MODE == MODE_SPARSE) {
+  if (KSPARSE) {
     qrow = irow;
     hi = valid ? irow : -1;
     lo = (irow / a.q_block) * a.q_block + a.q_block - a.window;
@@ -184,7 +208,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   }
   int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
   int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
-  const int sink = (MODE == MODE_SPARSE) ? a.sink : 0;
+  const int sink = KSPARSE ? a.sink : 0;
 
   // ---- tile-wide bounds (valid rows only) ----
 #pragma unroll
@@ -212,7 +236,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
 
   // ---- key tiles to visit ----
   int n_first, n_second, second_t0;
-  if (MODE == MODE_SPARSE) {
+  if (KSPARSE) {
     // sink tiles [0, ceil(min(sink, lo_min, hi_max + 1) / BN)), then window
     // tiles from the tile holding lo_min up to the tile holding hi_max.
     int sink_end = min(min(sink, lo_min), hi_max + 1);
@@ -448,6 +472,28 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     }
   };
 
+  // Fused epilogue: DMA the tile's dense anchor rows ([group][head][D]) into
+  // dpre now, so the epilogue does not wait on global memory. Slots past the
+  // tile's anchors point beyond the buffer and read as zero.
+  bool pre = false;
+  if constexpr (MODE == MODE_FUSED) {
+    const int n_grp = (BM / GT) / a.gamma;
+    pre = n_grp * GT * D * (int)esz <= DPRE_BYTES;
+    if (pre) {
+      const int g0 = mt * (BM / GT) / a.gamma;
+      const int slot = tid / DCH, ch = tid % DCH;
+      const int gl = slot / GT, hl = slot % GT;
+      const int64_t span = ((int64_t)(a.n_anchor - 1) * a.dsel_a + (int64_t)(a.Hq - 1) * a.dsel_h + D) * esz;
+      const char* dbase = (const char*)a.dsel + (int64_t)b * a.dsel_b * esz;
+      const __amdgpu_buffer_rsrc_t rd =
+          make_rsrc(dbase, span > 0xffffffffLL ? 0xffffffffu : (uint32_t)span);
+      const bool ok = slot < n_grp * GT && g0 + gl < a.n_anchor;
+      const int64_t off = ((int64_t)(g0 + gl) * a.dsel_a + (int64_t)(hk * G + hs * GT + hl) * a.dsel_h) * esz + ch * 16;
+      if (tid < DPRE_BYTES / 16)
+        dma16(rd, (DA_LDS void*)(&dpre[wave * 1024]), ok && off < 0xffff0000LL ? (uint32_t)off : 0xffffffffu);
+    }
+  }
+
   f32x16 sa[NH], sb[NH];
   if (nt > 0) {
     // prologue: K(0), V(0), K(1); S(0) and its running max
@@ -477,6 +523,83 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
 
   // ---- epilogue ----
   const float l_tot = sum32(l_i);
+  if (MODE == MODE_FUSED) {
+    // out[r] = rnd(rnd(sparse[r]) + delta[r / gamma]) for rows r < s_p, with
+    // delta[g] = rnd(dense[g] - rnd(sparse[g * gamma])) formed by the anchor
+    // row's lanes (gamma divides the tile height, so every group of the tile
+    // has its anchor in it) and shared through LDS. Rows >= s_p are not
+    // written: they hold the dense tail.
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    u32x2 sp[NDT][4];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        sp[dt][jq][0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
+        sp[dt][jq][1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+      }
+    const int row0 = mt * (BM / GT);                 // first row of the tile
+    const bool live = valid && irow < a.s_p;
+    const int gl = (irow - row0) / a.gamma;          // group within the tile
+    // delta rows in LDS. With the dense rows prefetched, each anchor lane
+    // replaces its own dense elements in dpre ([group][head][D]) by the delta,
+    // so one barrier suffices. Otherwise they go to the K/V stage memory
+    // ([group][head][lg][D/2]) once every wave is done with it.
+    DA_LDS u32x2* dl;
+    if (pre) {
+      dl = (DA_LDS u32x2*)&dpre[0] + ((gl * GT + mflat % GT) * D) / 4 + lg;
+      if (nt == 0) {     // no key tile ran: make every wave's dpre DMA visible
+        wait_vmcnt<0>();
+        __syncthreads();
+      }
+    } else {
+      dl = (DA_LDS u32x2*)&smem[0][0][0] + ((gl * GT + mflat % GT) * 2 + lg) * (NDT * 4);
+      __syncthreads();   // every wave is done with the K/V stages
+    }
+    // element (dt, jq) of this lane: dims 32 dt + 8 jq + 4 lg .. +3
+    auto dslot = [&](int dt, int jq) -> DA_LDS u32x2* {
+      return pre ? dl + 8 * dt + 2 * jq : dl + dt * 4 + jq;
+    };
+    if (live && irow % a.gamma == 0) {
+      const int64_t g = irow / a.gamma;
+      const char* dp = (const char*)a.dsel +
+                       ((int64_t)b * a.dsel_b + (int64_t)hrow * a.dsel_h + g * a.dsel_a) * esz;
+      char* op = a.dout ? (char*)a.dout +
+                              ((int64_t)b * a.dout_b + (int64_t)hrow * a.dout_h + g * a.dout_a) * esz
+                        : nullptr;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          const int d = 32 * dt + 8 * jq + 4 * lg;
+          const u32x2 dn = pre ? *dslot(dt, jq) : *(const u32x2*)(dp + d * esz);
+          u32x2 dv;
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+            dv[e] = E::pack2(E::lo(dn[e]) - E::lo(sp[dt][jq][e]), E::hi(dn[e]) - E::hi(sp[dt][jq][e]));
+          *dslot(dt, jq) = dv;
+          if (op) *(u32x2*)(op + d * esz) = dv;
+        }
+    }
+    __syncthreads();
+    if (live) {
+      char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
+                               (int64_t)qrow * a.os_s) * esz;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          const int d = 32 * dt + 8 * jq + 4 * lg;
+          const u32x2 dv = *dslot(dt, jq);
+          u32x2 o;
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+            o[e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[e]), E::hi(sp[dt][jq][e]) + E::hi(dv[e]));
+          *(u32x2*)(op + d * esz) = o;
+        }
+    }
+    return;
+  }
   if (MODE == MODE_SPARSE) {
     if (!valid) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -611,6 +734,10 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
         char* dp = (char*)a.delta +
                    ((int64_t)b * a.ds_b + (int64_t)h * a.ds_h + (int64_t)i * a.ds_a + 8 * c) * esz;
         *(u32x4*)dp = dl;
+      } else if (a.epi == DA_EPI_DENSE && i < a.n_anchor) {
+        char* dp = (char*)a.delta +
+                   ((int64_t)b * a.ds_b + (int64_t)h * a.ds_h + (int64_t)i * a.ds_a + 8 * c) * esz;
+        *(u32x4*)dp = pk;
       } else {
         *(u32x4*)op = pk;
       }
@@ -667,6 +794,11 @@ static void launch_merge(const MergeArgs& m, int n_tiles, hipStream_t s) {
   hipLaunchKernelGGL((qsparse_merge_kernel<T, D>), dim3(n_tiles), dim3(MTHR), 0, s, m);
 }
 
+// Query heads per key-sparse row tile: two of an even GQA group (64-row
+// tiles, so that a stride group of up to 64 rows has its anchor in the tile),
+// else the whole group.
+static int tile_heads(int G) { return (G % 2 == 0) ? 2 : G; }
+
 // Key/value row strides (elements) in [0, 2^23): row byte strides below 2^24.
 static bool kv_rows_ok(const int64_t k_str[3], const int64_t v_str[3]) {
   return k_str[2] >= 0 && k_str[2] < (1 << 23) && v_str[2] >= 0 && v_str[2] < (1 << 23);
@@ -676,12 +808,12 @@ static bool kv_rows_ok(const int64_t k_str[3], const int64_t v_str[3]) {
 
 using namespace da;
 
-extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out,
-                                  int B, int Hq, int Hkv, int S, int D,
-                                  const int64_t q_str[3], const int64_t k_str[3],
-                                  const int64_t v_str[3], const int64_t o_str[3],
-                                  int window, int sink, int q_block, float sm_scale,
-                                  int dtype, void* stream) {
+// Checks and argument block shared by the two key-sparse entry points.
+static int sparse_args(AttnArgs& a, const void* q, const void* k, const void* v, void* out,
+                       int B, int Hq, int Hkv, int S, int D,
+                       const int64_t q_str[3], const int64_t k_str[3],
+                       const int64_t v_str[3], const int64_t o_str[3],
+                       int window, int sink, int q_block, float sm_scale, int dtype) {
   int rc;
   if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
   if (S < 0 || window < 0 || sink < 0 || q_block < 1) return DA_ERR_INVALID_ARG;
@@ -692,7 +824,7 @@ extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, v
       !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
     return DA_ERR_ALIGNMENT;
   if (!kv_rows_ok(k_str, v_str)) return DA_ERR_INVALID_ARG;
-  AttnArgs a = {};
+  a = AttnArgs{};
   a.q = q; a.k = k; a.v = v; a.o = out;
   a.qs_b = q_str[0]; a.qs_h = q_str[1]; a.qs_s = q_str[2];
   a.ks_b = k_str[0]; a.ks_h = k_str[1]; a.ks_s = k_str[2];
@@ -700,14 +832,71 @@ extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, v
   a.os_b = o_str[0]; a.os_h = o_str[1]; a.os_s = o_str[2];
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv;
   a.n_rows = S; a.n_q = S; a.n_kv = S;
-  a.n_mtiles = (int)(((int64_t)S * a.G + BM - 1) / BM);
-  const int64_t items = (int64_t)B * Hkv * a.n_mtiles;
-  if (items > 0x7fffff00LL) return DA_ERR_INVALID_ARG;
-  a.n_items = (int)items;
+  a.Gs = tile_heads(a.G); a.n_hs = a.G / a.Gs;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.window = window; a.sink = sink; a.q_block = q_block;
+  return DA_OK;
+}
+
+// Work items for rows [0, n_rows) of the argument block.
+static int sparse_items(AttnArgs& a) {
+  a.n_mtiles = (int)(((int64_t)a.n_rows * a.Gs + BM - 1) / BM);
+  const int64_t items = (int64_t)a.B * a.Hkv * a.n_hs * a.n_mtiles;
+  if (items > 0x7fffff00LL) return DA_ERR_INVALID_ARG;
+  a.n_items = (int)items;
+  return DA_OK;
+}
+
+extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                                  int B, int Hq, int Hkv, int S, int D,
+                                  const int64_t q_str[3], const int64_t k_str[3],
+                                  const int64_t v_str[3], const int64_t o_str[3],
+                                  int window, int sink, int q_block, float sm_scale,
+                                  int dtype, void* stream) {
+  AttnArgs a;
+  int rc = sparse_args(a, q, k, v, out, B, Hq, Hkv, S, D, q_str, k_str, v_str, o_str,
+                       window, sink, q_block, sm_scale, dtype);
+  if (rc != DA_OK || S == 0) return rc;
+  if ((rc = sparse_items(a)) != DA_OK) return rc;
   (void)hipGetLastError();
   dispatch_attn<MODE_SPARSE>(a, D, dtype, (hipStream_t)stream);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}
+
+extern "C" int da_fused_delta_rows(int Hq, int Hkv) {
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;
+  const int gs = tile_heads(Hq / Hkv);
+  return gs <= 2 ? BM / gs : 0;
+}
+
+extern "C" int da_sparse_attn_delta_fwd(const void* q, const void* k, const void* v, void* out,
+                                        int B, int Hq, int Hkv, int S, int D,
+                                        const int64_t q_str[3], const int64_t k_str[3],
+                                        const int64_t v_str[3], const int64_t o_str[3],
+                                        int window, int sink, int q_block, float sm_scale,
+                                        const void* dense_sel, const int64_t ds_str[3],
+                                        int gamma, int s_p,
+                                        void* delta_out, const int64_t dl_str[3],
+                                        int dtype, void* stream) {
+  AttnArgs a;
+  int rc = sparse_args(a, q, k, v, out, B, Hq, Hkv, S, D, q_str, k_str, v_str, o_str,
+                       window, sink, q_block, sm_scale, dtype);
+  if (rc != DA_OK) return rc;
+  const int rows = da_fused_delta_rows(Hq, Hkv);
+  if (gamma < 1 || rows == 0 || rows % gamma != 0) return DA_ERR_INVALID_ARG;
+  if (s_p < 0 || s_p > S || s_p % gamma != 0) return DA_ERR_INVALID_ARG;
+  if (s_p == 0) return DA_OK;
+  if (!dense_sel || !ds_str) return DA_ERR_INVALID_ARG;
+  if (!aligned16(dense_sel) || !strides8(ds_str)) return DA_ERR_ALIGNMENT;
+  if (delta_out && (!dl_str)) return DA_ERR_INVALID_ARG;
+  if (delta_out && (!aligned16(delta_out) || !strides8(dl_str))) return DA_ERR_ALIGNMENT;
+  a.dsel = dense_sel; a.dsel_b = ds_str[0]; a.dsel_h = ds_str[1]; a.dsel_a = ds_str[2];
+  a.dout = delta_out;
+  if (delta_out) { a.dout_b = dl_str[0]; a.dout_h = dl_str[1]; a.dout_a = dl_str[2]; }
+  a.gamma = gamma; a.s_p = s_p; a.n_anchor = s_p / gamma;
+  if ((rc = sparse_items(a)) != DA_OK) return rc;
+  (void)hipGetLastError();
+  dispatch_attn<MODE_FUSED>(a, D, dtype, (hipStream_t)stream);
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }
 
@@ -728,12 +917,13 @@ extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
   int rc;
   if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
   if (n < 0 || Sq < 0 || Skv < 0 || rl_bstride < 0) return DA_ERR_INVALID_ARG;
-  if (epi != DA_EPI_OUTPUT && epi != DA_EPI_DELTA && epi != DA_EPI_SCATTER) return DA_ERR_INVALID_ARG;
+  if (epi != DA_EPI_OUTPUT && epi != DA_EPI_DELTA && epi != DA_EPI_SCATTER && epi != DA_EPI_DENSE)
+    return DA_ERR_INVALID_ARG;
   if (!q_str || !k_str || !v_str || !o_str) return DA_ERR_INVALID_ARG;
   if (n == 0) return DA_OK;
   if (!q || !k || !v || !o || !row_last || Sq < 1 || Skv < 1) return DA_ERR_INVALID_ARG;
   if (q_rows == nullptr && n > Sq) return DA_ERR_INVALID_ARG;
-  if (epi == DA_EPI_DELTA) {
+  if (epi == DA_EPI_DELTA || epi == DA_EPI_DENSE) {
     if (n_anchor < 0 || n_anchor > n) return DA_ERR_INVALID_ARG;
     if (n_anchor > 0 && (!delta || !d_str)) return DA_ERR_INVALID_ARG;
     if (n_anchor > 0 && (!aligned16(delta) || !strides8(d_str))) return DA_ERR_ALIGNMENT;
@@ -751,7 +941,7 @@ extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
   a.qs_b = q_str[0]; a.qs_h = q_str[1]; a.qs_s = q_str[2];
   a.ks_b = k_str[0]; a.ks_h = k_str[1]; a.ks_s = k_str[2];
   a.vs_b = v_str[0]; a.vs_h = v_str[1]; a.vs_s = v_str[2];
-  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.Gs = a.G; a.n_hs = 1;
   a.n_rows = n; a.n_q = Sq; a.n_kv = Skv;
   a.n_mtiles = p.n_mtiles;
   a.n_items = p.n_items;
@@ -766,7 +956,7 @@ extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
   m.n_rows = n; m.n_q = Sq; m.G = a.G; m.Hkv = Hkv; m.n_kv = Skv; m.n_mtiles = p.n_mtiles;
   m.n_splits = p.n_splits; m.chunk = p.chunk;
   m.part_o = a.part_o; m.part_ml = a.part_ml;
-  m.epi = epi; m.n_anchor = (epi == DA_EPI_DELTA) ? n_anchor : 0;
+  m.epi = epi; m.n_anchor = (epi == DA_EPI_DELTA || epi == DA_EPI_DENSE) ? n_anchor : 0;
   m.o = o; m.os_b = o_str[0]; m.os_h = o_str[1]; m.os_s = o_str[2];
   m.delta = delta;
   if (d_str) { m.ds_b = d_str[0]; m.ds_h = d_str[1]; m.ds_a = d_str[2]; }

@@ -26,9 +26,12 @@ DA_FP16 = 1
 DA_EPI_OUTPUT = 0
 DA_EPI_DELTA = 1
 DA_EPI_SCATTER = 2
+DA_EPI_DENSE = 3
 
 EXPORTS = (
     "da_sparse_attn_fwd",
+    "da_sparse_attn_delta_fwd",
+    "da_fused_delta_rows",
     "da_qsparse_workspace_bytes",
     "da_qsparse_attn_fwd",
     "da_delta_add",
@@ -77,6 +80,12 @@ def lib() -> ctypes.CDLL:
     L.da_sparse_attn_fwd.restype = _i
     L.da_sparse_attn_fwd.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                      _p3, _p3, _p3, _p3, _i, _i, _i, _f, _i, _vp]
+    L.da_sparse_attn_delta_fwd.restype = _i
+    L.da_sparse_attn_delta_fwd.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                           _p3, _p3, _p3, _p3, _i, _i, _i, _f,
+                                           _vp, _p3, _i, _i, _vp, _p3, _i, _vp]
+    L.da_fused_delta_rows.restype = _i
+    L.da_fused_delta_rows.argtypes = [_i, _i]
     L.da_qsparse_workspace_bytes.restype = _sz
     L.da_qsparse_workspace_bytes.argtypes = [_i, _i, _i, _i, _i, _i]
     L.da_qsparse_attn_fwd.restype = _i

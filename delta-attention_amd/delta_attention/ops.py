@@ -87,6 +87,49 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, windo
     return out
 
 
+def fused_delta_rows(H: int, Hkv: int) -> int:
+    """Row-tile height of the key-sparse kernel (64 for an even GQA ratio, 128
+    for MHA), or 0 when the fused delta epilogue is unavailable."""
+    return int(L.lib().da_fused_delta_rows(int(H), int(Hkv)))
+
+
+def sparse_attention_delta(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int,
+                           sink: int, sm_scale: float, dense_sel: torch.Tensor, gamma: int,
+                           s_p: int, out: torch.Tensor, delta_out: Optional[torch.Tensor] = None,
+                           q_block: int = Q_BLOCK) -> torch.Tensor:
+    """Kernel (1) with the delta broadcast-add in its epilogue: rows r < s_p of
+    `out` [B,S,H,D] become rnd(rnd(sparse[r]) + delta[r // gamma]) with
+    delta[g] = rnd(dense_sel[:, g] - rnd(sparse[g * gamma])) (llama.py:733-755);
+    rows >= s_p are left as they are (the dense tail). dense_sel [B,n_anchor,H,D];
+    delta_out (same shape) receives the deltas when given."""
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    assert k.shape == (B, Hkv, S, D) and v.shape == (B, Hkv, S, D), (q.shape, k.shape, v.shape)
+    assert q.dtype == k.dtype == v.dtype == out.dtype == dense_sel.dtype
+    assert out.shape == (B, S, H, D) and out.stride(-1) == 1 and out.data_ptr() % 16 == 0
+    n_anchor = -(-s_p // gamma) if s_p > 0 else 0
+    assert dense_sel.shape == (B, n_anchor, H, D) and dense_sel.stride(-1) == 1, dense_sel.shape
+    dev = _on_gpu(q, k, v, out, dense_sel)
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    dl = L.strides3(0, 0, 0)
+    if delta_out is not None:
+        assert delta_out.shape == dense_sel.shape and delta_out.dtype == q.dtype
+        assert delta_out.stride(-1) == 1
+        dl = L.strides3(delta_out.stride(0), delta_out.stride(2), delta_out.stride(1))
+    with torch.cuda.device(dev):
+        rc = L.lib().da_sparse_attn_delta_fwd(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, S, D,
+            L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+            L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+            L.strides3(v.stride(0), v.stride(1), v.stride(2)),
+            L.strides3(out.stride(0), out.stride(2), out.stride(1)),
+            int(window), int(sink), int(q_block), float(sm_scale),
+            _ptr(dense_sel), L.strides3(dense_sel.stride(0), dense_sel.stride(2), dense_sel.stride(1)),
+            int(gamma), int(s_p), _ptr(delta_out), dl, _code(q), _stream(dev))
+    L.check(rc, "da_sparse_attn_delta_fwd")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # kernel (2)
 
@@ -118,8 +161,8 @@ def qsparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     q [B,H,Sq,D]; k/v [B,Hkv,Skv,D] (GQA native, any strides);
     q_rows: optional [n] int64 rows of q to use (default: rows 0..n-1, n = len(row_last)).
     epi == DA_EPI_OUTPUT: returns o [B,H,n,D] (new, or `out`).
-    epi == DA_EPI_DELTA / DA_EPI_SCATTER: `out` is the [B,S,H,D] layer output;
-    see include/delta_attn.h.
+    epi == DA_EPI_DELTA / DA_EPI_SCATTER / DA_EPI_DENSE: `out` is the [B,S,H,D]
+    layer output; see include/delta_attn.h.
     """
     B, H, Sq, D = q.shape
     Hkv, Skv = k.shape[1], k.shape[2]
@@ -144,7 +187,7 @@ def qsparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         o_str = L.strides3(out.stride(0), out.stride(2), out.stride(1))
     assert out.dtype == q.dtype and out.stride(-1) == 1
     d_str = None
-    if epi == L.DA_EPI_DELTA and n_anchor > 0:
+    if epi in (L.DA_EPI_DELTA, L.DA_EPI_DENSE) and n_anchor > 0:
         assert delta is not None and delta.shape == (B, n_anchor, H, D) and delta.dtype == q.dtype
         d_str = L.strides3(delta.stride(0), delta.stride(2), delta.stride(1))
     if workspace is None:
@@ -267,7 +310,7 @@ def selected_rows(s: int, gamma: int, device: str) -> torch.Tensor:
 def delta_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, gamma: int,
                   window: int, sink: int, sm_scale: float, mode: str = "delta",
                   out: Optional[torch.Tensor] = None,
-                  return_delta: bool = False):
+                  return_delta: bool = False, fused: bool = True):
     """One delta-attention layer prefill: q [B,H,s,D], k/v [B,Hkv,s,D] (post-RoPE)
     -> [B,s,H,D] (llama.py:659-757).
 
@@ -276,14 +319,34 @@ def delta_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, gamma: i
     the anchor at or before each row, dense tail rows.
     When s <= cut_n there are no anchors and every row is computed densely.
     return_delta: also return the [B,n_anchor,H,D] anchor deltas (drift telemetry).
+    fused (mode "delta"): when the head geometry and gamma allow it
+    (gamma | fused_delta_rows(H, Hkv)), kernel (2) runs first and kernel (3) is
+    fused into kernel (1)'s epilogue; the result is bit-identical to the
+    three-kernel sequence (fused=False).
     """
     assert mode in ("delta", "recompute", "sparse-only"), mode
     assert gamma >= 1
     B, H, s, D = q.shape
+    cut_n, s_p, n_anchor = anchor_layout(s, gamma)
+    rows = fused_delta_rows(H, k.shape[1])
+    if mode == "delta" and s_p > 0 and fused and rows and rows % gamma == 0:
+        # kernel (2) first (dense tail into the output, dense anchor rows
+        # aside), then kernel (1) with the broadcast-add in its epilogue
+        if out is None:
+            out = torch.empty((B, s, H, D), device=q.device, dtype=q.dtype)
+        idx = selected_rows(s, gamma, str(q.device))
+        ws = qsparse_workspace(B, H, k.shape[1], idx.numel(), s, D, q.device)
+        dense_sel = torch.empty((B, n_anchor, H, D), device=q.device, dtype=q.dtype)
+        qsparse_attention(q, k, v, idx, sm_scale, q_rows=idx, epi=L.DA_EPI_DENSE, out=out,
+                          n_anchor=n_anchor, delta=dense_sel, workspace=ws)
+        delta = torch.empty_like(dense_sel) if return_delta else None
+        sparse_attention_delta(q, k, v, window=window, sink=sink, sm_scale=sm_scale,
+                               dense_sel=dense_sel, gamma=gamma, s_p=s_p, out=out,
+                               delta_out=delta)
+        return (out, delta) if return_delta else out
     out = sparse_attention(q, k, v, window=window, sink=sink, sm_scale=sm_scale, out=out)
     if mode == "sparse-only":
         return (out, None) if return_delta else out
-    cut_n, s_p, n_anchor = anchor_layout(s, gamma)
     idx = selected_rows(s, gamma, str(q.device))
     ws = qsparse_workspace(B, H, k.shape[1], idx.numel(), s, D, q.device)
     if mode == "recompute" or s_p <= 0:

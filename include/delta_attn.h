@@ -50,6 +50,9 @@ extern "C" {
 #define DA_EPI_DELTA 1     /* rows i < n_anchor: delta[b, i, h, :] = dense - sparse[b, q_rows[i], h, :];
                               rows i >= n_anchor: out[b, q_rows[i], h, :] = dense */
 #define DA_EPI_SCATTER 2   /* out[b, q_rows[i], h, :] = dense for every row (mode "recompute") */
+#define DA_EPI_DENSE 3     /* rows i < n_anchor: delta[b, i, h, :] = dense (the dense anchor rows
+                              da_sparse_attn_delta_fwd consumes); rows i >= n_anchor:
+                              out[b, q_rows[i], h, :] = dense */
 
 /*
  * Kernel (1): key-sparse attention (sink + block-anchored sliding window).
@@ -69,6 +72,39 @@ int da_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out,
                        const int64_t v_str[3], const int64_t o_str[3],
                        int window, int sink, int q_block, float sm_scale,
                        int dtype, void* stream);
+
+/*
+ * Kernel (1) with kernel (3) fused into its epilogue: the uniform-stride
+ * broadcast of delta_attention/llama.py:733-755 applied while the key-sparse
+ * rows are still in registers, so the sparse output is written once and never
+ * re-read. For rows r < s_p:
+ *   delta[g] = rnd(dense_sel[b, g, h, :] - rnd(sparse[b, g * gamma, h, :]))
+ *   out[b, r, h, :] = rnd(rnd(sparse[b, r, h, :]) + delta[r / gamma])
+ * (the reference's bf16 composition, bit-identical to da_sparse_attn_fwd
+ * followed by da_delta_add on the same inputs). Rows >= s_p of `out` are not
+ * written (they hold the dense tail, written by da_qsparse_attn_fwd with
+ * DA_EPI_DENSE, which also produces dense_sel [B, n_anchor, Hq, D] with ds_str
+ * = {batch, head, anchor}). delta_out (NULL: not written) receives the deltas
+ * in the same layout (dl_str). Requires s_p % gamma == 0 and gamma dividing
+ * da_fused_delta_rows(Hq, Hkv); other arguments as for da_sparse_attn_fwd.
+ * No counterpart in the reference beyond the composition it replaces.
+ */
+int da_sparse_attn_delta_fwd(const void* q, const void* k, const void* v, void* out,
+                             int B, int Hq, int Hkv, int S, int D,
+                             const int64_t q_str[3], const int64_t k_str[3],
+                             const int64_t v_str[3], const int64_t o_str[3],
+                             int window, int sink, int q_block, float sm_scale,
+                             const void* dense_sel, const int64_t ds_str[3],
+                             int gamma, int s_p,
+                             void* delta_out, const int64_t dl_str[3],
+                             int dtype, void* stream);
+
+/*
+ * Row-tile height of the key-sparse kernel for this head geometry (64 when
+ * Hq / Hkv is even, 128 when it is 1), or 0 when the fused delta epilogue is
+ * not available (odd GQA ratio above 1). The stride gamma must divide it.
+ */
+int da_fused_delta_rows(int Hq, int Hkv);
 
 /*
  * Workspace (bytes) that da_qsparse_attn_fwd needs for these sizes; 0 is a
@@ -93,6 +129,8 @@ size_t da_qsparse_workspace_bytes(int B, int Hq, int Hkv, int n, int Skv, int D)
  *       Rounding follows the reference's bf16 composition
  *       (delta_attention/llama.py:740): delta = rnd(rnd(dense) - sparse).
  *   epi == DA_EPI_SCATTER: `o` as for DA_EPI_DELTA, every row written.
+ *   epi == DA_EPI_DENSE  : as DA_EPI_DELTA, but `delta` receives rnd(dense) for
+ *       rows i < n_anchor (`o` is not read).
  * workspace must hold da_qsparse_workspace_bytes(...) bytes.
  */
 int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,

@@ -126,3 +126,30 @@ def test_rope_checks(lib):
     assert call(w=8) == L.DA_ERR_ALIGNMENT
     assert call(qs=_s3(128 * 8 * 128, 8 * 128, 100)) == L.DA_ERR_ALIGNMENT
     assert call(S=0) == L.DA_OK
+
+
+def test_fused_delta_rows_and_checks(lib):
+    assert lib.da_fused_delta_rows(32, 8) == 64      # GQA 4: two heads per 64-row tile
+    assert lib.da_fused_delta_rows(8, 8) == 128      # MHA
+    assert lib.da_fused_delta_rows(6, 3) == 64
+    assert lib.da_fused_delta_rows(40, 8) == 0       # GQA 5: not available
+    assert lib.da_fused_delta_rows(6, 4) == 0 and lib.da_fused_delta_rows(0, 1) == 0
+    s3 = _s3(128 * 32 * 128, 128, 32 * 128)
+    q3 = _s3(32 * 4096 * 128, 4096 * 128, 128)
+    k3 = _s3(8 * 4096 * 128, 4096 * 128, 128)
+
+    def call(gamma=64, s_p=3968, dense=16, S=4096, Hq=32, Hkv=8, dout=0):
+        return lib.da_sparse_attn_delta_fwd(
+            ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+            1, Hq, Hkv, S, 128, q3, k3, k3, s3, 512, 64, 64, 0.1,
+            ctypes.c_void_p(dense), s3, gamma, s_p, ctypes.c_void_p(dout), s3, L.DA_BF16, None)
+
+    assert call(gamma=128, s_p=3840) == L.DA_ERR_INVALID_ARG     # gamma must divide the 64-row tile
+    assert call(s_p=3900) == L.DA_ERR_INVALID_ARG                # s_p % gamma != 0
+    assert call(s_p=4160) == L.DA_ERR_INVALID_ARG                # s_p > S
+    assert call(dense=0) == L.DA_ERR_INVALID_ARG
+    assert call(Hq=40) == L.DA_ERR_INVALID_ARG                   # odd GQA ratio
+    assert call(dense=8) == L.DA_ERR_ALIGNMENT
+    assert call(dout=8) == L.DA_ERR_ALIGNMENT
+    assert call(s_p=0) == L.DA_OK
+    assert call(S=0, s_p=0) == L.DA_OK

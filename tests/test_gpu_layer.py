@@ -165,3 +165,38 @@ def test_adaptive_stride_path(gpu):
     tail = O.causal_attention_rows(qn, kn, vn, np.arange(s_p, s), scale)
     ref = np.concatenate([O.apply_delta_variable(sparse, dense_sel, idx, s_p), tail], 1)
     assert_close(np64(out), ref, what="adaptive")
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,gamma,window,sink", [
+    (1, 8, 2, 4096, 128, 64, 512, 128),   # GQA 4: 64-row tiles, two heads each
+    (2, 8, 2, 1200, 128, 16, 256, 8),     # s % gamma != 0, batch 2
+    (1, 4, 4, 1000, 64, 128, 192, 4),     # MHA: 128-row tiles, gamma 128
+    (1, 6, 3, 777, 128, 32, 100, 0),      # GQA 2
+    (1, 8, 2, 600, 128, 1, 128, 16),      # gamma 1: every row before the tail is an anchor
+])
+def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
+    """Kernel (3) fused into kernel (1)'s epilogue (kernel (2) first) gives the
+    same bits as the three-kernel sequence, deltas included, and matches the
+    oracle's delta_forward."""
+    from delta_attention import ops
+    rows = ops.fused_delta_rows(H, Hkv)
+    assert rows and rows % gamma == 0          # the fused path is the one taken
+    q, k, v = gen_qkv(B, H, Hkv, S, D, seed=gamma + S, model_layout=True)
+    scale = D ** -0.5
+    a, da = ops.delta_prefill(q, k, v, gamma=gamma, window=window, sink=sink, sm_scale=scale,
+                              return_delta=True)
+    b, db = ops.delta_prefill(q, k, v, gamma=gamma, window=window, sink=sink, sm_scale=scale,
+                              return_delta=True, fused=False)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert torch.equal(da, db)
+    ref = O.delta_forward(np64(q), np64(k), np64(v), gamma, window, sink, scale)
+    assert_close(np64(a), ref, what=f"fused B{B} H{H}/{Hkv} S{S} g{gamma}")
+
+
+def test_fused_delta_not_taken_for_odd_gqa(gpu):
+    # GQA 5 (Qwen3 geometry): no fused epilogue, the three-kernel path runs
+    from delta_attention import ops
+    assert ops.fused_delta_rows(10, 2) == 0
+    got, ref, _ = _layer(1, 10, 2, 1024, 128, 64, 256, 16, seed=3)
+    assert_close(got, ref, what="gqa5")
