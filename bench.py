@@ -56,7 +56,13 @@ def parse():
                    help="time only the fused RoPE (+ optional per-head q/k RMSNorm with "
                         "--qk-norm) prologue kernel on the workload's [B,S,H,D] q/k projection "
                         "outputs and print one JSON line with its HBM roofline")
-    p.add_argument("--qk-norm", action="store_true")
+    p.add_argument("--qk-norm", action="store_true",
+                   help="per-head RMSNorm (weight 1, eps 1e-6) on q and k before RoPE (the Qwen3 "
+                        "recipe); with --prologue, time the kernel with the norm")
+    p.add_argument("--no-q-scale", action="store_true",
+                   help="q ~ N(0,1) without the d^-0.5 factor (the Qwen3 recipe)")
+    p.add_argument("--workload", type=str, default="",
+                   help="name recorded in config.workload (default: derived from the shape)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -74,7 +80,8 @@ def copy_calibration():
 
 
 def make_inputs(a, device):
-    """Seeded N(0,1) q/k/v drawn in q, k, v order, q * d^-0.5, RoPE on q and k
+    """Seeded N(0,1) q/k/v drawn in q, k, v order, q * d^-0.5 (unless
+    --no-q-scale), per-head RMSNorm on q and k (with --qk-norm), RoPE on q and k
     (rotate_half, inv_freq = theta^(-2i/d), fp32 tables), cast to bf16."""
     import torch
     from delta_attention.llama import apply_rotary_pos_emb, rope_cos_sin
@@ -89,8 +96,13 @@ def make_inputs(a, device):
     CH = 8192
     for c0 in range(0, S, CH):
         c1 = min(S, c0 + CH)
-        qc = torch.randn(B, H, c1 - c0, D, device=device, generator=g) * D ** -0.5
+        qc = torch.randn(B, H, c1 - c0, D, device=device, generator=g)
+        if not a.no_q_scale:
+            qc = qc * D ** -0.5
         kc = torch.randn(B, Hkv, c1 - c0, D, device=device, generator=g)
+        if a.qk_norm:
+            qc = qc * torch.rsqrt(qc.pow(2).mean(-1, keepdim=True) + 1e-6)
+            kc = kc * torch.rsqrt(kc.pow(2).mean(-1, keepdim=True) + 1e-6)
         qc, kc = apply_rotary_pos_emb(qc, kc, cos[:, c0:c1], sin[:, c0:c1])
         q[:, :, c0:c1] = qc.to(torch.bfloat16)
         k[:, :, c0:c1] = kc.to(torch.bfloat16)
@@ -269,25 +281,41 @@ def main():
     idx = ops.selected_rows(S, a.gamma, str(dev))
     n_sel = idx.numel()
     rows = ops.fused_delta_rows(H, Hkv)
-    assert rows and rows % a.gamma == 0 and s_p > 0, "this workload runs the fused epilogue"
+    fused = bool(rows) and rows % a.gamma == 0
+    assert s_p > 0, "the sequence must be longer than the dense tail"
     out = torch.empty(B, S, H, D, device=dev, dtype=torch.bfloat16)
     dense_sel = torch.empty(B, n_anchor, H, D, device=dev, dtype=torch.bfloat16)
     ws = ops.qsparse_workspace(B, H, Hkv, n_sel, S, D, dev)
 
-    # one layer prefill: kernel (2) writes the dense tail rows into the output
-    # and the dense anchor rows aside, then kernel (1) runs with kernel (3)
-    # (the delta broadcast-add) fused into its epilogue
+    # one layer prefill. Fused order: kernel (2) writes the dense tail rows into
+    # the output and the dense anchor rows aside, then kernel (1) runs with
+    # kernel (3) (the delta broadcast-add) fused into its epilogue. Otherwise
+    # (GQA ratio 5, gamma 128 with GQA): kernel (1), kernel (2) writing the
+    # tail and the deltas, kernel (3) in place.
     def step(ev=None):
         if ev is not None:
             ev[0].record()
-        ops.qsparse_attention(q, k, v, idx, scale, q_rows=idx, epi=L.DA_EPI_DENSE, out=out,
-                              n_anchor=n_anchor, delta=dense_sel, workspace=ws)
-        if ev is not None:
-            ev[1].record()
-        ops.sparse_attention_delta(q, k, v, window=a.window, sink=a.sink, sm_scale=scale,
-                                   dense_sel=dense_sel, gamma=a.gamma, s_p=s_p, out=out)
-        if ev is not None:
-            ev[2].record()
+        if fused:
+            ops.qsparse_attention(q, k, v, idx, scale, q_rows=idx, epi=L.DA_EPI_DENSE, out=out,
+                                  n_anchor=n_anchor, delta=dense_sel, workspace=ws)
+            if ev is not None:
+                ev[1].record()
+            ops.sparse_attention_delta(q, k, v, window=a.window, sink=a.sink, sm_scale=scale,
+                                       dense_sel=dense_sel, gamma=a.gamma, s_p=s_p, out=out)
+            if ev is not None:
+                ev[2].record()
+                ev[3].record()
+        else:
+            ops.sparse_attention(q, k, v, window=a.window, sink=a.sink, sm_scale=scale, out=out)
+            if ev is not None:
+                ev[1].record()
+            ops.qsparse_attention(q, k, v, idx, scale, q_rows=idx, epi=L.DA_EPI_DELTA, out=out,
+                                  n_anchor=n_anchor, delta=dense_sel, workspace=ws)
+            if ev is not None:
+                ev[2].record()
+            ops.delta_add(out, s_p=s_p, out=out, delta=dense_sel, gamma=a.gamma)
+            if ev is not None:
+                ev[3].record()
 
     for _ in range(a.warmup):
         step()
@@ -302,11 +330,11 @@ def main():
     ms = (time.perf_counter() - t0) / a.steps * 1e3
 
     # per-kernel durations from HIP events on the launch stream (separate pass)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(a.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
     for e in evs:
         step(e)
     torch.cuda.synchronize()
-    k_ms = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / a.steps for i in range(2)]
+    k_ms = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / a.steps for i in range(3)]
 
     # outside the step: the stand-alone kernels (1) and (3) on the same data, the
     # forms the sparse-only / recompute modes and the variable-stride path use
@@ -334,37 +362,57 @@ def main():
     f_sparse = O.flops_sparse(B, H, D, S, a.window, a.sink)  # kernel (1) over every row
     f_q = O.flops_qsparse(B, H, D, idx.cpu().numpy())
     bytes_add = B * H * D * 2 * (2 * s_p + n_anchor)
-    tflops = (f_fused + f_q) / (ms * 1e-3) / 1e12
+    # the layer's work: the sparse rows it needs (all rows when kernel (1) runs alone)
+    f_layer = (f_fused if fused else f_sparse) + f_q
+    tflops = f_layer / (ms * 1e-3) / 1e12
 
     def mf(f, t):
         return {"ms": round(t, 4), "tflops": round(f / t / 1e9, 2),
                 "frac_mfma": round(f / t / 1e9 / PEAK_BF16_TFLOPS, 4), "flop": f}
-    kernels = {
-        "qsparse_attn": dict(mf(f_q, k_ms[0]), rows=n_sel, in_step=True),
-        "sparse_attn_delta": dict(mf(f_fused, k_ms[1]), in_step=True),
-        "sparse_attn": dict(mf(f_sparse, ms_sparse), in_step=False),
-        "delta_add": {"ms": round(ms_add, 4), "gbs": round(bytes_add / ms_add / 1e6, 1),
-                      "frac_hbm": round(bytes_add / ms_add / 1e6 / PEAK_HBM_GBS, 4),
-                      "bytes": bytes_add, "in_step": False},
-    }
+    add = {"ms": round(ms_add, 4), "gbs": round(bytes_add / ms_add / 1e6, 1),
+           "frac_hbm": round(bytes_add / ms_add / 1e6 / PEAK_HBM_GBS, 4), "bytes": bytes_add}
+    if fused:
+        kernels = {
+            "qsparse_attn": dict(mf(f_q, k_ms[0]), rows=n_sel, in_step=True),
+            "sparse_attn_delta": dict(mf(f_fused, k_ms[1]), in_step=True),
+            "sparse_attn": dict(mf(f_sparse, ms_sparse), in_step=False),
+            "delta_add": dict(add, in_step=False),
+        }
+        dom = "sparse_attn_delta" if k_ms[1] >= k_ms[0] else "qsparse_attn"
+    else:
+        kernels = {
+            "sparse_attn": dict(mf(f_sparse, k_ms[0]), in_step=True),
+            "qsparse_attn": dict(mf(f_q, k_ms[1]), rows=n_sel, in_step=True),
+            "delta_add": dict(add, ms=round(k_ms[2], 4),
+                              gbs=round(bytes_add / k_ms[2] / 1e6, 1),
+                              frac_hbm=round(bytes_add / k_ms[2] / 1e6 / PEAK_HBM_GBS, 4),
+                              in_step=True),
+        }
+        dom = "sparse_attn" if k_ms[0] >= k_ms[1] else "qsparse_attn"
+    standard = (B, H, Hkv, S, D, a.window, a.sink, a.gamma) == (1, 32, 8, 131072, 128, 2048, 128, 64)
     for name in kernels:
-        kernels[name]["traffic"] = load_traffic(name)
-    dom = "sparse_attn_delta" if k_ms[1] >= k_ms[0] else "qsparse_attn"
+        # committed rocprofv3 traffic figures are for the default workload only
+        kernels[name]["traffic"] = load_traffic(name) if standard else None
     achieved = kernels[dom]["tflops"]
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": load_traffic(dom)}
+                "traffic": kernels[dom]["traffic"]}
 
     cpu = None
     if a.cpu_budget > 0:
-        cpu = cpu_baseline(a, q, k, v, f_fused + f_q)
+        cpu = cpu_baseline(a, q, k, v, f_layer)
 
     line = {
         "metric": METRIC, "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) q/k/v, q*d^-0.5, RoPE theta 5e5, bf16)",
-        "config": {"workload": "llama-3.1-8b-shaped delta-attention layer prefill",
+        "data": ("synthetic (seeded N(0,1) q/k/v" + ("" if a.no_q_scale else ", q*d^-0.5")
+                 + (", per-head q/k RMSNorm" if a.qk_norm else "")
+                 + f", RoPE theta {a.rope_theta:g}, bf16)"),
+        "config": {"workload": a.workload or (
+                       "llama-3.1-8b-shaped delta-attention layer prefill" if (H, Hkv, D) == (32, 8, 128)
+                       else f"delta-attention layer prefill, {H}/{Hkv} heads, head_dim {D}"),
+                   "order": "fused (2) -> (1)+(3)" if fused else "(1) -> (2) -> (3)",
                    "batch": B, "seq_len": S, "q_heads": H, "kv_heads": Hkv, "head_dim": D,
                    "window": a.window, "sink": a.sink, "gamma": a.gamma,
                    "selected_rows": n_sel, "parallelism": "none (1 GPU)"},

@@ -795,9 +795,10 @@ static void launch_merge(const MergeArgs& m, int n_tiles, hipStream_t s) {
 }
 
 // Query heads per key-sparse row tile: two of an even GQA group (64-row
-// tiles, so that a stride group of up to 64 rows has its anchor in the tile),
-// else the whole group.
-static int tile_heads(int G) { return (G % 2 == 0) ? 2 : G; }
+// tiles), else one (128-row tiles), so that a stride group of up to 64 (128)
+// rows has its anchor in the tile. Sharing each K/V tile between fewer heads
+// measured free (the tiles of one row block read K/V from L2 back to back).
+static int tile_heads(int G) { return (G % 2 == 0) ? 2 : 1; }
 
 // Key/value row strides (elements) in [0, 2^23): row byte strides below 2^24.
 static bool kv_rows_ok(const int64_t k_str[3], const int64_t v_str[3]) {
@@ -865,8 +866,7 @@ extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, v
 
 extern "C" int da_fused_delta_rows(int Hq, int Hkv) {
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;
-  const int gs = tile_heads(Hq / Hkv);
-  return gs <= 2 ? BM / gs : 0;
+  return BM / tile_heads(Hq / Hkv);
 }
 
 extern "C" int da_sparse_attn_delta_fwd(const void* q, const void* k, const void* v, void* out,

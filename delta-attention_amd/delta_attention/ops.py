@@ -89,7 +89,7 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, windo
 
 def fused_delta_rows(H: int, Hkv: int) -> int:
     """Row-tile height of the key-sparse kernel (64 for an even GQA ratio, 128
-    for MHA), or 0 when the fused delta epilogue is unavailable."""
+    for an odd one); the fused delta epilogue needs gamma to divide it."""
     return int(L.lib().da_fused_delta_rows(int(H), int(Hkv)))
 
 

@@ -100,9 +100,10 @@ int da_sparse_attn_delta_fwd(const void* q, const void* k, const void* v, void* 
                              int dtype, void* stream);
 
 /*
- * Row-tile height of the key-sparse kernel for this head geometry (64 when
- * Hq / Hkv is even, 128 when it is 1), or 0 when the fused delta epilogue is
- * not available (odd GQA ratio above 1). The stride gamma must divide it.
+ * Row-tile height of the key-sparse kernel for this head geometry: 64 when
+ * Hq / Hkv is even (two heads per tile), 128 when it is odd (one head per
+ * tile); 0 for invalid head counts. The fused delta epilogue needs gamma to
+ * divide it.
  */
 int da_fused_delta_rows(int Hq, int Hkv);
 

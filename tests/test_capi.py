@@ -132,7 +132,7 @@ def test_fused_delta_rows_and_checks(lib):
     assert lib.da_fused_delta_rows(32, 8) == 64      # GQA 4: two heads per 64-row tile
     assert lib.da_fused_delta_rows(8, 8) == 128      # MHA
     assert lib.da_fused_delta_rows(6, 3) == 64
-    assert lib.da_fused_delta_rows(40, 8) == 0       # GQA 5: not available
+    assert lib.da_fused_delta_rows(40, 8) == 128     # GQA 5: one head per 128-row tile
     assert lib.da_fused_delta_rows(6, 4) == 0 and lib.da_fused_delta_rows(0, 1) == 0
     s3 = _s3(128 * 32 * 128, 128, 32 * 128)
     q3 = _s3(32 * 4096 * 128, 4096 * 128, 128)
@@ -148,7 +148,7 @@ def test_fused_delta_rows_and_checks(lib):
     assert call(s_p=3900) == L.DA_ERR_INVALID_ARG                # s_p % gamma != 0
     assert call(s_p=4160) == L.DA_ERR_INVALID_ARG                # s_p > S
     assert call(dense=0) == L.DA_ERR_INVALID_ARG
-    assert call(Hq=40) == L.DA_ERR_INVALID_ARG                   # odd GQA ratio
+    assert call(Hq=40, gamma=256, s_p=3840) == L.DA_ERR_INVALID_ARG   # 256 does not divide 128
     assert call(dense=8) == L.DA_ERR_ALIGNMENT
     assert call(dout=8) == L.DA_ERR_ALIGNMENT
     assert call(s_p=0) == L.DA_OK

@@ -173,6 +173,7 @@ def test_adaptive_stride_path(gpu):
     (1, 4, 4, 1000, 64, 128, 192, 4),     # MHA: 128-row tiles, gamma 128
     (1, 6, 3, 777, 128, 32, 100, 0),      # GQA 2
     (1, 8, 2, 600, 128, 1, 128, 16),      # gamma 1: every row before the tail is an anchor
+    (2, 10, 2, 1100, 128, 64, 256, 16),   # GQA 5 (Qwen3): one head per 128-row tile
 ])
 def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
     """Kernel (3) fused into kernel (1)'s epilogue (kernel (2) first) gives the
@@ -194,9 +195,9 @@ def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
     assert_close(np64(a), ref, what=f"fused B{B} H{H}/{Hkv} S{S} g{gamma}")
 
 
-def test_fused_delta_not_taken_for_odd_gqa(gpu):
-    # GQA 5 (Qwen3 geometry): no fused epilogue, the three-kernel path runs
+def test_unfused_when_gamma_exceeds_the_tile(gpu):
+    # gamma 128 with GQA 4 (64-row tiles): the three-kernel path runs
     from delta_attention import ops
-    assert ops.fused_delta_rows(10, 2) == 0
-    got, ref, _ = _layer(1, 10, 2, 1024, 128, 64, 256, 16, seed=3)
-    assert_close(got, ref, what="gqa5")
+    assert ops.fused_delta_rows(8, 2) % 128 != 0
+    got, ref, _ = _layer(1, 8, 2, 1024, 128, 128, 256, 16, seed=3)
+    assert_close(got, ref, what="gamma 128, gqa 4")
