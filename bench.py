@@ -63,6 +63,11 @@ def parse():
                    help="q ~ N(0,1) without the d^-0.5 factor (the Qwen3 recipe)")
     p.add_argument("--workload", type=str, default="",
                    help="name recorded in config.workload (default: derived from the shape)")
+    p.add_argument("--model", action="store_true",
+                   help="full random-init Llama-3.1-8B-architecture prefill of --seq random token "
+                        "ids with delta attention in every layer: time to first token and the "
+                        "attention kernels' share (one JSON line; --steps/--warmup count prefills)")
+    p.add_argument("--layers", type=int, default=32, help="decoder layers of --model")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -237,6 +242,70 @@ def prologue(a, dev):
         "config": {"batch": B, "seq_len": S, "heads": H, "kv_heads": Hkv, "head_dim": D}}), flush=True)
 
 
+def model_prefill(a, dev):
+    """Time to first token of a random-init Llama-3.1-8B-architecture model
+    (32 layers, hidden 4096, 32/8 heads, MLP 14336, vocab 128256, bf16 weights
+    ~ N(0, 0.02)) on a.seq random token ids: embedding, every decoder layer
+    (projections, fused RoPE, delta attention, o_proj, fused add+RMSNorm,
+    SwiGLU MLP), final norm, lm_head on the last position and the greedy token."""
+    import torch
+    from delta_attention import ops
+    from delta_attention.model import LlamaConfig, random_llama
+    from delta_attention.timing import Timer
+    from oracle import delta_oracle as O
+    cfg = LlamaConfig(num_hidden_layers=a.layers, delta_lambda=a.gamma, sliding_window=a.window,
+                      sink_tokens=a.sink)
+    B, S = a.batch, a.seq
+    t0 = time.perf_counter()
+    model = random_llama(cfg, dev, torch.bfloat16, seed=a.seed)
+    torch.cuda.synchronize()
+    init_s = time.perf_counter() - t0
+    g = torch.Generator(device=dev).manual_seed(a.seed + 1)
+    ids = torch.randint(0, cfg.vocab_size, (B, S), device=dev, generator=g)
+    for _ in range(a.warmup):
+        model.prefill_next_token(ids)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        tok = model.prefill_next_token(ids)
+    torch.cuda.synchronize()
+    ttft = (time.perf_counter() - t0) / a.steps * 1e3
+    timer = Timer()
+    model.prefill_next_token(ids, timer)
+    parts = {k: round(v, 3) for k, v in timer.totals().items()}
+    timed_total = sum(parts.values())
+    H, Hkv, D, L = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.num_hidden_layers
+    cut_n, s_p, n_anchor = ops.anchor_layout(S, a.gamma)
+    counts = O.sparse_row_counts(S, a.window, a.sink)
+    rows = ops.fused_delta_rows(H, Hkv)
+    f_sparse = 4.0 * D * H * B * float(counts[:s_p].sum() if rows and rows % a.gamma == 0 else counts.sum())
+    f_attn = L * (f_sparse + O.flops_qsparse(B, H, D, O.selected_rows(S, a.gamma)))
+    hid, inter = cfg.hidden_size, cfg.intermediate_size
+    per_tok = 2 * (hid * (H + 2 * Hkv) * D + H * D * hid + 3 * hid * inter)
+    f_gemm = L * per_tok * B * S + 2 * B * hid * cfg.vocab_size
+    attn_ms = parts.get("attention_kernels", 0.0)
+    gemm_ms = sum(parts.get(k, 0.0) for k in ("qkv_gemm", "o_gemm", "mlp_gemm", "lm_head"))
+    line = {
+        "metric": "llama-3.1-8b-architecture prefill time to first token at 128K",
+        "value": round(ttft, 2), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "higher_is_better": False, "dtype": "bf16",
+        "data": "synthetic (random token ids, weights ~ N(0, 0.02) per the reference's _init_weights)",
+        "config": {"workload": "llama-3.1-8b-architecture causal LM prefill, delta attention in every layer",
+                   "layers": L, "batch": B, "seq_len": S, "window": a.window, "sink": a.sink,
+                   "gamma": a.gamma, "params": sum(p.numel() for p in model.parameters()),
+                   "rope_scaling": cfg.rope_scaling, "parallelism": "none (1 GPU)"},
+        "attention_share": round(attn_ms / timed_total, 4),
+        "tokens_per_s": round(B * S / (ttft * 1e-3), 1),
+        "breakdown_ms": parts, "breakdown_total_ms": round(timed_total, 2),
+        "flop": {"attention": f_attn, "gemm": f_gemm},
+        "tflops": {"attention_kernels": round(f_attn / attn_ms / 1e9, 1) if attn_ms else None,
+                   "gemm": round(f_gemm / gemm_ms / 1e9, 1) if gemm_ms else None,
+                   "model": round((f_attn + f_gemm) / (ttft * 1e-3) / 1e12, 1)},
+        "first_token": int(tok[0]), "init_s": round(init_s, 2),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def load_traffic(name):
     """HBM bytes per launch of `name` from the committed rocprofv3 PMC summary."""
     path = os.path.join(REPO, "profiles", "hbm_traffic.json")
@@ -268,6 +337,9 @@ def main():
     torch.cuda.set_device(dev)
     if a.prologue:
         prologue(a, dev)
+        return
+    if a.model:
+        model_prefill(a, dev)
         return
     B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
     scale = D ** -0.5

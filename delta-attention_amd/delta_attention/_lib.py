@@ -36,6 +36,8 @@ EXPORTS = (
     "da_qsparse_attn_fwd",
     "da_delta_add",
     "da_rope_qk",
+    "da_add_rmsnorm",
+    "da_swiglu",
     "da_build_target",
 )
 
@@ -99,6 +101,11 @@ def lib() -> ctypes.CDLL:
     L.da_rope_qk.restype = _i
     L.da_rope_qk.argtypes = [_vp, _p3, _i, _vp, _p3, _i, _i, _i, _i, _vp, _vp,
                              ctypes.POINTER(ctypes.c_int64), _vp, _vp, _f, _i, _vp]
+    L.da_add_rmsnorm.restype = _i
+    L.da_add_rmsnorm.argtypes = [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i, _f,
+                                 _i, _vp]
+    L.da_swiglu.restype = _i
+    L.da_swiglu.argtypes = [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i, _i, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
     _lib = L

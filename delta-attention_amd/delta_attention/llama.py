@@ -20,6 +20,7 @@ from torch import nn
 
 from . import ops
 from .delta_kernel import attention as qsa_kernel
+from .timing import region
 
 
 class LlamaRMSNorm(nn.Module):
@@ -38,13 +39,36 @@ class LlamaRMSNorm(nn.Module):
         return self.weight.to(dt) * x.to(dt)
 
 
+def llama3_inv_freq(inv_freq: torch.Tensor, factor: float = 8.0, low_freq_factor: float = 1.0,
+                    high_freq_factor: float = 4.0,
+                    original_max_position_embeddings: int = 8192) -> torch.Tensor:
+    """Llama 3.1's RoPE frequency scaling (the "llama3" rope type the
+    reference's LlamaRotaryEmbedding takes from the model config,
+    llama.py:83-127): wavelengths longer than original/low_freq_factor are
+    divided by `factor`, shorter than original/high_freq_factor kept, and the
+    band between interpolated linearly in original/wavelength."""
+    low_wl = original_max_position_embeddings / low_freq_factor
+    high_wl = original_max_position_embeddings / high_freq_factor
+    wavelen = 2 * torch.pi / inv_freq
+    scaled = torch.where(wavelen > low_wl, inv_freq / factor, inv_freq)
+    smooth = (original_max_position_embeddings / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor)
+    smoothed = (1 - smooth) * scaled / factor + smooth * scaled
+    medium = (wavelen >= high_wl) & (wavelen <= low_wl)
+    return torch.where(medium, smoothed, scaled)
+
+
 def rope_cos_sin(position_ids: torch.Tensor, head_dim: int, theta: float,
-                 dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+                 dtype: torch.dtype, rope_scaling: Optional[dict] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Default RoPE tables for position_ids [b, s] -> cos/sin [b, s, head_dim]:
     inv_freq = theta^(-2i/d), angles in float32, emb = cat(freqs, freqs)
-    (llama.py:129-158)."""
+    (llama.py:129-158). rope_scaling {"rope_type": "llama3", factor, ...}
+    applies llama3_inv_freq."""
     inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64,
                                              device=position_ids.device).float() / head_dim))
+    if rope_scaling:
+        kw = dict(rope_scaling)
+        assert kw.pop("rope_type", "llama3") == "llama3", rope_scaling
+        inv_freq = llama3_inv_freq(inv_freq, **kw)
     freqs = position_ids[..., None].float() * inv_freq[None, None, :]
     emb = torch.cat((freqs, freqs), dim=-1)
     return emb.cos().to(dtype), emb.sin().to(dtype)
@@ -223,7 +247,7 @@ class LlamaAttention(nn.Module):
         """(q_norm weight, k_norm weight, eps) applied before RoPE, or Nones."""
         return None, None, 1e-6
 
-    def _qkv_rope(self, hidden_states, hidden_shape, cos, sin):
+    def _qkv_rope(self, hidden_states, hidden_shape, cos, sin, timer=None):
         """Projections, then the fused prologue kernel (optional per-head q/k
         RMSNorm + RoPE) in place on the [b, s, h, d] projection outputs; returns
         [b, h, s, d] views, the layout the attention kernels read without copies."""
@@ -233,11 +257,13 @@ class LlamaAttention(nn.Module):
             q, k, v = self._qkv(hidden_states, hidden_shape)
             q, k = apply_rotary_pos_emb(q, k, cos, sin)
             return q, k, v
-        q = self.q_proj(hidden_states).view(hidden_shape)
-        k = self.k_proj(hidden_states).view(hidden_shape)
-        v = self.v_proj(hidden_states).view(hidden_shape)
-        qw, kw, eps = self._qk_norm()
-        ops.rope_qk(q, k, cos, sin, q_norm_w=qw, k_norm_w=kw, eps=eps)
+        with region(timer, "qkv_gemm"):
+            q = self.q_proj(hidden_states).view(hidden_shape)
+            k = self.k_proj(hidden_states).view(hidden_shape)
+            v = self.v_proj(hidden_states).view(hidden_shape)
+        with region(timer, "rope_prologue"):
+            qw, kw, eps = self._qk_norm()
+            ops.rope_qk(q, k, cos, sin, q_norm_w=qw, k_norm_w=kw, eps=eps)
         return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
 
     def forward(self, hidden_states, position_embeddings, attention_mask=None,
@@ -247,7 +273,9 @@ class LlamaAttention(nn.Module):
         input_shape = hidden_states.shape[:-1]
         hidden_shape = (*input_shape, -1, self.head_dim)
         cos, sin = position_embeddings
-        query_states, key_states, value_states = self._qkv_rope(hidden_states, hidden_shape, cos, sin)
+        timer = kwargs.get("timer")
+        query_states, key_states, value_states = self._qkv_rope(hidden_states, hidden_shape, cos, sin,
+                                                                timer)
         if past_key_value is not None:
             key_states, value_states = past_key_value.update(
                 key_states, value_states, self.layer_idx,
@@ -257,10 +285,12 @@ class LlamaAttention(nn.Module):
             raise NotImplementedError(
                 f"attention implementation {impl!r} is not part of the MI355X delta path "
                 "(use 'window')")
-        attn_output, attn_weights = self.delta_forward(
-            self, query_states, key_states, value_states, attention_mask,
-            dropout=0.0 if not self.training else self.attention_dropout, scaling=self.scaling)
+        with region(timer, "attention_kernels"):
+            attn_output, attn_weights = self.delta_forward(
+                self, query_states, key_states, value_states, attention_mask,
+                dropout=0.0 if not self.training else self.attention_dropout, scaling=self.scaling)
         assert attn_output.shape[-2] == self.config.num_attention_heads, attn_output.shape
         b, s, _, _ = attn_output.size()
         attn_output = attn_output.reshape(b, s, -1)
-        return self.o_proj(attn_output), attn_weights
+        with region(timer, "o_gemm"):
+            return self.o_proj(attn_output), attn_weights

@@ -1,0 +1,184 @@
+"""Llama causal LM with delta attention in every layer, for the full-model
+prefill (time to first token): the reference's LlamaMLP, LlamaDecoderLayer,
+LlamaModel and LlamaForCausalLM (delta_attention/llama.py:195-215, 917-1004,
+1006-1029, 1111-1145, 1455-1470), random-initialised as its `_init_weights`
+does (normal(0, initializer_range) for every linear and embedding weight,
+RMSNorm weights 1).
+
+Compute: projections and the MLP GEMMs are torch matmuls (hipBLASLt); the
+attention layer is `LlamaAttention` (fused RoPE prologue + the delta-attention
+kernels); every residual add is fused into the RMSNorm that follows it
+(`ops.add_rmsnorm`), and the SwiGLU gate is one element-wise kernel
+(`ops.swiglu`). A decoder layer therefore hands on (branch output, residual)
+and the next norm forms their sum.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+from torch import nn
+
+from . import ops
+from .llama import LlamaAttention, LlamaRMSNorm, rope_cos_sin
+from .timing import Timer, region as _region
+
+
+@dataclass
+class LlamaConfig:
+    """Llama-3.1-8B architecture plus the delta-attention pipeline knobs."""
+    vocab_size: int = 128256
+    hidden_size: int = 4096
+    intermediate_size: int = 14336
+    num_hidden_layers: int = 32
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    rope_theta: float = 500000.0
+    rope_scaling: Optional[dict] = field(default_factory=lambda: {
+        "rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+        "original_max_position_embeddings": 8192})
+    rms_norm_eps: float = 1e-5
+    initializer_range: float = 0.02
+    attention_bias: bool = False
+    mlp_bias: bool = False
+    attention_dropout: float = 0.0
+    _attn_implementation: str = "window"
+    mode: str = "delta"
+    delta_lambda: int = 64
+    sliding_window: int = 2048
+    sink_tokens: int = 128
+    stride_policy: str = "fixed"
+    log_drift: bool = False
+
+
+class LlamaMLP(nn.Module):
+    """down_proj(silu(gate_proj(x)) * up_proj(x)) (llama.py:195-215)."""
+
+    def __init__(self, config):
+        super().__init__()
+        bias = getattr(config, "mlp_bias", False)
+        self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=bias)
+        self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=bias)
+        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=bias)
+
+    def forward(self, x: torch.Tensor, timer: Optional[Timer] = None) -> torch.Tensor:
+        with _region(timer, "mlp_gemm"):
+            g = self.gate_proj(x)
+            u = self.up_proj(x)
+        with _region(timer, "swiglu"):
+            if g.dtype in (torch.bfloat16, torch.float16):
+                a = ops.swiglu(g, u, out=g)     # in place over the gate
+            else:
+                a = nn.functional.silu(g) * u
+        del u
+        with _region(timer, "mlp_gemm"):
+            return self.down_proj(a)
+
+
+def _norm(norm: LlamaRMSNorm, x: torch.Tensor, residual: Optional[torch.Tensor], timer):
+    """(norm(x + residual), x + residual) with the add fused into the norm."""
+    with _region(timer, "norm"):
+        if x.dtype in (torch.bfloat16, torch.float16) and x.shape[-1] in (2048, 4096, 5120, 8192):
+            if residual is None:
+                return ops.add_rmsnorm(x, norm.weight, norm.variance_epsilon), x
+            return ops.add_rmsnorm(x, norm.weight, norm.variance_epsilon, residual=residual,
+                                   residual_out=residual)
+        h = x if residual is None else residual + x
+        return norm(h), h
+
+
+class LlamaDecoderLayer(nn.Module):
+    attn_cls = LlamaAttention  # model-family hook (qwen3.py overrides)
+
+    def __init__(self, config, layer_idx: int):
+        super().__init__()
+        self.self_attn = self.attn_cls(config, layer_idx)
+        self.mlp = LlamaMLP(config)
+        self.input_layernorm = LlamaRMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.post_attention_layernorm = LlamaRMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward_fused(self, hidden_states: torch.Tensor, residual: Optional[torch.Tensor],
+                      position_embeddings, timer: Optional[Timer] = None):
+        """The layer on the split residual stream: its input is
+        hidden_states + residual (residual None: hidden_states alone), its
+        output (mlp_out, residual) with the same meaning."""
+        x, residual = _norm(self.input_layernorm, hidden_states, residual, timer)
+        a, _ = self.self_attn(x, position_embeddings, timer=timer)
+        x, residual = _norm(self.post_attention_layernorm, a, residual, timer)
+        return self.mlp(x, timer), residual
+
+    def forward(self, hidden_states: torch.Tensor, position_embeddings, **kwargs):
+        """(hidden_states_out,) as llama.py:917-1004 returns it."""
+        out, residual = self.forward_fused(hidden_states, None, position_embeddings)
+        return (residual + out,)
+
+
+class LlamaModel(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([LlamaDecoderLayer(config, i) for i in range(config.num_hidden_layers)])
+        self.norm = LlamaRMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def rotary(self, position_ids: torch.Tensor, dtype: torch.dtype):
+        c = self.config
+        return rope_cos_sin(position_ids, c.head_dim, c.rope_theta, dtype, c.rope_scaling)
+
+    def forward(self, input_ids: torch.Tensor, timer: Optional[Timer] = None) -> torch.Tensor:
+        """input_ids [b, s] -> final hidden states [b, s, hidden] (llama.py:1148-1300)."""
+        with _region(timer, "embed"):
+            h = self.embed_tokens(input_ids)
+            pos = torch.arange(input_ids.shape[1], device=input_ids.device)[None]
+            cos, sin = self.rotary(pos, h.dtype)
+        residual = None
+        for layer in self.layers:
+            h, residual = layer.forward_fused(h, residual, (cos, sin), timer)
+        out, _ = _norm(self.norm, h, residual, timer)
+        return out
+
+
+class LlamaForCausalLM(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        self.config = config
+        self.model = LlamaModel(config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+
+    @torch.inference_mode()
+    def prefill_next_token(self, input_ids: torch.Tensor, timer: Optional[Timer] = None) -> torch.Tensor:
+        """The prefill of generation: the whole prompt through the model, then
+        lm_head on the last position only and the greedy next token
+        (sample.py:144, 178-179). -> [b] token ids."""
+        h = self.model(input_ids, timer)
+        with _region(timer, "lm_head"):
+            logits = self.lm_head(h[:, -1])
+            return logits.argmax(-1)
+
+
+def init_weights_(model: nn.Module, std: float, seed: int = 0) -> nn.Module:
+    """normal(0, std) for every linear and embedding weight, zero biases, RMSNorm
+    weights 1 (llama.py:1020-1029), drawn on the model's device."""
+    dev = next(model.parameters()).device
+    g = torch.Generator(device=dev).manual_seed(seed)
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, (nn.Linear, nn.Embedding)):
+                m.weight.normal_(0.0, std, generator=g)
+                if getattr(m, "bias", None) is not None:
+                    m.bias.zero_()
+            elif isinstance(m, LlamaRMSNorm):
+                m.weight.fill_(1.0)
+    return model
+
+
+def random_llama(config: LlamaConfig, device="cuda", dtype=torch.bfloat16, seed: int = 0) -> LlamaForCausalLM:
+    """Build on the meta device, materialise on `device` in `dtype`, initialise;
+    an inference model (no gradients)."""
+    with torch.device("meta"):
+        model = LlamaForCausalLM(config)
+    model = model.to_empty(device=device).to(dtype)
+    return init_weights_(model, config.initializer_range, seed).eval().requires_grad_(False)

@@ -286,6 +286,67 @@ def rope_qk(q: Optional[torch.Tensor], k: Optional[torch.Tensor], cos: torch.Ten
 
 
 # ---------------------------------------------------------------------------
+# decoder-layer element-wise kernels (full-model prefill)
+
+def _rows2d(t: torch.Tensor) -> Tuple[int, int]:
+    """(rows, row stride) of a tensor whose last dim is contiguous and whose
+    leading dims collapse to one row index."""
+    assert t.stride(-1) == 1, "last dim must be contiguous"
+    n = t.shape[-1]
+    rows = t.numel() // n if n else 0
+    if t.dim() == 1:
+        return 1, n
+    lead = t.reshape(-1, n) if rows else t
+    assert lead.data_ptr() == t.data_ptr(), "leading dims must collapse without a copy"
+    return rows, lead.stride(0)
+
+
+def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, *,
+                residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                residual_out: Optional[torch.Tensor] = None):
+    """LlamaRMSNorm (llama.py:69-74) of x, or of rnd(x + residual) when a
+    residual is given (the decoder layer's add, llama.py:968-979).
+    Returns y, or (y, h) with h = x + residual (written to residual_out,
+    default a new tensor)."""
+    n = x.shape[-1]
+    dev = _on_gpu(x, weight)
+    rows, xs = _rows2d(x)
+    if out is None:
+        out = torch.empty_like(x)
+    assert out.shape == x.shape and out.dtype == x.dtype
+    _, ys = _rows2d(out)
+    w = weight.to(device=dev, dtype=x.dtype).contiguous()
+    h = None
+    rs = hs = 0
+    if residual is not None:
+        assert residual.shape == x.shape and residual.dtype == x.dtype
+        _, rs = _rows2d(residual)
+        h = torch.empty_like(x) if residual_out is None else residual_out
+        _, hs = _rows2d(h)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_add_rmsnorm(_ptr(x), xs, _ptr(residual), rs, _ptr(h), hs, _ptr(out), ys,
+                                    _ptr(w), rows, n, float(eps), _code(x), _stream(dev))
+    L.check(rc, "da_add_rmsnorm")
+    return out if residual is None else (out, h)
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(gate) * up with the reference's bf16 rounding per op (llama.py:212-213)."""
+    assert gate.shape == up.shape and gate.dtype == up.dtype
+    dev = _on_gpu(gate, up)
+    rows, gs = _rows2d(gate)
+    _, us = _rows2d(up)
+    if out is None:
+        out = torch.empty_like(gate)
+    _, os_ = _rows2d(out)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_swiglu(_ptr(gate), gs, _ptr(up), us, _ptr(out), os_, rows, gate.shape[-1],
+                               _code(gate), _stream(dev))
+    L.check(rc, "da_swiglu")
+    return out
+
+
+# ---------------------------------------------------------------------------
 # the composed layer prefill (kernels 1 -> 2 -> 3)
 
 def anchor_layout(s: int, gamma: int) -> Tuple[int, int, int]:

@@ -172,6 +172,28 @@ int da_delta_add(const void* sparse, const int64_t sp_str[3],
                  int B, int H, int D, int dtype, void* stream);
 
 /*
+ * Decoder-layer residual add + RMSNorm over rows of n elements (n in {2048,
+ * 4096, 5120, 8192}), replacing `residual + hidden_states` followed by
+ * LlamaRMSNorm (delta_attention/llama.py:69-74, :968-979):
+ *   residual == NULL: y = rnd(w * rnd(x * rsqrt(mean(x^2) + eps)))
+ *   otherwise:        h = rnd(x + residual) is written to h, then y = norm(h).
+ * One rounding to `dtype` per torch op; fp32 inside. Row strides in elements;
+ * in-place use (h == x or h == residual, y == x) is allowed.
+ */
+int da_add_rmsnorm(const void* x, int64_t x_stride, const void* residual, int64_t r_stride,
+                   void* h, int64_t h_stride, void* y, int64_t y_stride,
+                   const void* weight, int64_t rows, int n, float eps,
+                   int dtype, void* stream);
+
+/*
+ * SwiGLU gate of LlamaMLP (delta_attention/llama.py:212-213):
+ * out = rnd(rnd(silu(gate)) * up), silu(g) = g / (1 + exp(-g)) in fp32, over
+ * rows of n elements (n % 8 == 0; row strides in elements).
+ */
+int da_swiglu(const void* gate, int64_t g_stride, const void* up, int64_t u_stride,
+              void* out, int64_t o_stride, int64_t rows, int n, int dtype, void* stream);
+
+/*
  * Attention prologue, in place: optional per-head RMSNorm (weights q_norm_w /
  * k_norm_w of length D, NULL = no norm; Qwen3, delta_attention/qwen3.py:37-43 and
  * llama.py:60-74) followed by rotary position embedding (rotate_half

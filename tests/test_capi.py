@@ -153,3 +153,20 @@ def test_fused_delta_rows_and_checks(lib):
     assert call(dout=8) == L.DA_ERR_ALIGNMENT
     assert call(s_p=0) == L.DA_OK
     assert call(S=0, s_p=0) == L.DA_OK
+
+
+def test_norm_and_swiglu_checks(lib):
+    P = ctypes.c_void_p
+    assert lib.da_add_rmsnorm(P(16), 4096, None, 0, None, 0, P(16), 4096, P(16), 8, 3000, 1e-5,
+                              L.DA_BF16, None) == L.DA_ERR_INVALID_ARG      # unsupported row length
+    assert lib.da_add_rmsnorm(P(16), 4096, P(16), 4096, None, 0, P(16), 4096, P(16), 8, 4096, 1e-5,
+                              L.DA_BF16, None) == L.DA_ERR_INVALID_ARG      # residual without h
+    assert lib.da_add_rmsnorm(P(24), 4096, None, 0, None, 0, P(16), 4096, P(16), 8, 4096, 1e-5,
+                              L.DA_BF16, None) == L.DA_ERR_ALIGNMENT
+    assert lib.da_add_rmsnorm(P(16), 4096, None, 0, None, 0, P(16), 4096, P(16), 0, 4096, 1e-5,
+                              L.DA_BF16, None) == L.DA_OK                   # no rows
+    assert lib.da_add_rmsnorm(P(16), 4096, None, 0, None, 0, P(16), 4096, P(16), 8, 4096, 1e-5,
+                              9, None) == L.DA_ERR_DTYPE
+    assert lib.da_swiglu(P(16), 64, P(16), 64, P(16), 64, 8, 60, L.DA_BF16, None) == L.DA_ERR_INVALID_ARG
+    assert lib.da_swiglu(P(16), 64, P(8), 64, P(16), 64, 8, 64, L.DA_BF16, None) == L.DA_ERR_ALIGNMENT
+    assert lib.da_swiglu(P(16), 64, P(16), 64, P(16), 64, 0, 64, L.DA_BF16, None) == L.DA_OK
