@@ -86,7 +86,7 @@ struct AttnArgs {
   const int64_t* q_rows;
   const int64_t* row_last;
   int64_t rl_b;
-  int chunk;        // keys per split (multiple of BN)
+  int chunk;        // query-sparse mode: key tiles of the tile list per split item
   int n_splits;
   float* part_o;    // [item][BM][D]
   float* part_ml;   // [item][2][BM]  (running max, row sum)
@@ -122,6 +122,19 @@ struct Tile {
   static __device__ __forceinline__ int kswz(int row) { return sigma32(row & 31) & (DCH - 1); }
   static __device__ __forceinline__ int vswz(int row) { return (4 * (row & 3)) & (DCH - 1); }
 };
+
+// Key tiles a row tile visits, in order: the sink tiles [0, ceil(min(sink,
+// lo_min, hi_max + 1) / BN)), then the tiles from the one holding lo_min to the
+// one holding hi_max (lo_min: the smallest first window key of the tile's
+// rows; without a window lo_min = 0 and the list is tiles 0 .. hi_max / BN).
+__device__ __forceinline__ void tile_list(int hi_max, int lo_min, int sink, int& n_first,
+                                          int& second_t0, int& n_second) {
+  int sink_end = min(min(sink, lo_min), hi_max + 1);
+  if (sink_end < 0) sink_end = 0;
+  n_first = (sink_end + BN - 1) / BN;
+  second_t0 = max(max(lo_min, 0) / BN, n_first);
+  n_second = hi_max >= 0 ? max(0, hi_max / BN - second_t0 + 1) : 0;
+}
 
 // s_waitcnt immediate (gfx9 encoding) that waits until at most `vm` vector
 // memory operations are outstanding; LDS and export counters are not waited on.
@@ -200,15 +213,17 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     hi = valid ? irow : -1;
     lo = (irow / a.q_block) * a.q_block + a.q_block - a.window;
   } else {
+    // row_last == NULL: every row sees all keys (a decode row at the end of
+    // the cache); window > 0: the row sees sinks + its last `window` keys
     qrow = a.q_rows ? (int)min(max(a.q_rows[irow], (int64_t)0), (int64_t)(a.n_q - 1)) : irow;
-    int64_t lim = a.row_last[(int64_t)b * a.rl_b + irow];
+    int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + irow] : (int64_t)a.n_kv - 1;
     if (lim > a.n_kv - 1) lim = a.n_kv - 1;
     hi = valid ? (int)(lim < -1 ? -1 : lim) : -1;
-    lo = 0;
+    lo = a.window > 0 ? hi - a.window + 1 : 0;
   }
   int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
   int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
-  const int sink = KSPARSE ? a.sink : 0;
+  const int sink = (KSPARSE || a.window > 0) ? a.sink : 0;
 
   // ---- tile-wide bounds (valid rows only) ----
 #pragma unroll
@@ -234,25 +249,16 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     lo_max = max(lo_max, red[3][i]);
   }
 
-  // ---- key tiles to visit ----
+  // ---- key tiles to visit: the tile list, or (query-sparse mode) this
+  //      split's `chunk` tiles of it ----
   int n_first, n_second, second_t0;
-  if (KSPARSE) {
-    // sink tiles [0, ceil(min(sink, lo_min, hi_max + 1) / BN)), then window
-    // tiles from the tile holding lo_min up to the tile holding hi_max.
-    int sink_end = min(min(sink, lo_min), hi_max + 1);
-    if (sink_end < 0) sink_end = 0;
-    n_first = (sink_end + BN - 1) / BN;
-    second_t0 = max(max(lo_min, 0) / BN, n_first);
-    n_second = hi_max >= 0 ? max(0, hi_max / BN - second_t0 + 1) : 0;
-  } else {
-    const int c0 = split * a.chunk;
-    if (c0 > hi_max) return;   // nothing visible: the merge skips this split
-    const int c1 = min(c0 + a.chunk, hi_max + 1);
-    n_first = 0;
-    second_t0 = c0 / BN;
-    n_second = (c1 - 1) / BN - second_t0 + 1;
+  tile_list(hi_max, lo_min, sink, n_first, second_t0, n_second);
+  int nt = n_first + n_second, t_off = 0;
+  if (!KSPARSE) {
+    t_off = split * a.chunk;
+    if (t_off >= nt) return;   // past the list: the merge skips this split
+    nt = min(a.chunk, nt - t_off);
   }
-  const int nt = n_first + n_second;
 
   constexpr size_t esz = sizeof(T);
   const char* kbase = (const char*)a.k + ((int64_t)b * a.ks_b + (int64_t)hk * a.ks_h) * esz;
@@ -285,7 +291,8 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     voff[c] = (uint32_t)row * vrow_b + (uint32_t)((pc ^ TL::vswz(row)) * 16);
   }
   auto tile_n0 = [&](int t) -> int {
-    return (t < n_first ? t : second_t0 + (t - n_first)) * BN;
+    const int u = t + t_off;
+    return (u < n_first ? u : second_t0 + (u - n_first)) * BN;
   };
   // DMA of key tile t into LDS stage `slot` (K) / (V); the buffer covers the
   // rows from the tile start to the last key (n0 <= hi_max < n_kv), so the
@@ -641,6 +648,7 @@ struct MergeArgs {
   const int64_t* row_last;
   int64_t rl_b;
   int n_rows, G, Hkv, n_kv, n_mtiles, n_splits, chunk;
+  int window, sink;
   const float* part_o;
   const float* part_ml;
   int epi, n_anchor, n_q;
@@ -654,7 +662,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   using E = Elt<T>;
   constexpr int CPR = D / 8;   // 8-column chunks per row
-  __shared__ int s_hmax[4];
+  __shared__ int s_hmax[4], s_lmin[4];
   const int tile = blockIdx.x;
   const int mt = tile % a.n_mtiles;
   const int bh = tile / a.n_mtiles;
@@ -663,22 +671,32 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   const int tid = threadIdx.x;
   const int G = a.G;
 
-  // Same hi_max as the split kernel saw, hence the same set of written splits.
-  int my_hmax = -1;
+  // Same tile list as the split kernel saw, hence the same set of written splits.
+  int my_hmax = -1, my_lmin = 0x7fffffff;
   if (tid < BM) {
     const int mflat = mt * BM + tid;
     if (mflat < a.n_rows * G) {
-      int64_t lim = a.row_last[(int64_t)b * a.rl_b + mflat / G];
+      int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + mflat / G] : (int64_t)a.n_kv - 1;
       if (lim > a.n_kv - 1) lim = a.n_kv - 1;
       my_hmax = (int)(lim < -1 ? -1 : lim);
+      my_lmin = a.window > 0 ? my_hmax - a.window + 1 : 0;
     }
   }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) my_hmax = max(my_hmax, __shfl_xor(my_hmax, off));
-  if ((tid & 63) == 0) s_hmax[tid >> 6] = my_hmax;
+  for (int off = 32; off >= 1; off >>= 1) {
+    my_hmax = max(my_hmax, __shfl_xor(my_hmax, off));
+    my_lmin = min(my_lmin, __shfl_xor(my_lmin, off));
+  }
+  if ((tid & 63) == 0) {
+    s_hmax[tid >> 6] = my_hmax;
+    s_lmin[tid >> 6] = my_lmin;
+  }
   __syncthreads();
   const int hi_max = max(max(s_hmax[0], s_hmax[1]), max(s_hmax[2], s_hmax[3]));
-  const int nsv = hi_max >= 0 ? hi_max / a.chunk + 1 : 0;
+  const int lo_min = min(min(s_lmin[0], s_lmin[1]), min(s_lmin[2], s_lmin[3]));
+  int n_first, second_t0, n_second;
+  tile_list(hi_max, lo_min, a.window > 0 ? a.sink : 0, n_first, second_t0, n_second);
+  const int nsv = (n_first + n_second + a.chunk - 1) / a.chunk;
 
   const size_t esz = sizeof(T);
   for (int task = tid; task < BM * CPR; task += MTHR) {
@@ -753,23 +771,37 @@ struct QsparsePlan {
   size_t ws_bytes;
 };
 
-static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int Skv, int D) {
+// Split plan over the tile lists: `vis` bounds a row tile's list length, each
+// item takes `chunk` consecutive tiles of it; `target` items in total.
+static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int D, int target) {
   QsparsePlan p;
   const int G = Hq / Hkv;
   p.n_mtiles = (int)(((int64_t)n * G + BM - 1) / BM);
   const int64_t base = (int64_t)B * Hkv * p.n_mtiles;
-  const int nkt = (Skv + BN - 1) / BN;
-  // Aim for ~4096 split items (about half of them are empty for a causal row
-  // set), i.e. several equal-sized items per CU.
-  int64_t want = (4096 + base - 1) / base;
+  if (vis < 1) vis = 1;
+  int64_t want = (target + base - 1) / base;
   if (want < 1) want = 1;
-  if (want > nkt) want = nkt;
-  const int chunk_tiles = (int)((nkt + want - 1) / want);
-  p.chunk = chunk_tiles * BN;
-  p.n_splits = (nkt + chunk_tiles - 1) / chunk_tiles;
+  if (want > vis) want = vis;
+  p.chunk = (int)((vis + want - 1) / want);
+  p.n_splits = (int)((vis + p.chunk - 1) / p.chunk);
   p.n_items = (int)(base * p.n_splits);
   p.ws_bytes = (size_t)p.n_items * BM * (D + 2) * sizeof(float);
   return p;
+}
+
+// Causal selected rows: ~4096 items (about half of them past the end of a
+// causal row tile's list), several equal-sized items per CU.
+static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
+  return plan_qsparse(B, Hq, Hkv, n, (Skv + BN - 1) / BN, D, 4096);
+}
+
+// One decode row per batch at the end of the cache: its list is the sink
+// tiles plus the window tiles (all tiles without a window); ~1024 items.
+static QsparsePlan plan_decode(int B, int Hq, int Hkv, int n_keys, int D, int window, int sink) {
+  const int64_t all = (n_keys + BN - 1) / BN;
+  int64_t vis = all;
+  if (window > 0) vis = min(all, (int64_t)(min(sink, n_keys) + BN - 1) / BN + (window + BN - 1) / BN + 1);
+  return plan_qsparse(B, Hq, Hkv, 1, vis, D, 1024);
 }
 
 template <typename T, int D, int MODE>
@@ -900,10 +932,63 @@ extern "C" int da_sparse_attn_delta_fwd(const void* q, const void* k, const void
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }
 
+// Split kernel + merge for a plan (arguments already validated).
+static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const void* v,
+                       const int64_t* q_rows, const int64_t* row_last, int64_t rl_bstride,
+                       int n, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                       const int64_t q_str[3], const int64_t k_str[3], const int64_t v_str[3],
+                       void* o, const int64_t o_str[3],
+                       int epi, int n_anchor, void* delta, const int64_t d_str[3],
+                       int window, int sink, float sm_scale, void* workspace,
+                       size_t workspace_bytes, int dtype, void* stream) {
+  if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
+
+  AttnArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.o = nullptr;
+  a.qs_b = q_str[0]; a.qs_h = q_str[1]; a.qs_s = q_str[2];
+  a.ks_b = k_str[0]; a.ks_h = k_str[1]; a.ks_s = k_str[2];
+  a.vs_b = v_str[0]; a.vs_h = v_str[1]; a.vs_s = v_str[2];
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.Gs = a.G; a.n_hs = 1;
+  a.n_rows = n; a.n_q = Sq; a.n_kv = Skv;
+  a.n_mtiles = p.n_mtiles;
+  a.n_items = p.n_items;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.q_rows = q_rows; a.row_last = row_last; a.rl_b = rl_bstride;
+  a.chunk = p.chunk; a.n_splits = p.n_splits;
+  a.window = window; a.sink = sink;
+  a.part_o = (float*)workspace;
+  a.part_ml = (float*)workspace + (size_t)p.n_items * BM * D;
+
+  MergeArgs m = {};
+  m.q_rows = q_rows; m.row_last = row_last; m.rl_b = rl_bstride;
+  m.n_rows = n; m.n_q = Sq; m.G = a.G; m.Hkv = Hkv; m.n_kv = Skv; m.n_mtiles = p.n_mtiles;
+  m.n_splits = p.n_splits; m.chunk = p.chunk;
+  m.window = window; m.sink = sink;
+  m.part_o = a.part_o; m.part_ml = a.part_ml;
+  m.epi = epi; m.n_anchor = (epi == DA_EPI_DELTA || epi == DA_EPI_DENSE) ? n_anchor : 0;
+  m.o = o; m.os_b = o_str[0]; m.os_h = o_str[1]; m.os_s = o_str[2];
+  m.delta = delta;
+  if (d_str) { m.ds_b = d_str[0]; m.ds_h = d_str[1]; m.ds_a = d_str[2]; }
+
+  hipStream_t s = (hipStream_t)stream;
+  (void)hipGetLastError();
+  dispatch_attn<MODE_QSPARSE>(a, D, dtype, s);
+  const int n_tiles = B * Hkv * p.n_mtiles;
+  if (dtype == DA_BF16) {
+    if (D == 128) launch_merge<__bf16, 128>(m, n_tiles, s);
+    else launch_merge<__bf16, 64>(m, n_tiles, s);
+  } else {
+    if (D == 128) launch_merge<_Float16, 128>(m, n_tiles, s);
+    else launch_merge<_Float16, 64>(m, n_tiles, s);
+  }
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}
+
 extern "C" size_t da_qsparse_workspace_bytes(int B, int Hq, int Hkv, int n, int Skv, int D) {
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n < 1 || Skv < 1 || (D != 64 && D != 128))
     return 0;
-  return plan_qsparse(B, Hq, Hkv, n, Skv, D).ws_bytes;
+  return plan_rows(B, Hq, Hkv, n, Skv, D).ws_bytes;
 }
 
 extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
@@ -932,45 +1017,40 @@ extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
       !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
     return DA_ERR_ALIGNMENT;
   if (!kv_rows_ok(k_str, v_str)) return DA_ERR_INVALID_ARG;
-  const QsparsePlan p = plan_qsparse(B, Hq, Hkv, n, Skv, D);
+  const QsparsePlan p = plan_rows(B, Hq, Hkv, n, Skv, D);
+  return run_qsparse(p, q, k, v, q_rows, row_last, rl_bstride, n, B, Hq, Hkv, Sq, Skv, D,
+                     q_str, k_str, v_str, o, o_str, epi, n_anchor, delta, d_str, 0, 0,
+                     sm_scale, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" size_t da_decode_workspace_bytes(int B, int Hq, int Hkv, int n_keys, int D, int window,
+                                            int sink) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n_keys < 1 || (D != 64 && D != 128) ||
+      window < 0 || sink < 0)
+    return 0;
+  return plan_decode(B, Hq, Hkv, n_keys, D, window, sink).ws_bytes;
+}
+
+extern "C" int da_decode_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                                  int B, int Hq, int Hkv, int n_keys, int D,
+                                  const int64_t q_str[3], const int64_t k_str[3],
+                                  const int64_t v_str[3], const int64_t o_str[3],
+                                  int window, int sink, float sm_scale,
+                                  void* workspace, size_t workspace_bytes, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
+  if (n_keys < 0 || window < 0 || sink < 0) return DA_ERR_INVALID_ARG;
+  if (!q_str || !k_str || !v_str || !o_str) return DA_ERR_INVALID_ARG;
+  if (!q || !k || !v || !out) return DA_ERR_INVALID_ARG;
+  if (n_keys == 0) return DA_ERR_INVALID_ARG;   // a decode row has at least its own key
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
+      !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
+    return DA_ERR_ALIGNMENT;
+  if (!kv_rows_ok(k_str, v_str)) return DA_ERR_INVALID_ARG;
+  const QsparsePlan p = plan_decode(B, Hq, Hkv, n_keys, D, window, sink);
   if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
-
-  AttnArgs a = {};
-  a.q = q; a.k = k; a.v = v; a.o = nullptr;
-  a.qs_b = q_str[0]; a.qs_h = q_str[1]; a.qs_s = q_str[2];
-  a.ks_b = k_str[0]; a.ks_h = k_str[1]; a.ks_s = k_str[2];
-  a.vs_b = v_str[0]; a.vs_h = v_str[1]; a.vs_s = v_str[2];
-  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.Gs = a.G; a.n_hs = 1;
-  a.n_rows = n; a.n_q = Sq; a.n_kv = Skv;
-  a.n_mtiles = p.n_mtiles;
-  a.n_items = p.n_items;
-  a.scale_log2 = sm_scale * 1.4426950408889634f;
-  a.q_rows = q_rows; a.row_last = row_last; a.rl_b = rl_bstride;
-  a.chunk = p.chunk; a.n_splits = p.n_splits;
-  a.part_o = (float*)workspace;
-  a.part_ml = (float*)workspace + (size_t)p.n_items * BM * D;
-
-  MergeArgs m = {};
-  m.q_rows = q_rows; m.row_last = row_last; m.rl_b = rl_bstride;
-  m.n_rows = n; m.n_q = Sq; m.G = a.G; m.Hkv = Hkv; m.n_kv = Skv; m.n_mtiles = p.n_mtiles;
-  m.n_splits = p.n_splits; m.chunk = p.chunk;
-  m.part_o = a.part_o; m.part_ml = a.part_ml;
-  m.epi = epi; m.n_anchor = (epi == DA_EPI_DELTA || epi == DA_EPI_DENSE) ? n_anchor : 0;
-  m.o = o; m.os_b = o_str[0]; m.os_h = o_str[1]; m.os_s = o_str[2];
-  m.delta = delta;
-  if (d_str) { m.ds_b = d_str[0]; m.ds_h = d_str[1]; m.ds_a = d_str[2]; }
-
-  hipStream_t s = (hipStream_t)stream;
-  (void)hipGetLastError();
-  dispatch_attn<MODE_QSPARSE>(a, D, dtype, s);
-  const int n_tiles = B * Hkv * p.n_mtiles;
-  if (dtype == DA_BF16) {
-    if (D == 128) launch_merge<__bf16, 128>(m, n_tiles, s);
-    else launch_merge<__bf16, 64>(m, n_tiles, s);
-  } else {
-    if (D == 128) launch_merge<_Float16, 128>(m, n_tiles, s);
-    else launch_merge<_Float16, 64>(m, n_tiles, s);
-  }
-  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+  return run_qsparse(p, q, k, v, nullptr, nullptr, 0, 1, B, Hq, Hkv, 1, n_keys, D,
+                     q_str, k_str, v_str, out, o_str, DA_EPI_OUTPUT, 0, nullptr, nullptr,
+                     window, sink, sm_scale, workspace, workspace_bytes, dtype, stream);
 }

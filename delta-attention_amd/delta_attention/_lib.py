@@ -35,6 +35,8 @@ EXPORTS = (
     "da_qsparse_workspace_bytes",
     "da_qsparse_attn_fwd",
     "da_delta_add",
+    "da_decode_workspace_bytes",
+    "da_decode_attn_fwd",
     "da_rope_qk",
     "da_add_rmsnorm",
     "da_swiglu",
@@ -95,6 +97,11 @@ def lib() -> ctypes.CDLL:
                                       _i, _i, _i, _i, _i, _i, _i,
                                       _p3, _p3, _p3, _vp, _p3,
                                       _i, _i, _vp, _p3, _f, _vp, _sz, _i, _vp]
+    L.da_decode_workspace_bytes.restype = _sz
+    L.da_decode_workspace_bytes.argtypes = [_i, _i, _i, _i, _i, _i, _i]
+    L.da_decode_attn_fwd.restype = _i
+    L.da_decode_attn_fwd.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                     _p3, _p3, _p3, _p3, _i, _i, _f, _vp, _sz, _i, _vp]
     L.da_delta_add.restype = _i
     L.da_delta_add.argtypes = [_vp, _p3, _vp, _p3, _vp, _p3, _vp, _p3, _vp,
                                _i, _i, _i, _i, _i, _i, _i, _vp]

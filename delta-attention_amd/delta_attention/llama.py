@@ -234,6 +234,111 @@ class LlamaAttention(nn.Module):
         out = torch.cat((corrected, tail_dense), dim=1)
         return out.to(query_states.dtype)
 
+    # -- decode (llama.py:498-657) ---------------------------------------------------
+    def sdpa_rectangle_forward(self, module, query_states, key_states, value_states,
+                               attention_mask=None, dropout: float = 0.0, scaling: float = 1.0,
+                               **kwargs):
+        """Queries at the end of the KV cache: row i of s attends keys
+        0 .. n - s + i (llama.py:498-535) -> ([b, s, h, d], None). One-row
+        steps with decode_mode "sparse" / "delta" go to delta_decode_forward."""
+        b, h, s, d = query_states.size()
+        if s == 1 and getattr(self.config, "decode_mode", "dense") != "dense":
+            return self.delta_decode_forward(module, query_states, key_states, value_states,
+                                             scaling=scaling)
+        q, k, v = self._half(query_states, key_states, value_states)
+        n = k.size(2)
+        if s == 1:
+            out = ops.decode_attention(q, k, v, window=0, sink=0, sm_scale=float(scaling))
+        else:
+            mask = torch.arange(n - s, n, device=q.device, dtype=torch.int64)[None]
+            out = qsa_kernel(q, k, v, mask, float(scaling))
+        return out.transpose(1, 2).contiguous().to(query_states.dtype), None
+
+    @staticmethod
+    def _half(q, k, v):
+        if q.dtype == torch.float32:
+            return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+        return q, k, v
+
+    def _decode_sparse_row(self, q, k, v, scaling):
+        """One decode row over the sink tokens + the last sliding_window keys of
+        the cache, softmax over exactly that set (llama.py:537-549; every key
+        when the cache holds at most sink + window keys). GQA native."""
+        return ops.decode_attention(q, k, v, window=int(self.config.sliding_window),
+                                    sink=self._sink(), sm_scale=float(scaling))
+
+    def delta_decode_forward(self, module, query_states, key_states, value_states,
+                             scaling: float = 1.0, **kwargs):
+        """Decode step with sparse attention + cached delta correction
+        (llama.py:551-657). Per-layer state `_dec_state` = {last_delta, steps
+        since anchor, last_sparse, cos_hist}, reset for every new prompt.
+        Anchor when: no delta yet | fixed policy and steps >= gamma_dec | drift
+        policy and cos(sparse_t, sparse_{t-1}) < drift_threshold | drift_rel
+        and that cosine falls below mean - drift_k * std of the last 16 steps
+        (>= 8 of them) | steps >= gamma_dec_max. Anchors output the dense row
+        and refresh delta = dense - sparse; other steps output sparse + delta.
+        log_drift records per-step points in `_dec_drift_points`."""
+        assert query_states.size(0) == 1, "sparse/delta decode supports batch size 1 only"
+        mode = self.config.decode_mode
+        assert mode in ("sparse", "delta"), mode
+        q, k, v = self._half(query_states, key_states, value_states)
+        sparse_out = self._decode_sparse_row(q, k, v, scaling)
+        if mode == "sparse":
+            return sparse_out.transpose(1, 2).contiguous().to(query_states.dtype), None
+
+        st = getattr(self, "_dec_state", None) or {
+            "last_delta": None, "steps": 0, "last_sparse": None, "cos_hist": []}
+        log_drift = bool(getattr(self.config, "log_drift", False))
+        policy = getattr(self.config, "refresh_policy", "fixed")
+
+        def _cos(a, b):
+            return torch.nn.functional.cosine_similarity(
+                a.flatten().float(), b.flatten().float(), dim=0).item()
+
+        if st["last_delta"] is None:
+            anchor, cur = True, 0
+        else:
+            cur = st["steps"] + 1
+            anchor = cur >= int(getattr(self.config, "gamma_dec_max", 128))
+            if policy == "fixed" and cur >= int(self.config.gamma_dec):
+                anchor = True
+            if not anchor and policy in ("drift", "drift_rel") and st["last_sparse"] is not None:
+                c = _cos(sparse_out, st["last_sparse"])
+                if policy == "drift":
+                    anchor = c < float(self.config.drift_threshold)
+                else:
+                    hist = st["cos_hist"]
+                    if len(hist) >= 8:
+                        mu = sum(hist) / len(hist)
+                        sd = (sum((x - mu) ** 2 for x in hist) / len(hist)) ** 0.5
+                        anchor = c < mu - float(getattr(self.config, "drift_k", 2.0)) * sd
+                    hist.append(c)
+                    del hist[:-16]
+
+        dense_out = None
+        if anchor or log_drift:
+            dense_out = ops.decode_attention(q, k, v, window=0, sink=0, sm_scale=float(scaling))
+        if anchor:
+            st["last_delta"] = dense_out - sparse_out
+            st["steps"] = 0
+            out = dense_out
+        else:
+            out = sparse_out + st["last_delta"]
+            st["steps"] = cur
+        if log_drift:
+            true_delta = dense_out - sparse_out
+            pts = getattr(self, "_dec_drift_points", None) or []
+            pts.append({
+                "steps_since_anchor": int(cur),
+                "anchor": bool(anchor),
+                "drift_cos": _cos(true_delta, st["last_delta"]),
+                "applied_vs_true_cos": _cos(out, dense_out),
+            })
+            self._dec_drift_points = pts
+        st["last_sparse"] = sparse_out
+        self._dec_state = st
+        return out.transpose(1, 2).contiguous().to(query_states.dtype), None
+
     # -- projections and dispatch -----------------------------------------------
     def _qkv(self, hidden_states, hidden_shape):
         """The reference's model-family hook (llama.py:826-830): projected q/k/v
@@ -281,12 +386,16 @@ class LlamaAttention(nn.Module):
                 key_states, value_states, self.layer_idx,
                 {"sin": sin, "cos": cos, "cache_position": cache_position})
         impl = self.config._attn_implementation
-        if impl != "window":
+        if impl == "window":
+            interface = self.delta_forward
+        elif impl == "sdpa_rectangle":       # decode steps after the prefill (sample.py:160)
+            interface = self.sdpa_rectangle_forward
+        else:
             raise NotImplementedError(
                 f"attention implementation {impl!r} is not part of the MI355X delta path "
-                "(use 'window')")
+                "(use 'window', then 'sdpa_rectangle' for decode)")
         with region(timer, "attention_kernels"):
-            attn_output, attn_weights = self.delta_forward(
+            attn_output, attn_weights = interface(
                 self, query_states, key_states, value_states, attention_mask,
                 dropout=0.0 if not self.training else self.attention_dropout, scaling=self.scaling)
         assert attn_output.shape[-2] == self.config.num_attention_heads, attn_output.shape

@@ -52,6 +52,39 @@ class LlamaConfig:
     sink_tokens: int = 128
     stride_policy: str = "fixed"
     log_drift: bool = False
+    decode_mode: str = "dense"
+    gamma_dec: int = 32
+    refresh_policy: str = "fixed"
+    drift_threshold: float = 0.95
+    drift_k: float = 2.0
+    gamma_dec_max: int = 128
+
+
+class KVCache:
+    """Per-layer key/value storage preallocated as [B, max_len, Hkv, D] (the
+    projection layout, so appending is one strided copy); `update` appends
+    and returns [B, Hkv, len, D] views, which the kernels read in place."""
+
+    def __init__(self, config, batch: int, max_len: int, device, dtype):
+        shape = (batch, max_len, config.num_key_value_heads, config.head_dim)
+        n = config.num_hidden_layers
+        self.k = [torch.empty(shape, device=device, dtype=dtype) for _ in range(n)]
+        self.v = [torch.empty(shape, device=device, dtype=dtype) for _ in range(n)]
+        self.len = [0] * n
+        self.max_len = max_len
+
+    def update(self, key_states, value_states, layer_idx: int, cache_kwargs=None):
+        s = key_states.shape[2]
+        l0 = self.len[layer_idx]
+        assert l0 + s <= self.max_len, (l0, s, self.max_len)
+        self.k[layer_idx][:, l0:l0 + s] = key_states.transpose(1, 2)
+        self.v[layer_idx][:, l0:l0 + s] = value_states.transpose(1, 2)
+        self.len[layer_idx] = l0 + s
+        return (self.k[layer_idx][:, :l0 + s].transpose(1, 2),
+                self.v[layer_idx][:, :l0 + s].transpose(1, 2))
+
+    def seq_len(self) -> int:
+        return self.len[0]
 
 
 class LlamaMLP(nn.Module):
@@ -101,12 +134,12 @@ class LlamaDecoderLayer(nn.Module):
         self.post_attention_layernorm = LlamaRMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
     def forward_fused(self, hidden_states: torch.Tensor, residual: Optional[torch.Tensor],
-                      position_embeddings, timer: Optional[Timer] = None):
+                      position_embeddings, timer: Optional[Timer] = None, cache=None):
         """The layer on the split residual stream: its input is
         hidden_states + residual (residual None: hidden_states alone), its
         output (mlp_out, residual) with the same meaning."""
         x, residual = _norm(self.input_layernorm, hidden_states, residual, timer)
-        a, _ = self.self_attn(x, position_embeddings, timer=timer)
+        a, _ = self.self_attn(x, position_embeddings, past_key_value=cache, timer=timer)
         x, residual = _norm(self.post_attention_layernorm, a, residual, timer)
         return self.mlp(x, timer), residual
 
@@ -128,15 +161,18 @@ class LlamaModel(nn.Module):
         c = self.config
         return rope_cos_sin(position_ids, c.head_dim, c.rope_theta, dtype, c.rope_scaling)
 
-    def forward(self, input_ids: torch.Tensor, timer: Optional[Timer] = None) -> torch.Tensor:
-        """input_ids [b, s] -> final hidden states [b, s, hidden] (llama.py:1148-1300)."""
+    def forward(self, input_ids: torch.Tensor, timer: Optional[Timer] = None,
+                cache: Optional[KVCache] = None) -> torch.Tensor:
+        """input_ids [b, s] -> final hidden states [b, s, hidden] (llama.py:1148-1300);
+        with a cache, positions continue after the cached ones."""
         with _region(timer, "embed"):
             h = self.embed_tokens(input_ids)
-            pos = torch.arange(input_ids.shape[1], device=input_ids.device)[None]
+            start = cache.seq_len() if cache is not None else 0
+            pos = torch.arange(start, start + input_ids.shape[1], device=input_ids.device)[None]
             cos, sin = self.rotary(pos, h.dtype)
         residual = None
         for layer in self.layers:
-            h, residual = layer.forward_fused(h, residual, (cos, sin), timer)
+            h, residual = layer.forward_fused(h, residual, (cos, sin), timer, cache)
         out, _ = _norm(self.norm, h, residual, timer)
         return out
 
@@ -157,6 +193,46 @@ class LlamaForCausalLM(nn.Module):
         with _region(timer, "lm_head"):
             logits = self.lm_head(h[:, -1])
             return logits.argmax(-1)
+
+
+    def reset_decode_state(self):
+        """Per-prompt hygiene of the decode-delta state (sample.py:147-152)."""
+        for m in self.modules():
+            if isinstance(m, LlamaAttention):
+                m._dec_state = None
+                m._dec_drift_points = None
+
+    @torch.inference_mode()
+    def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
+                        timer: Optional[Timer] = None, step_ms: Optional[list] = None) -> torch.Tensor:
+        """Greedy generation as sample.py drives it: the prompt is prefilled
+        with the configured attention ("window": delta attention), then each
+        new token runs one decode step with `sdpa_rectangle` (dense, or the
+        sparse / delta decode of config.decode_mode). -> [b, max_new_tokens].
+        step_ms: receives each decode step's wall time."""
+        import time
+        cfg = self.config
+        b, s = input_ids.shape
+        cache = KVCache(cfg, b, s + max_new_tokens, input_ids.device, self.lm_head.weight.dtype)
+        self.reset_decode_state()
+        impl = cfg._attn_implementation
+        out = []
+        try:
+            h = self.model(input_ids, timer, cache)
+            tok = self.lm_head(h[:, -1]).argmax(-1)
+            out.append(tok)
+            cfg._attn_implementation = "sdpa_rectangle"
+            for _ in range(max_new_tokens - 1):
+                t0 = time.perf_counter()
+                h = self.model(tok[:, None], timer, cache)
+                tok = self.lm_head(h[:, -1]).argmax(-1)
+                out.append(tok)
+                if step_ms is not None:
+                    torch.cuda.synchronize()
+                    step_ms.append((time.perf_counter() - t0) * 1e3)
+        finally:
+            cfg._attn_implementation = impl
+        return torch.stack(out, dim=1)
 
 
 def init_weights_(model: nn.Module, std: float, seed: int = 0) -> nn.Module:

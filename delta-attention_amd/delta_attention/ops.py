@@ -286,6 +286,39 @@ def rope_qk(q: Optional[torch.Tensor], k: Optional[torch.Tensor], cos: torch.Ten
 
 
 # ---------------------------------------------------------------------------
+# decode rows
+
+def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int, sink: int,
+                     sm_scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The query row at the end of the cache: q [B,H,1,D] against k/v
+    [B,Hkv,n,D] (GQA native) over keys [0, sink) and the last `window` keys
+    (window 0: all keys; llama.py:537-549, 598-600) -> [B,H,1,D]."""
+    assert q.dim() == 4 and q.shape[2] == 1, q.shape
+    B, H, _, D = q.shape
+    Hkv, n = k.shape[1], k.shape[2]
+    assert k.shape == (B, Hkv, n, D) and v.shape == k.shape and H % Hkv == 0, (q.shape, k.shape)
+    assert q.dtype == k.dtype == v.dtype
+    dev = _on_gpu(q, k, v)
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    if out is None:
+        out = torch.empty((B, H, 1, D), device=dev, dtype=q.dtype)
+    assert out.shape == (B, H, 1, D) and out.stride(-1) == 1 and out.data_ptr() % 16 == 0
+    w, sk = max(int(window), 0), max(int(sink), 0)
+    nbytes = int(L.lib().da_decode_workspace_bytes(B, H, Hkv, n, D, w, sk))
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_decode_attn_fwd(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, n, D,
+            L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+            L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+            L.strides3(v.stride(0), v.stride(1), v.stride(2)),
+            L.strides3(out.stride(0), out.stride(1), out.stride(2)),
+            w, sk, float(sm_scale), _ptr(ws), nbytes, _code(q), _stream(dev))
+    L.check(rc, "da_decode_attn_fwd")
+    return out
+
+
+# ---------------------------------------------------------------------------
 # decoder-layer element-wise kernels (full-model prefill)
 
 def _rows2d(t: torch.Tensor) -> Tuple[int, int]:

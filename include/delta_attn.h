@@ -144,6 +144,26 @@ int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
                         int dtype, void* stream);
 
 /*
+ * Decode row: the query at the end of a KV cache of n_keys keys (position
+ * n_keys - 1) attends keys [0, sink) and its last `window` keys
+ * [n_keys - window, n_keys) (window == 0: every key). Replaces the decode
+ * rows of delta_attention/llama.py:537-549 (`_decode_sparse_row`, sink + last
+ * window keys; with window >= n_keys - sink that is every key) and the dense
+ * anchor row of :598-600 (window 0), which delta_decode_forward composes.
+ * q [B, Hq, 1, D] and out [B, Hq, 1, D] with strides {batch, head, row};
+ * k/v [B, Hkv, n_keys, D] ({batch, head, seq}). Split-KV over the row's key
+ * tiles, merged in a second kernel; workspace must hold
+ * da_decode_workspace_bytes(...) bytes.
+ */
+size_t da_decode_workspace_bytes(int B, int Hq, int Hkv, int n_keys, int D, int window, int sink);
+int da_decode_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                       int B, int Hq, int Hkv, int n_keys, int D,
+                       const int64_t q_str[3], const int64_t k_str[3],
+                       const int64_t v_str[3], const int64_t o_str[3],
+                       int window, int sink, float sm_scale,
+                       void* workspace, size_t workspace_bytes, int dtype, void* stream);
+
+/*
  * Kernel (3): delta broadcast-add over rows 0 .. s_p-1.
  * Replaces the torch broadcast at delta_attention/llama.py:740-755 (uniform
  * stride) and delta_attention/stride.py:26-40 (`apply_delta_variable`).

@@ -14,6 +14,9 @@ prefill (file:line cite the reference, singhh5050/delta-attention):
   qsparse_attention      delta_kernel.py:36-97, 199-251 (row i attends keys 0..mask[i])
   delta_forward          llama.py:659-757 (modes delta / recompute / sparse-only)
   apply_delta_variable   stride.py:26-40
+  decode_row             llama.py:537-549 (_decode_sparse_row: sink + last window
+                         keys of the cache) and the dense decode row of :598-600
+  delta_decode_steps     llama.py:551-657 (fixed-stride delta decode composition)
   round_bf16, *_bf16     the bf16 elementwise arithmetic of llama.py:740-751 and
                          stride.py:38-40 (fp32 op, one round-to-nearest-even)
   rope / rms_norm        llama.py:129-192 (rotate_half RoPE), llama.py:60-74 (RMSNorm),
@@ -214,6 +217,45 @@ def causal_attention_rows(q: np.ndarray, k: np.ndarray, v: np.ndarray, rows: np.
     """Full causal attention at the given rows of q [B,H,S,d] -> [B,len(rows),H,d]."""
     rows = np.asarray(rows, dtype=np.int64)
     return qsparse_attention(q[:, :, rows], k, v, rows, scale).transpose(0, 2, 1, 3)
+
+
+def decode_keys(n: int, window: int, sink: int) -> np.ndarray:
+    """Keys the decode row at position n-1 attends (llama.py:542-549): all of
+    them when n <= sink + window (or window == 0), else the first `sink` and
+    the last `window`."""
+    if window <= 0 or n <= sink + window:
+        return np.arange(n)
+    return np.concatenate([np.arange(sink), np.arange(n - window, n)])
+
+
+def decode_row(q: np.ndarray, k: np.ndarray, v: np.ndarray, window: int, sink: int,
+               scale: float) -> np.ndarray:
+    """The decode row: q [B,H,1,d] against k/v [B,Hkv,n,d] over decode_keys(...)
+    -> [B,H,1,d]; window 0 is the dense row."""
+    n = k.shape[2]
+    keys = decode_keys(n, window, sink)
+    allowed = np.zeros((1, n), dtype=bool)
+    allowed[0, keys] = True
+    return masked_attention(q, k, v, allowed, scale)
+
+
+def delta_decode_steps(qs: Sequence[np.ndarray], k: np.ndarray, v: np.ndarray, window: int,
+                       sink: int, scale: float, gamma_dec: int) -> list:
+    """Fixed-policy delta decode over successive query rows against one cache
+    (llama.py:551-657): the first step and every gamma_dec-th one output the
+    dense row and refresh delta = dense - sparse; the others output
+    sparse + delta."""
+    outs, delta, steps = [], None, 0
+    for q in qs:
+        sp = decode_row(q, k, v, window, sink, scale)
+        if delta is None or steps + 1 >= gamma_dec:
+            dn = decode_row(q, k, v, 0, 0, scale)
+            delta, steps = dn - sp, 0
+            outs.append(dn)
+        else:
+            steps += 1
+            outs.append(sp + delta)
+    return outs
 
 
 # ---------------------------------------------------------------------------

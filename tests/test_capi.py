@@ -170,3 +170,24 @@ def test_norm_and_swiglu_checks(lib):
     assert lib.da_swiglu(P(16), 64, P(16), 64, P(16), 64, 8, 60, L.DA_BF16, None) == L.DA_ERR_INVALID_ARG
     assert lib.da_swiglu(P(16), 64, P(8), 64, P(16), 64, 8, 64, L.DA_BF16, None) == L.DA_ERR_ALIGNMENT
     assert lib.da_swiglu(P(16), 64, P(16), 64, P(16), 64, 0, 64, L.DA_BF16, None) == L.DA_OK
+
+
+def test_decode_checks(lib):
+    P = ctypes.c_void_p
+    s3 = _s3(32 * 128, 128, 128)
+    k3 = _s3(8 * 8192 * 128, 8192 * 128, 128)
+    ws = lib.da_decode_workspace_bytes
+    assert ws(1, 32, 8, 8192, 128, 2048, 128) > 0
+    assert ws(1, 32, 8, 8192, 128, 2048, 128) < ws(1, 32, 8, 8192, 128, 0, 0) * 4
+    assert ws(1, 32, 8, 8192, 96, 0, 0) == 0 and ws(1, 32, 8, 0, 128, 0, 0) == 0
+    need = ws(1, 32, 8, 8192, 128, 2048, 128)
+
+    def call(n=8192, window=2048, sink=128, w=16, nbytes=None, D=128):
+        return lib.da_decode_attn_fwd(P(16), P(16), P(16), P(16), 1, 32, 8, n, D, s3, k3, k3, s3,
+                                      window, sink, 0.1, P(w), need if nbytes is None else nbytes,
+                                      L.DA_BF16, None)
+    assert call(nbytes=need - 1) == L.DA_ERR_WORKSPACE
+    assert call(w=0) == L.DA_ERR_WORKSPACE
+    assert call(n=0) == L.DA_ERR_INVALID_ARG
+    assert call(window=-1) == L.DA_ERR_INVALID_ARG
+    assert call(D=80) == L.DA_ERR_HEAD_DIM

@@ -344,3 +344,50 @@ def test_bf16_prologue_ops_match_torch():
     diff = np.abs(got - tref.float().numpy())
     ulp = np.abs(tref.float().numpy()) * 2.0 ** -7
     assert (diff <= ulp + 1e-30).all() and (diff == 0).mean() > 0.99
+
+
+# ---------------------------------------------------------------------------
+# decode rows
+
+@pytest.mark.parametrize("n,window,sink", [(40, 8, 4), (40, 36, 4), (40, 0, 4), (7, 3, 2), (1, 4, 2)])
+def test_decode_row_brute_force(n, window, sink):
+    # the reference's key set: concat(k[:sink], k[n-window:]) when n > sink + window
+    if window and n > sink + window:
+        keys = list(range(sink)) + list(range(n - window, n))
+    else:
+        keys = list(range(n))
+    assert list(O.decode_keys(n, window, sink)) == keys
+    q, k, v = _qkv(1, 4, 2, 1, 8, seed=n + window, N=n)
+    got = O.decode_row(q, k, v, window, sink, 0.3)
+    ref = np.zeros_like(got)
+    for h in range(4):
+        sc = [0.3 * float(np.dot(q[0, h, 0], k[0, h // 2, j])) for j in keys]
+        m = max(sc)
+        w = [math.exp(x - m) for x in sc]
+        ref[0, h, 0] = sum(wi * v[0, h // 2, j] for wi, j in zip(w, keys)) / sum(w)
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_decode_dense_row_is_last_causal_row():
+    q, k, v = _qkv(2, 6, 3, 1, 16, seed=3, N=90)
+    qq = np.concatenate([np.zeros((2, 6, 89, 16)), q], axis=2)
+    ref = O.causal_attention_rows(qq, k, v, np.array([89]), 0.25).transpose(0, 2, 1, 3)
+    np.testing.assert_allclose(O.decode_row(q, k, v, 0, 0, 0.25), ref, rtol=1e-12, atol=1e-14)
+    # window covering everything past the sinks is the dense row too
+    np.testing.assert_allclose(O.decode_row(q, k, v, 86, 4, 0.25), ref, rtol=1e-12, atol=1e-14)
+
+
+def test_delta_decode_steps_schedule():
+    q0 = _qkv(1, 2, 1, 1, 8, seed=1, N=50)
+    k, v = q0[1], q0[2]
+    qs = [_qkv(1, 2, 1, 1, 8, seed=10 + i, N=50)[0] for i in range(5)]
+    outs = O.delta_decode_steps(qs, k, v, 8, 2, 0.5, gamma_dec=2)
+    dense = [O.decode_row(q, k, v, 0, 0, 0.5) for q in qs]
+    sparse = [O.decode_row(q, k, v, 8, 2, 0.5) for q in qs]
+    for i in (0, 2, 4):        # anchors: the dense rows
+        np.testing.assert_array_equal(outs[i], dense[i])
+    for i in (1, 3):           # sparse + the delta of the previous anchor
+        np.testing.assert_allclose(outs[i], sparse[i] + dense[i - 1] - sparse[i - 1], rtol=1e-12)
+    # gamma_dec 1: every step is an anchor, i.e. dense decode
+    for o, d in zip(O.delta_decode_steps(qs, k, v, 8, 2, 0.5, gamma_dec=1), dense):
+        np.testing.assert_array_equal(o, d)
