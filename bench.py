@@ -68,6 +68,14 @@ def parse():
                         "ids with delta attention in every layer: time to first token and the "
                         "attention kernels' share (one JSON line; --steps/--warmup count prefills)")
     p.add_argument("--layers", type=int, default=32, help="decoder layers of --model")
+    p.add_argument("--decode", action="store_true",
+                   help="decode step of one layer against a --seq key cache: the sparse decode row "
+                        "(sinks + last window keys), the dense anchor row and the delta step at "
+                        "--gamma-dec, with their HBM rooflines (one JSON line)")
+    p.add_argument("--gamma-dec", type=int, default=32)
+    p.add_argument("--decode-tokens", type=int, default=0,
+                   help="with --model: also generate this many tokens after the prefill, with "
+                        "dense and with delta decode, and report ms per decode token")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -248,6 +256,7 @@ def model_prefill(a, dev):
     ~ N(0, 0.02)) on a.seq random token ids: embedding, every decoder layer
     (projections, fused RoPE, delta attention, o_proj, fused add+RMSNorm,
     SwiGLU MLP), final norm, lm_head on the last position and the greedy token."""
+    import numpy as np
     import torch
     from delta_attention import ops
     from delta_attention.model import LlamaConfig, random_llama
@@ -303,7 +312,72 @@ def model_prefill(a, dev):
                    "model": round((f_attn + f_gemm) / (ttft * 1e-3) / 1e12, 1)},
         "first_token": int(tok[0]), "init_s": round(init_s, 2),
     }
+    if a.decode_tokens > 1:
+        # generation after the prefill: ms per decode token, dense vs delta decode
+        dec = {}
+        for mode in ("dense", "delta"):
+            cfg.decode_mode, cfg.gamma_dec = mode, a.gamma_dec
+            steps_ms = []
+            toks = model.generate_greedy(ids, a.decode_tokens, step_ms=steps_ms)
+            dec[mode] = {"ms_per_token": round(float(np.median(steps_ms)), 3),
+                         "tokens": int(toks.shape[1])}
+        line["decode"] = dict(dec, gamma_dec=a.gamma_dec, context=S,
+                              note="median wall time of one decode step (32 layers + lm_head)")
     print(json.dumps(line), flush=True)
+
+
+def decode_layer(a, dev):
+    """One layer's decode step against a KV cache of a.seq keys (batch 1):
+    the sparse decode row, the dense anchor row, and the delta step averaged
+    over gamma_dec steps (one dense + gamma_dec - 1 sparse rows + the add)."""
+    import torch
+    from delta_attention import ops
+    H, Hkv, D, n = a.heads, a.kv_heads, a.head_dim, a.seq
+    g = torch.Generator(device=dev).manual_seed(a.seed)
+    q = torch.randn(1, H, 1, D, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, Hkv, n, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, Hkv, n, D, device=dev, generator=g).to(torch.bfloat16)
+    scale = D ** -0.5
+    delta = torch.zeros(1, H, 1, D, device=dev, dtype=torch.bfloat16)
+
+    def timed(fn, iters):
+        for _ in range(max(a.warmup, 3)):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters * 1e3   # us
+    iters = max(a.steps, 50)
+    us_sparse = timed(lambda: ops.decode_attention(q, k, v, window=a.window, sink=a.sink,
+                                                   sm_scale=scale), iters)
+    us_dense = timed(lambda: ops.decode_attention(q, k, v, window=0, sink=0, sm_scale=scale), iters)
+    us_add = timed(lambda: ops.decode_attention(q, k, v, window=a.window, sink=a.sink,
+                                                sm_scale=scale).add_(delta), iters) - us_sparse
+    n_sparse = min(n, a.sink + a.window)
+    row_b = Hkv * D * 2 * 2                     # one key's K and V bytes
+    b_sparse, b_dense = n_sparse * row_b, n * row_b
+    gd = a.gamma_dec
+    us_delta = (us_dense + (gd - 1) * (us_sparse + max(us_add, 0.0))) / gd
+
+    def hbm(b, us):
+        gbs = b / (us * 1e-6) / 1e9
+        return {"bytes": b, "us": round(us, 2), "gbs": round(gbs, 1),
+                "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    print(json.dumps({
+        "metric": "delta-attention decode step latency (one layer)", "value": round(us_delta, 2),
+        "unit": "us", "higher_is_better": False, "dtype": "bf16", "n_gpus": 1,
+        "config": {"workload": "decode row against a KV cache", "keys": n, "q_heads": H,
+                   "kv_heads": Hkv, "head_dim": D, "window": a.window, "sink": a.sink,
+                   "gamma_dec": gd},
+        "sparse_row": hbm(b_sparse, us_sparse), "dense_row": hbm(b_dense, us_dense),
+        "delta_step_avg_us": round(us_delta, 2),
+        "roofline": dict(hbm(b_dense, us_dense), bound="hbm", kernel="dense decode row",
+                         peak=PEAK_HBM_GBS, unit="GB/s"),
+    }), flush=True)
 
 
 def load_traffic(name):
@@ -340,6 +414,9 @@ def main():
         return
     if a.model:
         model_prefill(a, dev)
+        return
+    if a.decode:
+        decode_layer(a, dev)
         return
     B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
     scale = D ** -0.5

@@ -51,6 +51,10 @@ namespace da {
 #ifndef DA_WAVES
 #define DA_WAVES 4
 #endif
+// Split items a decode-row launch aims for.
+#ifndef DA_DECODE_ITEMS
+#define DA_DECODE_ITEMS 1024
+#endif
 constexpr int NWAVE = DA_WAVES;
 static_assert(NWAVE == 4 || NWAVE == 8, "4 or 8 waves per workgroup");
 constexpr int NTHR = 64 * NWAVE;
@@ -623,6 +627,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
         *(u32x2*)(op + d * esz) = pkd;
       }
   } else {
+    if (!valid) return;   // the merge reads the rows of the selection only
     const int r = wave * 32 + ln;
     float* po = a.part_o + ((int64_t)w * BM + r) * D;
 #pragma unroll
@@ -641,14 +646,19 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-KV merge + epilogue of kernel (2). One workgroup per (b, kv head,
-// m tile); MTHR threads cover BM rows x D/8 column chunks.
+// Split-KV merge + epilogue of kernel (2). `wgs` workgroups per (b, kv head,
+// m tile) cover its valid rows x D/8 column chunks; each (row, chunk) task is
+// shared by P = `lanes` consecutive threads that take every P-th split and
+// combine (max, sum, O) by xor-shuffles, so long split lists (decode rows)
+// are read with P loads in flight per task.
 struct MergeArgs {
   const int64_t* q_rows;
   const int64_t* row_last;
   int64_t rl_b;
   int n_rows, G, Hkv, n_kv, n_mtiles, n_splits, chunk;
   int window, sink;
+  int lanes;        // P: threads sharing one (row, 8-column) task, splits s = p mod P
+  int wgs;          // workgroups per row tile
   const float* part_o;
   const float* part_ml;
   int epi, n_anchor, n_q;
@@ -663,7 +673,8 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   using E = Elt<T>;
   constexpr int CPR = D / 8;   // 8-column chunks per row
   __shared__ int s_hmax[4], s_lmin[4];
-  const int tile = blockIdx.x;
+  const int tile = blockIdx.x / a.wgs;
+  const int sub = blockIdx.x % a.wgs;
   const int mt = tile % a.n_mtiles;
   const int bh = tile / a.n_mtiles;
   const int hk = bh % a.Hkv;
@@ -699,24 +710,29 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   const int nsv = (n_first + n_second + a.chunk - 1) / a.chunk;
 
   const size_t esz = sizeof(T);
-  for (int task = tid; task < BM * CPR; task += MTHR) {
+  const int P = a.lanes;
+  const int p = tid % P;
+  {
+    const int task = sub * (MTHR / P) + tid / P;
     const int r = task / CPR;
     const int c = task % CPR;
     const int mflat = mt * BM + r;
-    if (mflat >= a.n_rows * G) continue;
+    // whole P-lane groups leave together (the shuffles stay inside a group)
+    if (r >= BM || mflat >= a.n_rows * G) return;
     const int i = mflat / G;
     const int h = hk * G + mflat % G;
 
     float M = NEG_BIG;
-    for (int s = 0; s < nsv; ++s) {
+    for (int s = p; s < nsv; s += P) {
       const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
       M = fmaxf(M, a.part_ml[w * 2 * BM + r]);
     }
+    for (int off = 1; off < P; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
     float L = 0.f;
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    for (int s = 0; s < nsv; ++s) {
+    for (int s = p; s < nsv; s += P) {
       const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
       const float sc = fast_exp2(a.part_ml[w * 2 * BM + r] - M);
       L += sc * a.part_ml[w * 2 * BM + BM + r];
@@ -728,6 +744,12 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
         acc[4 + e] += sc * x1[e];
       }
     }
+    for (int off = 1; off < P; off <<= 1) {
+      L += __shfl_xor(L, off);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], off);
+    }
+    if (p != 0) return;
     const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] *= inv;
@@ -801,7 +823,7 @@ static QsparsePlan plan_decode(int B, int Hq, int Hkv, int n_keys, int D, int wi
   const int64_t all = (n_keys + BN - 1) / BN;
   int64_t vis = all;
   if (window > 0) vis = min(all, (int64_t)(min(sink, n_keys) + BN - 1) / BN + (window + BN - 1) / BN + 1);
-  return plan_qsparse(B, Hq, Hkv, 1, vis, D, 1024);
+  return plan_qsparse(B, Hq, Hkv, 1, vis, D, DA_DECODE_ITEMS);
 }
 
 template <typename T, int D, int MODE>
@@ -965,6 +987,14 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   m.n_rows = n; m.n_q = Sq; m.G = a.G; m.Hkv = Hkv; m.n_kv = Skv; m.n_mtiles = p.n_mtiles;
   m.n_splits = p.n_splits; m.chunk = p.chunk;
   m.window = window; m.sink = sink;
+  // P threads per (row, column chunk) task: about 4 splits each, up to 16;
+  // workgroups per row tile cover its valid rows only
+  m.lanes = 1;
+  while (m.lanes < 16 && m.lanes * 4 < p.n_splits) m.lanes <<= 1;
+  {
+    const int64_t rows = min((int64_t)BM, (int64_t)n * a.G);
+    m.wgs = (int)((rows * (D / 8) * m.lanes + MTHR - 1) / MTHR);
+  }
   m.part_o = a.part_o; m.part_ml = a.part_ml;
   m.epi = epi; m.n_anchor = (epi == DA_EPI_DELTA || epi == DA_EPI_DENSE) ? n_anchor : 0;
   m.o = o; m.os_b = o_str[0]; m.os_h = o_str[1]; m.os_s = o_str[2];
@@ -974,7 +1004,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
   dispatch_attn<MODE_QSPARSE>(a, D, dtype, s);
-  const int n_tiles = B * Hkv * p.n_mtiles;
+  const int n_tiles = B * Hkv * p.n_mtiles * m.wgs;
   if (dtype == DA_BF16) {
     if (D == 128) launch_merge<__bf16, 128>(m, n_tiles, s);
     else launch_merge<__bf16, 64>(m, n_tiles, s);
