@@ -51,6 +51,10 @@ namespace da {
 #ifndef DA_WAVES
 #define DA_WAVES 4
 #endif
+// Split items a selected-rows launch aims for.
+#ifndef DA_ROWS_ITEMS
+#define DA_ROWS_ITEMS 8192
+#endif
 // Split items a decode-row launch aims for.
 #ifndef DA_DECODE_ITEMS
 #define DA_DECODE_ITEMS 1024
@@ -794,8 +798,10 @@ struct QsparsePlan {
 };
 
 // Split plan over the tile lists: `vis` bounds a row tile's list length, each
-// item takes `chunk` consecutive tiles of it; `target` items in total.
-static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int D, int target) {
+// item takes `chunk` consecutive tiles of it (at least `min_chunk`); `target`
+// items in total.
+static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int D, int target,
+                                int min_chunk = 1) {
   QsparsePlan p;
   const int G = Hq / Hkv;
   p.n_mtiles = (int)(((int64_t)n * G + BM - 1) / BM);
@@ -805,16 +811,18 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
   if (want < 1) want = 1;
   if (want > vis) want = vis;
   p.chunk = (int)((vis + want - 1) / want);
+  if (p.chunk < min_chunk) p.chunk = (int)min((int64_t)min_chunk, vis);
   p.n_splits = (int)((vis + p.chunk - 1) / p.chunk);
   p.n_items = (int)(base * p.n_splits);
   p.ws_bytes = (size_t)p.n_items * BM * (D + 2) * sizeof(float);
   return p;
 }
 
-// Causal selected rows: ~4096 items (about half of them past the end of a
-// causal row tile's list), several equal-sized items per CU.
+// Causal selected rows: ~8192 items (about half of them past the end of a
+// causal row tile's list), but at least 40 key tiles each: short items pay
+// their prologue and partials (measured at 32K and 128K keys).
 static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
-  return plan_qsparse(B, Hq, Hkv, n, (Skv + BN - 1) / BN, D, 4096);
+  return plan_qsparse(B, Hq, Hkv, n, (Skv + BN - 1) / BN, D, DA_ROWS_ITEMS, 40);
 }
 
 // One decode row per batch at the end of the cache: its list is the sink
