@@ -1,9 +1,13 @@
-// Attention kernels of the delta-attention prefill path on gfx950:
-//   kernel (1)  da_sparse_attn_fwd   sink + block-anchored sliding window
-//   kernel (2)  da_qsparse_attn_fwd  selected query rows against all causal keys,
-//                                    split over the key axis, merged by
-//                                    qsparse_merge_kernel, which also runs the
-//                                    delta epilogue.
+// Attention kernels of the delta-attention path on gfx950:
+//   kernel (1)  da_sparse_attn_fwd   sink + block-anchored sliding window;
+//               da_sparse_attn_delta_fwd  the same with the delta broadcast-add
+//                                    (kernel (3)) in its epilogue
+//   kernel (2)  da_qsparse_attn_fwd  selected query rows against their causal
+//                                    keys (optionally sinks + a window: the
+//                                    decode rows of da_decode_attn_fwd), split
+//                                    over each row tile's key-tile list,
+//                                    merged by qsparse_merge_kernel, which also
+//                                    runs the output / delta / dense epilogues.
 //
 // Tiling (one workgroup = 4 waves = 256 threads, two workgroups per CU):
 //   * M tile: BM = 128 flattened (query row, head-in-group) pairs. The G

@@ -1,11 +1,14 @@
 """Llama attention with the delta-attention prefill path
 (delta_attention/llama.py:60-192, 218-229, 364-496, 659-914 of the reference).
 
-`LlamaAttention.forward` projects q/k/v, applies RoPE and routes
-`config._attn_implementation == "window"` to `delta_forward`, which runs the
-three MI355X kernels: key-sparse attention (kernel 1), query-sparse dense rows
-with the fused delta epilogue (kernel 2) and the delta broadcast-add
-(kernel 3). The module's config object needs the Llama fields
+`LlamaAttention.forward` projects q/k/v, applies the fused RoPE (+ Qwen3 q/k
+norm) prologue kernel and routes `config._attn_implementation == "window"` to
+`delta_forward`: query-sparse dense rows (kernel 2, dense tail into the output,
+dense anchor rows aside), then key-sparse attention (kernel 1) with the delta
+broadcast-add (kernel 3) fused into its epilogue, or kernels 1 -> 2 -> 3 when
+the stride does not divide the row tile. "sdpa_rectangle" (decode after the
+prefill) routes to `sdpa_rectangle_forward` and the sparse / delta decode.
+The module's config object needs the Llama fields
 (hidden_size, num_attention_heads, num_key_value_heads, optional head_dim,
 attention_bias, attention_dropout, rms_norm_eps, _attn_implementation) and the
 pipeline knobs of `config.PIPELINE_FIELDS`.
@@ -152,8 +155,10 @@ class LlamaAttention(nn.Module):
 
         mode "sparse-only": kernel (1) only. "recompute": kernel (1), then the
         selected rows (anchors every delta_lambda rows + the cut_n dense tail)
-        are replaced by dense rows. "delta": kernel (2) writes the tail rows and
-        the anchor deltas, kernel (3) adds each delta over its stride group.
+        are replaced by dense rows. "delta": sparse + the anchor delta over each
+        stride group, dense tail rows (ops.delta_prefill: kernel (2) then kernel
+        (1) with the broadcast-add in its epilogue, bit-identical to kernels
+        (1) -> (2) -> (3)).
         """
         cfg = self.config
         lambd = int(cfg.delta_lambda)
