@@ -817,8 +817,12 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
   p.chunk = (int)((vis + want - 1) / want);
   if (p.chunk < min_chunk) p.chunk = (int)min((int64_t)min_chunk, vis);
   p.n_splits = (int)((vis + p.chunk - 1) / p.chunk);
-  p.n_items = (int)(base * p.n_splits);
-  p.ws_bytes = (size_t)p.n_items * BM * (D + 2) * sizeof(float);
+  const int64_t items = base * p.n_splits;
+  // grids past 2^31 workgroups (split kernel, or merge at <= 128 per tile)
+  // are refused by the entry points (n_items = 0)
+  const bool fits = items <= 0x7fffff00LL && base * 128 <= 0x7fffff00LL;
+  p.n_items = fits ? (int)items : 0;
+  p.ws_bytes = fits ? (size_t)p.n_items * BM * (D + 2) * sizeof(float) : 0;
   return p;
 }
 
@@ -975,6 +979,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
                        int epi, int n_anchor, void* delta, const int64_t d_str[3],
                        int window, int sink, float sm_scale, void* workspace,
                        size_t workspace_bytes, int dtype, void* stream) {
+  if (p.n_items <= 0) return DA_ERR_INVALID_ARG;
   if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
 
