@@ -233,32 +233,56 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     hi = valid ? (int)(lim < -1 ? -1 : lim) : -1;
     lo = a.window > 0 ? hi - a.window + 1 : 0;
   }
-  int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
-  int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
   const int sink = (KSPARSE || a.window > 0) ? a.sink : 0;
+  constexpr size_t esz = sizeof(T);
 
-  // ---- tile-wide bounds (valid rows only) ----
+  // ---- Q^T fragments (registers for the whole kernel), loaded first so
+  //      that their latency overlaps the set-up below ----
+  u32x4 qf[NDS];
+  {
+    const char* qp = (const char*)a.q +
+                     ((int64_t)b * a.qs_b + (int64_t)hrow * a.qs_h + (int64_t)qrow * a.qs_s) * esz;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    v_hmin = min(v_hmin, __shfl_xor(v_hmin, off));
-    v_hmax = max(v_hmax, __shfl_xor(v_hmax, off));
-    v_lmin = min(v_lmin, __shfl_xor(v_lmin, off));
-    v_lmax = max(v_lmax, __shfl_xor(v_lmax, off));
+    for (int ds = 0; ds < NDS; ++ds)
+      qf[ds] = valid ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
   }
-  if (lane == 0) {
-    red[0][wave] = v_hmin;
-    red[1][wave] = v_hmax;
-    red[2][wave] = v_lmin;
-    red[3][wave] = v_lmax;
-  }
-  __syncthreads();
-  int hi_min = red[0][0], hi_max = red[1][0], lo_min = red[2][0], lo_max = red[3][0];
+
+  // ---- tile-wide bounds over the valid rows ----
+  int hi_min, hi_max, lo_min, lo_max;
+  if (KSPARSE) {
+    // the tile holds rows r0 .. r1 (BM / GT of them, the last tile fewer);
+    // hi = row and lo grow with the row
+    const int r0 = mt * (BM / GT);
+    const int r1 = min(r0 + BM / GT, a.n_rows) - 1;
+    hi_min = r0;
+    hi_max = r1;
+    lo_min = (r0 / a.q_block) * a.q_block + a.q_block - a.window;
+    lo_max = (r1 / a.q_block) * a.q_block + a.q_block - a.window;
+  } else {
+    int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
+    int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
 #pragma unroll
-  for (int i = 1; i < NWAVE; ++i) {
-    hi_min = min(hi_min, red[0][i]);
-    hi_max = max(hi_max, red[1][i]);
-    lo_min = min(lo_min, red[2][i]);
-    lo_max = max(lo_max, red[3][i]);
+    for (int off = 32; off >= 1; off >>= 1) {
+      v_hmin = min(v_hmin, __shfl_xor(v_hmin, off));
+      v_hmax = max(v_hmax, __shfl_xor(v_hmax, off));
+      v_lmin = min(v_lmin, __shfl_xor(v_lmin, off));
+      v_lmax = max(v_lmax, __shfl_xor(v_lmax, off));
+    }
+    if (lane == 0) {
+      red[0][wave] = v_hmin;
+      red[1][wave] = v_hmax;
+      red[2][wave] = v_lmin;
+      red[3][wave] = v_lmax;
+    }
+    __syncthreads();
+    hi_min = red[0][0], hi_max = red[1][0], lo_min = red[2][0], lo_max = red[3][0];
+#pragma unroll
+    for (int i = 1; i < NWAVE; ++i) {
+      hi_min = min(hi_min, red[0][i]);
+      hi_max = max(hi_max, red[1][i]);
+      lo_min = min(lo_min, red[2][i]);
+      lo_max = max(lo_max, red[3][i]);
+    }
   }
 
   // ---- key tiles to visit: the tile list, or (query-sparse mode) this
@@ -272,7 +296,6 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     nt = min(a.chunk, nt - t_off);
   }
 
-  constexpr size_t esz = sizeof(T);
   const char* kbase = (const char*)a.k + ((int64_t)b * a.ks_b + (int64_t)hk * a.ks_h) * esz;
   const char* vbase = (const char*)a.v + ((int64_t)b * a.vs_b + (int64_t)hk * a.vs_h) * esz;
   // row strides in bytes are below 2^24 (checked on the host), so tile
@@ -281,16 +304,6 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   const uint32_t vrow_b = (uint32_t)(a.vs_s * (int64_t)esz);
   const uint64_t kend = (uint64_t)kbase + (uint64_t)(uint32_t)a.n_kv * krow_b;
   const uint64_t vend = (uint64_t)vbase + (uint64_t)(uint32_t)a.n_kv * vrow_b;
-
-  // ---- Q^T fragments (registers for the whole kernel) ----
-  u32x4 qf[NDS];
-  {
-    const char* qp = (const char*)a.q +
-                     ((int64_t)b * a.qs_b + (int64_t)hrow * a.qs_h + (int64_t)qrow * a.qs_s) * esz;
-#pragma unroll
-    for (int ds = 0; ds < NDS; ++ds)
-      qf[ds] = valid ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
-  }
 
   // ---- DMA source offsets: wave `wave`, chunk c fills LDS slots
   //      (c * NWAVE + wave) * 64 + lane of the tile; slot -> (row, swizzled chunk) ----

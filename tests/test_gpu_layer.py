@@ -195,6 +195,27 @@ def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
     assert_close(np64(a), ref, what=f"fused B{B} H{H}/{Hkv} S{S} g{gamma}")
 
 
+@pytest.mark.parametrize("H,Hkv,D,gamma", [(8, 2, 128, 64), (4, 4, 64, 32), (10, 2, 128, 16)])
+def test_fused_delta_bit_identical_fp16(gpu, H, Hkv, D, gamma):
+    """The fused order in fp16 (the delta and the add round to fp16): same bits
+    as the three-kernel sequence, within the T1 gate of the oracle."""
+    from delta_attention import ops
+    S, window, sink = 1500, 256, 16
+    assert ops.fused_delta_rows(H, Hkv) % gamma == 0
+    q, k, v = gen_qkv(1, H, Hkv, S, D, seed=H + D, dtype=torch.float16, model_layout=True)
+    scale = D ** -0.5
+    a, da = ops.delta_prefill(q, k, v, gamma=gamma, window=window, sink=sink, sm_scale=scale,
+                              return_delta=True)
+    b, db = ops.delta_prefill(q, k, v, gamma=gamma, window=window, sink=sink, sm_scale=scale,
+                              return_delta=True, fused=False)
+    torch.cuda.synchronize()
+    assert a.dtype == torch.float16 and da.dtype == torch.float16
+    assert torch.equal(a, b)
+    assert torch.equal(da, db)
+    ref = O.delta_forward(np64(q), np64(k), np64(v), gamma, window, sink, scale)
+    assert_close(np64(a), ref, what=f"fused fp16 H{H}/{Hkv} D{D} g{gamma}")
+
+
 def test_unfused_when_gamma_exceeds_the_tile(gpu):
     # gamma 128 with GQA 4 (64-row tiles): the three-kernel path runs
     from delta_attention import ops
