@@ -29,6 +29,7 @@ sys.path.insert(0, REPO)
 METRIC = "delta-attn layer prefill ms + TFLOP/s (%MFMA peak) at 128K, Llama-3.1-8B shape"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_SCLK_MHZ = 2400.0      # engine clock the MFMA peak is quoted at
 
 
 def parse():
@@ -380,6 +381,74 @@ def decode_layer(a, dev):
     }), flush=True)
 
 
+class GpuState:
+    """Samples the amdgpu sysfs files of the (single) GPU in a background
+    thread while the timed work runs: current engine clock (pp_dpm_sclk, the
+    level marked '*'), package power (hwmon power1_input) and junction
+    temperature (hwmon temp2_input). Fields whose files are absent are None."""
+
+    def __init__(self, period_s=0.002):
+        import glob
+        self.period = period_s
+        devs = sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+        self.dev = os.path.dirname(devs[0]) if devs else None
+        hw = sorted(glob.glob(os.path.join(self.dev, "hwmon", "hwmon*"))) if self.dev else []
+        self.hwmon = hw[0] if hw else None
+        self.samples = {"sclk_mhz": [], "power_w": [], "temp_c": []}
+        self._stop = None
+        self._thread = None
+
+    @staticmethod
+    def _read(path):
+        try:
+            with open(path) as f:
+                return f.read()
+        except OSError:
+            return None
+
+    def _sample(self):
+        import re
+        if self.dev:
+            t = self._read(os.path.join(self.dev, "pp_dpm_sclk"))
+            for line in (t or "").splitlines():
+                m = re.search(r"(\d+)\s*Mhz\s*\*", line)
+                if m:
+                    self.samples["sclk_mhz"].append(float(m.group(1)))
+        if self.hwmon:
+            p = self._read(os.path.join(self.hwmon, "power1_input"))
+            if p and p.strip().isdigit():
+                self.samples["power_w"].append(int(p) / 1e6)
+            c = self._read(os.path.join(self.hwmon, "temp2_input"))
+            if c and c.strip().lstrip("-").isdigit():
+                self.samples["temp_c"].append(int(c) / 1e3)
+
+    def __enter__(self):
+        import threading
+        self._stop = threading.Event()
+
+        def loop():
+            while not self._stop.is_set():
+                self._sample()
+                self._stop.wait(self.period)
+        self._thread = threading.Thread(target=loop, daemon=True)
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._thread.join()
+
+    def summary(self):
+        import statistics
+        out = {}
+        for k, v in self.samples.items():
+            out[k] = ({"min": round(min(v), 1), "median": round(statistics.median(v), 1),
+                       "max": round(max(v), 1), "n": len(v)} if v else None)
+        cap = self._read(os.path.join(self.hwmon, "power1_cap")) if self.hwmon else None
+        out["power_cap_w"] = int(cap) / 1e6 if cap and cap.strip().isdigit() else None
+        return out
+
+
 def load_traffic(name):
     """HBM bytes per launch of `name` from the committed rocprofv3 PMC summary."""
     path = os.path.join(REPO, "profiles", "hbm_traffic.json")
@@ -470,19 +539,22 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # timed region: exactly `steps` layer prefills
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / a.steps * 1e3
+    # timed region: exactly `steps` layer prefills (engine clock, power and
+    # temperature sampled meanwhile and through the per-kernel event pass)
+    gpu_state = GpuState()
+    with gpu_state:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / a.steps * 1e3
 
-    # per-kernel durations from HIP events on the launch stream (separate pass)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
-    for e in evs:
-        step(e)
-    torch.cuda.synchronize()
+        # per-kernel durations from HIP events on the launch stream (separate pass)
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(a.steps)]
+        for e in evs:
+            step(e)
+        torch.cuda.synchronize()
     k_ms = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / a.steps for i in range(3)]
 
     # outside the step: the stand-alone kernels (1) and (3) on the same data, the
@@ -546,6 +618,13 @@ def main():
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "traffic": kernels[dom]["traffic"]}
+    # the published peak is quoted at the 2400 MHz maximum engine clock; the
+    # fraction of the peak at the clock the GPU actually held is given beside it
+    st = gpu_state.summary()
+    if st["sclk_mhz"]:
+        sclk = st["sclk_mhz"]["median"]
+        roofline["sclk_mhz"] = sclk
+        roofline["frac_at_sclk"] = round(achieved / (PEAK_BF16_TFLOPS * sclk / PEAK_SCLK_MHZ), 4)
 
     cpu = None
     if a.cpu_budget > 0:
@@ -565,7 +644,7 @@ def main():
                    "batch": B, "seq_len": S, "q_heads": H, "kv_heads": Hkv, "head_dim": D,
                    "window": a.window, "sink": a.sink, "gamma": a.gamma,
                    "selected_rows": n_sel, "parallelism": "none (1 GPU)"},
-        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels,
+        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels, "gpu_state": st,
     }
     print(json.dumps(line), flush=True)
 
