@@ -40,6 +40,7 @@ EXPORTS = (
     "da_rope_qk",
     "da_add_rmsnorm",
     "da_swiglu",
+    "da_anchor_delta_cos",
     "da_build_target",
 )
 
@@ -113,6 +114,9 @@ def lib() -> ctypes.CDLL:
                                  _i, _vp]
     L.da_swiglu.restype = _i
     L.da_swiglu.argtypes = [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i, _i, _vp]
+    L.da_anchor_delta_cos.restype = _i
+    L.da_anchor_delta_cos.argtypes = [_vp, _p3, _vp, _p3, _vp, _i64, _i, _i, _i, _i,
+                                      _vp, _vp, _i, _f, _f, _i, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
     _lib = L

@@ -15,18 +15,22 @@ HIST_RANGE = (-1.0, 1.0)
 
 def drift_summary(dense_sparse_diff, layer_idx: int, gamma: int, seq_len: int) -> Dict[str, Any]:
     """Cosine between consecutive anchor deltas (per head, over d): mean,
-    p10/p50/p90 and a HIST_BINS histogram over HIST_RANGE (drift.py:23-49)."""
+    p10/p50/p90 and a HIST_BINS histogram over HIST_RANGE (drift.py:23-49).
+    The cosines and the histogram come from one kernel pass over the delta
+    buffer (ops.anchor_delta_cos); the mean and quantiles are taken over the
+    [b, n-1, h] cosines."""
     import torch
 
-    a = dense_sparse_diff[:, :-1].float()
-    b = dense_sparse_diff[:, 1:].float()
-    flat = torch.nn.functional.cosine_similarity(a, b, dim=-1).flatten()
-    hist = torch.histc(flat, bins=HIST_BINS, min=HIST_RANGE[0], max=HIST_RANGE[1])
+    from . import ops
+
+    cos, hist = ops.anchor_delta_cos(dense_sparse_diff, hist_bins=HIST_BINS, hist_range=HIST_RANGE)
+    flat = cos.flatten()
     qs = torch.quantile(flat, torch.tensor([0.1, 0.5, 0.9], device=flat.device))
+    mean, p10, p50, p90 = torch.cat((flat.mean()[None], qs)).tolist()   # one device sync
     return {
         "layer": int(layer_idx), "gamma": int(gamma), "seq_len": int(seq_len),
-        "n": int(flat.numel()), "mean": float(flat.mean().item()),
-        "p10": float(qs[0].item()), "p50": float(qs[1].item()), "p90": float(qs[2].item()),
+        "n": int(flat.numel()), "mean": float(mean),
+        "p10": float(p10), "p50": float(p50), "p90": float(p90),
         "hist_bins": HIST_BINS, "hist_range": list(HIST_RANGE),
         "hist": [int(x) for x in hist.tolist()],
     }

@@ -212,7 +212,8 @@ class LlamaAttention(nn.Module):
         for start, end in plan_chunks(s_p, int(cfg.adapt_chunk)):
             c_idx = torch.arange(start, end, step=gamma_c, device=device)
             dense_c = qsa_kernel(q[:, :, c_idx], k, v, c_idx.unsqueeze(0), scaling).transpose(1, 2)
-            cos_mean, cos_min = interanchor_cos(dense_c - sparse_attn_output[:, c_idx])
+            # deltas rnd(dense - sparse) at the chunk's anchors, formed in the kernel
+            cos_mean, cos_min = interanchor_cos(dense_c, sparse=sparse_attn_output, rows=c_idx)
             idx_parts.append(c_idx)
             dense_parts.append(dense_c)
             chunk_log.append({"start": int(start), "gamma": int(gamma_c), "cos_mean": cos_mean,

@@ -382,6 +382,49 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = N
 # ---------------------------------------------------------------------------
 # the composed layer prefill (kernels 1 -> 2 -> 3)
 
+# ---------------------------------------------------------------------------
+# consecutive-anchor delta cosine (drift signal)
+
+def anchor_delta_cos(a: torch.Tensor, *, sparse: Optional[torch.Tensor] = None,
+                     rows: Optional[torch.Tensor] = None, hist_bins: int = 0,
+                     hist_range: Tuple[float, float] = (-1.0, 1.0)):
+    """Cosine between consecutive anchor deltas, per (batch, head) over the
+    head dim: returns fp32 [B, n-1, H] (and, with hist_bins > 0, an int32
+    histogram of the cosines over hist_range with torch.histc's bins).
+
+    a: the deltas [B, n, H, D]; or, with `sparse` [B, S, H, D] given, the dense
+    anchor rows, whose deltas rnd(a - sparse[:, rows]) are formed inside the
+    kernel and never stored (rows: int64 [n] anchor rows, default 0..n-1)."""
+    assert a.dim() == 4, a.shape
+    B, n, H, D = a.shape
+    ts = [a] + ([sparse] if sparse is not None else [])
+    dev = _on_gpu(*ts)
+    code = _code(a)
+    if a.stride(-1) != 1 or a.data_ptr() % 4 or any(st % 2 for st in a.stride()[:-1]):
+        a = a.contiguous()
+    cos = torch.empty(B, max(n - 1, 0), H, device=dev, dtype=torch.float32)
+    hist = torch.zeros(hist_bins, device=dev, dtype=torch.int32) if hist_bins > 0 else None
+    s_str = None
+    n_rows = 0
+    if sparse is not None:
+        assert sparse.dim() == 4 and sparse.shape[0] == B and sparse.shape[2:] == (H, D), sparse.shape
+        assert sparse.dtype == a.dtype, (sparse.dtype, a.dtype)
+        if sparse.stride(-1) != 1 or sparse.data_ptr() % 4 or any(st % 2 for st in sparse.stride()[:-1]):
+            sparse = sparse.contiguous()
+        s_str = L.I64x3(*sparse.stride()[:3])
+        n_rows = sparse.shape[1]
+        if rows is not None:
+            rows = rows.to(device=dev, dtype=torch.int64).contiguous()
+            assert rows.numel() == n, (rows.numel(), n)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_anchor_delta_cos(
+            _ptr(a), L.I64x3(*a.stride()[:3]), _ptr(sparse), s_str, _ptr(rows), n_rows,
+            B, n, H, D, _ptr(cos), _ptr(hist), int(hist_bins),
+            float(hist_range[0]), float(hist_range[1]), code, _stream(dev))
+    L.check(rc, "da_anchor_delta_cos")
+    return (cos, hist) if hist_bins > 0 else cos
+
+
 def anchor_layout(s: int, gamma: int) -> Tuple[int, int, int]:
     """(cut_n, s_p, n_anchor) of delta_forward's fixed-stride layout
     (llama.py:692-693, 711-714): cut_n = s % gamma + max(128, gamma)."""

@@ -29,15 +29,21 @@ def apply_delta_variable(sparse_out, dense_out_sel, idx, s_p: int):
     return ops.delta_add(sparse_out, s_p=int(s_p), dense_sel=dense_out_sel, anchors=idx)
 
 
-def interanchor_cos(deltas) -> Tuple[float, float]:
+def interanchor_cos(deltas, *, sparse=None, rows=None) -> Tuple[float, float]:
     """(mean, min) cosine between consecutive anchor deltas [b, n, h, d],
-    per (b, pair, h) over d (stride.py:43-52)."""
-    import torch
+    per (b, pair, h) over d (stride.py:43-52), on the GPU kernel
+    (ops.anchor_delta_cos). With `sparse` and `rows` given, `deltas` holds the
+    dense anchor rows and the deltas rnd(dense - sparse[:, rows]) are formed
+    inside the kernel. Fewer than two anchors: (1.0, 1.0)."""
+    from . import ops
 
     if deltas.size(1) < 2:
         return 1.0, 1.0
-    cos = torch.nn.functional.cosine_similarity(deltas[:, :-1].float(), deltas[:, 1:].float(), dim=-1)
-    return cos.mean().item(), cos.min().item()
+    import torch
+
+    cos = ops.anchor_delta_cos(deltas, sparse=sparse, rows=rows)
+    mean, mn = torch.stack((cos.mean(), cos.min())).tolist()   # one device sync
+    return float(mean), float(mn)
 
 
 def next_gamma(cos_mean: float, gamma_c: int, *, threshold: float,

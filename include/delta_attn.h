@@ -231,6 +231,27 @@ int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
                const void* q_norm_w, const void* k_norm_w, float eps,
                int dtype, void* stream);
 
+/* Consecutive-anchor delta cosine (stride.py:43-52 interanchor_cos, the
+ * adaptive stride's drift signal, llama.py:784-788; drift.py:23-49
+ * drift_summary's cosines and histogram). For deltas d_0 .. d_{n-1} per
+ * (batch, head), writes cos_out[b, i, h] (dense [B, n-1, H] fp32) =
+ * <d_i, d_{i+1}> / (max(|d_i|, 1e-8) * max(|d_{i+1}|, 1e-8)), fp32 over D.
+ *   a       [B, n, H, D] (strides batch, anchor, head): the deltas, or with
+ *           `sparse` given the dense anchor rows; then d_i = rnd(a_i -
+ *           sparse[b, rows[i], h]) (one rounding to the element type, as the
+ *           reference's tensor subtraction).
+ *   sparse  [B, n_rows, H, D] (strides batch, row, head) or NULL; rows: device
+ *           int64 [n] anchor rows into it (clamped to [0, n_rows)), NULL for 0..n-1.
+ *   hist    NULL, or a device int32 [bins] that each cosine in [lo, hi] adds
+ *           one to (torch.histc's bin rule; the caller zeroes it).
+ * n < 2 launches nothing. Element strides must be even (4-byte pair reads). */
+int da_anchor_delta_cos(const void* a, const int64_t a_str[3],
+                        const void* sparse, const int64_t s_str[3],
+                        const int64_t* rows, int64_t n_rows,
+                        int B, int n, int H, int D,
+                        float* cos_out, int* hist, int bins, float lo, float hi,
+                        int dtype, void* stream);
+
 /* Library identification: the gfx target the code objects were built for. */
 const char* da_build_target(void);
 

@@ -24,6 +24,11 @@ prefill (file:line cite the reference, singhh5050/delta-attention):
                          variants round once per tensor op like the bf16 tensors
   visible_pairs          the algorithmic-work counts (pairs of the sparse pass,
                          sum(i+1) of the query-sparse pass)
+  interanchor_cos        stride.py:43-52 / drift.py:30-32: cosine of consecutive
+                         anchor deltas over the head dim (torch cosine_similarity,
+                         each norm clamped to eps = 1e-8)
+  histc                  drift.py:33: torch.histc's binning (bins over [lo, hi],
+                         x == hi in the last bin, out-of-range and NaN dropped)
 
 Pinning (tests/test_oracle.py): every function is checked against brute force
 on tiny inputs, library routines (torch scaled_dot_product_attention in
@@ -383,3 +388,30 @@ def head_row_cos(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     a = a.astype(np.float64)
     b = b.astype(np.float64)
     return (a * b).sum(-1) / np.maximum(np.sqrt((a * a).sum(-1) * (b * b).sum(-1)), 1e-300)
+
+
+# ---------------------------------------------------------------------------
+# drift signal (stride.py:43-52, drift.py:23-49)
+
+def interanchor_cos(deltas: np.ndarray, eps: float = 1e-8) -> np.ndarray:
+    """[B, n, H, D] deltas -> [B, n-1, H] cosine between consecutive anchors
+    over D: <a, b> / (max(|a|, eps) * max(|b|, eps)), in float64."""
+    d = deltas.astype(np.float64)
+    a, b = d[:, :-1], d[:, 1:]
+    na = np.maximum(np.sqrt((a * a).sum(-1)), eps)
+    nb = np.maximum(np.sqrt((b * b).sum(-1)), eps)
+    return (a * b).sum(-1) / (na * nb)
+
+
+def histc(x: np.ndarray, bins: int, lo: float, hi: float) -> np.ndarray:
+    """torch.histc counts (int64 [bins]): bin = floor((x - lo) * bins / (hi - lo))
+    evaluated in float32 as the GPU code does, x == hi in the last bin, values
+    outside [lo, hi] and NaN dropped. Pure-Python loop: small inputs only."""
+    out = np.zeros(bins, dtype=np.int64)
+    lo32, hi32, nb = np.float32(lo), np.float32(hi), np.float32(bins)
+    for v in np.asarray(x, dtype=np.float32).ravel():
+        if not (lo32 <= v <= hi32):
+            continue
+        k = int(np.float32(np.float32(v - lo32) * nb) / np.float32(hi32 - lo32))
+        out[min(k, bins - 1)] += 1
+    return out

@@ -103,6 +103,9 @@ def test_module_delta_forward_matches_ops(gpu):
     ref = ops.delta_prefill(q, k, v, gamma=64, window=256, sink=16, sm_scale=m.scaling)
     assert torch.equal(out, ref)
     assert m._drift_stats["n"] == (ops.anchor_layout(1536, 64)[2] - 1) * 8
+    _, delta = ops.delta_prefill(q, k, v, gamma=64, window=256, sink=16, sm_scale=m.scaling,
+                                 return_delta=True)
+    assert m._drift_stats["mean"] == pytest.approx(O.interanchor_cos(np64(delta)).mean(), abs=1e-5)
     # fp32 inputs run in bf16 and come back as fp32 (llama.py:382-388, 493-494)
     out32, _ = m.delta_forward(m, q.float(), k.float(), v.float(), None, scaling=m.scaling)
     assert out32.dtype == torch.float32 and torch.equal(out32.to(torch.bfloat16), out)

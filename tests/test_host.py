@@ -76,23 +76,25 @@ def test_next_gamma_rules():
     assert stride.plan_chunks(10000, 4096) == [(0, 4096), (4096, 8192), (8192, 10000)]
 
 
-def test_interanchor_cos_cpu():
-    d = torch.zeros(1, 3, 2, 4)
-    d[0, :, :, 0] = 1.0
-    d[0, 2, 1] = torch.tensor([0.0, 1.0, 0.0, 0.0])
-    mean, mn = stride.interanchor_cos(d)
-    assert mn == pytest.approx(0.0) and mean == pytest.approx(0.75)
-    assert stride.interanchor_cos(d[:, :1]) == (1.0, 1.0)
+def test_interanchor_cos_needs_gpu_deltas():
+    d = torch.zeros(1, 3, 2, 64, dtype=torch.bfloat16)
+    assert stride.interanchor_cos(d[:, :1]) == (1.0, 1.0)     # fewer than two anchors
+    with pytest.raises(AssertionError):
+        stride.interanchor_cos(d)                              # the product runs the kernel
+    with pytest.raises(AssertionError):
+        drift.drift_summary(d, layer_idx=0, gamma=64, seq_len=256)
 
 
-def test_drift_summary_and_aggregate():
-    torch.manual_seed(0)
-    s = drift.drift_summary(torch.randn(1, 9, 4, 16), layer_idx=3, gamma=64, seq_len=640)
-    assert s["n"] == 8 * 4 and sum(s["hist"]) == s["n"] and s["layer"] == 3
+def test_aggregate_drift():
+    hist = [0] * drift.HIST_BINS
+    hist[30] = 32
+    s = {"layer": 3, "gamma": 64, "seq_len": 640, "n": 32, "mean": 0.5, "p10": 0.4, "p50": 0.5,
+         "p90": 0.6, "hist_bins": drift.HIST_BINS, "hist_range": list(drift.HIST_RANGE), "hist": hist}
     json.dumps(s)
     agg = drift.aggregate_drift([s, dict(s, mean=1.0)])
     assert agg[3]["n"] == 64 and agg[3]["requests"] == 2
     assert agg[3]["mean"] == pytest.approx((s["mean"] + 1.0) / 2)
+    assert agg[3]["hist"][30] == 64 and sum(agg[3]["hist"]) == 64
     with pytest.raises(ValueError):
         drift.aggregate_drift([dict(s, hist_bins=10)])
     assert len(drift.hist_bin_edges()) == drift.HIST_BINS + 1

@@ -391,3 +391,31 @@ def test_delta_decode_steps_schedule():
     # gamma_dec 1: every step is an anchor, i.e. dense decode
     for o, d in zip(O.delta_decode_steps(qs, k, v, 8, 2, 0.5, gamma_dec=1), dense):
         np.testing.assert_array_equal(o, d)
+
+
+def test_interanchor_cos_closed_forms_and_library():
+    d = np.zeros((1, 5, 2, 4))
+    d[0, 0, :, 0] = 1.0
+    d[0, 1, :, 0] = 3.0                     # parallel: 1
+    d[0, 2, 0, 0] = -2.0                    # antiparallel: -1 (head 0)
+    d[0, 2, 1, 1] = 5.0                     # orthogonal: 0 (head 1)
+    d[0, 3] = 0.0                           # zero delta: clamped norm gives 0
+    d[0, 4, :, 2] = 1.0
+    c = O.interanchor_cos(d)
+    np.testing.assert_allclose(c[0, :, 0], [1.0, -1.0, 0.0, 0.0], atol=1e-15)
+    np.testing.assert_allclose(c[0, :, 1], [1.0, 0.0, 0.0, 0.0], atol=1e-15)
+    # torch's cosine_similarity (the reference's call) on random deltas
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 9, 3, 16))
+    t = torch.from_numpy(x)
+    ref = F.cosine_similarity(t[:, :-1], t[:, 1:], dim=-1).numpy()
+    np.testing.assert_allclose(O.interanchor_cos(x), ref, rtol=1e-12, atol=1e-14)
+
+
+def test_histc_edges_and_library():
+    x = np.array([-1.0, -0.5, 0.0, 0.99, 1.0, 1.5, -1.01, np.nan], dtype=np.float32)
+    np.testing.assert_array_equal(O.histc(x, 4, -1.0, 1.0), [1, 1, 1, 2])
+    rng = np.random.default_rng(6)
+    y = rng.uniform(-1.2, 1.2, 3000).astype(np.float32)
+    ref = torch.histc(torch.from_numpy(y), bins=40, min=-1.0, max=1.0).numpy().astype(np.int64)
+    np.testing.assert_array_equal(O.histc(y, 40, -1.0, 1.0), ref)
