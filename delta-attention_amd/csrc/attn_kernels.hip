@@ -59,9 +59,12 @@ namespace da {
 #ifndef DA_ROWS_ITEMS
 #define DA_ROWS_ITEMS 8192
 #endif
-// Split items a decode-row launch aims for.
+// Split items a decode-row launch aims for: one workgroup per resident slot
+// of the 256-CU gfx950 (two per CU), so the items run in a single round
+// (dense row over 131072 keys: 106-111 us against 118 us at 1024 items and
+// 131 us at 2048).
 #ifndef DA_DECODE_ITEMS
-#define DA_DECODE_ITEMS 1024
+#define DA_DECODE_ITEMS 512
 #endif
 constexpr int NWAVE = DA_WAVES;
 static_assert(NWAVE == 4 || NWAVE == 8, "4 or 8 waves per workgroup");
@@ -847,7 +850,7 @@ static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
 }
 
 // One decode row per batch at the end of the cache: its list is the sink
-// tiles plus the window tiles (all tiles without a window); ~1024 items.
+// tiles plus the window tiles (all tiles without a window); ~512 items.
 static QsparsePlan plan_decode(int B, int Hq, int Hkv, int n_keys, int D, int window, int sink) {
   const int64_t all = (n_keys + BN - 1) / BN;
   int64_t vis = all;
