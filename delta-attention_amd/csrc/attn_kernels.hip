@@ -591,48 +591,79 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
       dl = (DA_LDS u32x2*)&smem[0][0][0] + ((gl * GT + mflat % GT) * 2 + lg) * (NDT * 4);
       __syncthreads();   // every wave is done with the K/V stages
     }
-    // element (dt, jq) of this lane: dims 32 dt + 8 jq + 4 lg .. +3
-    auto dslot = [&](int dt, int jq) -> DA_LDS u32x2* {
-      return pre ? dl + 8 * dt + 2 * jq : dl + dt * 4 + jq;
+    // element (dt, jq) of this lane: dims 32 dt + 8 jq + 4 lg .. +3. One code
+    // path per delta layout (PRE: the prefetched dense rows), so that the
+    // anchor lanes issue all their reads, then all their writes, instead of
+    // one LDS round trip per element while the other waves wait.
+    auto fused_out = [&](auto pre_tag) {
+      constexpr bool PRE = decltype(pre_tag)::value;
+      auto dslot = [&](int dt, int jq) -> DA_LDS u32x2* {
+        return PRE ? dl + 8 * dt + 2 * jq : dl + dt * 4 + jq;
+      };
+      if (live && irow % a.gamma == 0) {
+        const int64_t g = irow / a.gamma;
+        u32x2 dn[NDT][4];
+        if constexpr (PRE) {
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) dn[dt][jq] = *dslot(dt, jq);
+        } else {
+          const char* dp = (const char*)a.dsel +
+                           ((int64_t)b * a.dsel_b + (int64_t)hrow * a.dsel_h + g * a.dsel_a) * esz;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq)
+              dn[dt][jq] = *(const u32x2*)(dp + (32 * dt + 8 * jq + 4 * lg) * esz);
+        }
+        u32x2 dv[NDT][4];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int jq = 0; jq < 4; ++jq)
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+              dv[dt][jq][e] = E::pack2(E::lo(dn[dt][jq][e]) - E::lo(sp[dt][jq][e]),
+                                       E::hi(dn[dt][jq][e]) - E::hi(sp[dt][jq][e]));
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int jq = 0; jq < 4; ++jq) *dslot(dt, jq) = dv[dt][jq];
+        if (a.dout) {
+          char* op = (char*)a.dout +
+                     ((int64_t)b * a.dout_b + (int64_t)hrow * a.dout_h + g * a.dout_a) * esz;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq)
+              *(u32x2*)(op + (32 * dt + 8 * jq + 4 * lg) * esz) = dv[dt][jq];
+        }
+      }
+      __syncthreads();
+      if (live) {
+        char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
+                                 (int64_t)qrow * a.os_s) * esz;
+        u32x2 dv[NDT][4];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int jq = 0; jq < 4; ++jq) dv[dt][jq] = *dslot(dt, jq);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int jq = 0; jq < 4; ++jq) {
+            u32x2 o;
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+              o[e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[dt][jq][e]),
+                              E::hi(sp[dt][jq][e]) + E::hi(dv[dt][jq][e]));
+            *(u32x2*)(op + (32 * dt + 8 * jq + 4 * lg) * esz) = o;
+          }
+      }
     };
-    if (live && irow % a.gamma == 0) {
-      const int64_t g = irow / a.gamma;
-      const char* dp = (const char*)a.dsel +
-                       ((int64_t)b * a.dsel_b + (int64_t)hrow * a.dsel_h + g * a.dsel_a) * esz;
-      char* op = a.dout ? (char*)a.dout +
-                              ((int64_t)b * a.dout_b + (int64_t)hrow * a.dout_h + g * a.dout_a) * esz
-                        : nullptr;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq) {
-          const int d = 32 * dt + 8 * jq + 4 * lg;
-          const u32x2 dn = pre ? *dslot(dt, jq) : *(const u32x2*)(dp + d * esz);
-          u32x2 dv;
-#pragma unroll
-          for (int e = 0; e < 2; ++e)
-            dv[e] = E::pack2(E::lo(dn[e]) - E::lo(sp[dt][jq][e]), E::hi(dn[e]) - E::hi(sp[dt][jq][e]));
-          *dslot(dt, jq) = dv;
-          if (op) *(u32x2*)(op + d * esz) = dv;
-        }
-    }
-    __syncthreads();
-    if (live) {
-      char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
-                               (int64_t)qrow * a.os_s) * esz;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq) {
-          const int d = 32 * dt + 8 * jq + 4 * lg;
-          const u32x2 dv = *dslot(dt, jq);
-          u32x2 o;
-#pragma unroll
-          for (int e = 0; e < 2; ++e)
-            o[e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[e]), E::hi(sp[dt][jq][e]) + E::hi(dv[e]));
-          *(u32x2*)(op + d * esz) = o;
-        }
-    }
+    if (pre) fused_out(std::true_type());
+    else fused_out(std::false_type());
     return;
   }
   if (MODE == MODE_SPARSE) {
