@@ -191,3 +191,32 @@ def test_decode_checks(lib):
     assert call(n=0) == L.DA_ERR_INVALID_ARG
     assert call(window=-1) == L.DA_ERR_INVALID_ARG
     assert call(D=80) == L.DA_ERR_HEAD_DIM
+
+
+def test_anchor_delta_cos_checks(lib):
+    P = ctypes.c_void_p
+    a3 = _s3(64 * 8 * 128, 8 * 128, 128)
+
+    def call(a=16, n=64, D=128, dtype=L.DA_BF16, cos=16, hist=None, bins=0, lo=-1.0, hi=1.0,
+             sparse=None, n_rows=0, s3=None, a_str=a3):
+        return lib.da_anchor_delta_cos(P(a), a_str, P(sparse) if sparse else None, s3, None, n_rows,
+                                       1, n, 8, D, P(cos), P(hist) if hist else None, bins,
+                                       lo, hi, dtype, None)
+    assert call(dtype=5) == L.DA_ERR_DTYPE
+    assert call(D=96) == L.DA_ERR_HEAD_DIM
+    assert call(n=-1) == L.DA_ERR_INVALID_ARG
+    assert call(n=1) == L.DA_OK and call(n=0) == L.DA_OK      # no consecutive pair: nothing to do
+    assert call(a=0) == L.DA_ERR_INVALID_ARG
+    assert call(cos=0) == L.DA_ERR_INVALID_ARG
+    assert call(hist=16, bins=0) == L.DA_ERR_INVALID_ARG
+    assert call(hist=16, bins=40, lo=1.0, hi=1.0) == L.DA_ERR_INVALID_ARG
+    assert call(sparse=16, n_rows=0, s3=a3) == L.DA_ERR_INVALID_ARG
+    assert call(sparse=16, n_rows=100, s3=None) == L.DA_ERR_INVALID_ARG
+    assert call(a=18) == L.DA_ERR_ALIGNMENT
+    assert call(a_str=_s3(64 * 8 * 128, 8 * 128, 127)) == L.DA_ERR_ALIGNMENT
+
+
+def test_split_plans_refuse_grid_overflow(lib):
+    # a selected-rows launch whose work items would not fit a 32-bit grid
+    assert lib.da_qsparse_workspace_bytes(1, 32, 8, 2_000_000_000, 131072, 128) == 0
+    assert lib.da_qsparse_workspace_bytes(1, 32, 8, 2174, 131072, 128) > 0
