@@ -899,10 +899,12 @@ template <int MODE>
 static void dispatch_attn(const AttnArgs& a, int D, int dtype, hipStream_t s) {
   if (dtype == DA_BF16) {
     if (D == 128) launch_attn<__bf16, 128, MODE>(a, s);
-    else launch_attn<__bf16, 64, MODE>(a, s);
+    else if (D == 64) launch_attn<__bf16, 64, MODE>(a, s);
+    else launch_attn<__bf16, 32, MODE>(a, s);
   } else {
     if (D == 128) launch_attn<_Float16, 128, MODE>(a, s);
-    else launch_attn<_Float16, 64, MODE>(a, s);
+    else if (D == 64) launch_attn<_Float16, 64, MODE>(a, s);
+    else launch_attn<_Float16, 32, MODE>(a, s);
   }
 }
 
@@ -1071,16 +1073,19 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   const int n_tiles = B * Hkv * p.n_mtiles * m.wgs;
   if (dtype == DA_BF16) {
     if (D == 128) launch_merge<__bf16, 128>(m, n_tiles, s);
-    else launch_merge<__bf16, 64>(m, n_tiles, s);
+    else if (D == 64) launch_merge<__bf16, 64>(m, n_tiles, s);
+    else launch_merge<__bf16, 32>(m, n_tiles, s);
   } else {
     if (D == 128) launch_merge<_Float16, 128>(m, n_tiles, s);
-    else launch_merge<_Float16, 64>(m, n_tiles, s);
+    else if (D == 64) launch_merge<_Float16, 64>(m, n_tiles, s);
+    else launch_merge<_Float16, 32>(m, n_tiles, s);
   }
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }
 
 extern "C" size_t da_qsparse_workspace_bytes(int B, int Hq, int Hkv, int n, int Skv, int D) {
-  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n < 1 || Skv < 1 || (D != 64 && D != 128))
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n < 1 || Skv < 1 ||
+      (D != 32 && D != 64 && D != 128))
     return 0;
   return plan_rows(B, Hq, Hkv, n, Skv, D).ws_bytes;
 }
@@ -1119,7 +1124,7 @@ extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
 
 extern "C" size_t da_decode_workspace_bytes(int B, int Hq, int Hkv, int n_keys, int D, int window,
                                             int sink) {
-  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n_keys < 1 || (D != 64 && D != 128) ||
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n_keys < 1 || (D != 32 && D != 64 && D != 128) ||
       window < 0 || sink < 0)
     return 0;
   return plan_decode(B, Hq, Hkv, n_keys, D, window, sink).ws_bytes;

@@ -14,7 +14,7 @@ inline bool strides8(const int64_t s[3]) { return s[0] % 8 == 0 && s[1] % 8 == 0
 
 inline int check_common(int B, int Hq, int Hkv, int D, int dtype) {
   if (dtype != DA_BF16 && dtype != DA_FP16) return DA_ERR_DTYPE;
-  if (D != 64 && D != 128) return DA_ERR_HEAD_DIM;
+  if (D != 32 && D != 64 && D != 128) return DA_ERR_HEAD_DIM;
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return DA_ERR_INVALID_ARG;
   return DA_OK;
 }

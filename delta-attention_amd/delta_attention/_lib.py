@@ -46,7 +46,7 @@ EXPORTS = (
 
 _ERR_TEXT = {
     DA_ERR_INVALID_ARG: "invalid argument (shape, stride, range or null pointer)",
-    DA_ERR_HEAD_DIM: "unsupported head_dim (64 and 128 are supported)",
+    DA_ERR_HEAD_DIM: "unsupported head_dim (32, 64 and 128 are supported)",
     DA_ERR_DTYPE: "unsupported dtype (bfloat16 and float16 are supported)",
     DA_ERR_ALIGNMENT: "tensor rows must be 16-byte aligned (strides multiple of 8 elements)",
     DA_ERR_WORKSPACE: "workspace missing or too small",

@@ -13,7 +13,7 @@ import torch
 
 from . import ops
 
-SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_HEAD_DIMS = (32, 64, 128)
 
 
 class _attention(torch.autograd.Function):

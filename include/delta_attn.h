@@ -36,7 +36,7 @@ extern "C" {
 
 #define DA_OK 0
 #define DA_ERR_INVALID_ARG (-1)      /* shape, stride, range or null-pointer error */
-#define DA_ERR_HEAD_DIM (-2)         /* head_dim not supported (64 and 128 are) */
+#define DA_ERR_HEAD_DIM (-2)         /* head_dim not supported (32, 64 and 128 are; the RoPE prologue takes 64 and 128) */
 #define DA_ERR_DTYPE (-3)            /* dtype not DA_BF16 / DA_FP16 */
 #define DA_ERR_ALIGNMENT (-4)        /* pointer or stride breaks 16-byte row alignment */
 #define DA_ERR_WORKSPACE (-5)        /* workspace missing or smaller than required */

@@ -119,6 +119,7 @@ def test_rope_checks(lib):
 
     assert call(dtype=5) == L.DA_ERR_DTYPE
     assert call(D=96) == L.DA_ERR_HEAD_DIM
+    assert call(D=32) == L.DA_ERR_HEAD_DIM       # the prologue takes 64 and 128 only
     assert call(cos=0) == L.DA_ERR_INVALID_ARG
     assert call(cs=(0, 64)) == L.DA_ERR_INVALID_ARG          # table rows shorter than D
     assert call(cos=24) == L.DA_ERR_ALIGNMENT

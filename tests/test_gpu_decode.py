@@ -29,6 +29,7 @@ def _rand(B, H, Hkv, n, D, seed, dtype=torch.bfloat16):
     (1, 32, 8, 8192, 128, 2048, 128),    # sink + last window of a long cache
     (1, 32, 8, 8192, 128, 0, 0),         # the dense anchor row
     (2, 8, 2, 3000, 64, 256, 16),        # head_dim 64, batch 2
+    (1, 8, 2, 3000, 32, 256, 16),        # head_dim 32
     (1, 8, 8, 1000, 128, 900, 200),      # n <= sink + window: every key
     (1, 4, 1, 1, 128, 16, 4),            # a one-key cache
     (1, 40, 8, 5000, 128, 4096, 64),     # GQA 5

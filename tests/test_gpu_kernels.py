@@ -37,6 +37,8 @@ def _sparse_case(B, H, Hkv, S, D, window, sink, qb=64, dtype=torch.bfloat16, see
     (1, 4, 4, 256, 128, 40, 3),        # window < q_block: rows with few keys
     (1, 4, 2, 384, 128, 4096, 0),      # window covers everything: causal
     (1, 4, 2, 384, 64, 8, 1000),       # sinks cover everything: causal
+    (1, 8, 2, 1100, 32, 300, 16),      # head_dim 32
+    (2, 6, 3, 500, 32, 64, 0),         # head_dim 32, GQA 2, batch 2
 ])
 def test_sparse_attention_parity(gpu, B, H, Hkv, S, D, window, sink):
     _sparse_case(B, H, Hkv, S, D, window, sink)
@@ -152,3 +154,26 @@ def test_apply_delta_variable_bit_exact(gpu):
     deltas = dense - sparse[:, idx]
     owner = torch.searchsorted(idx, torch.arange(s_p), right=True) - 1
     assert torch.equal(got.cpu(), sparse[:, :s_p] + deltas[:, owner])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_qsparse_head_dim_32(gpu, dtype):
+    """delta_kernel.attention with head_dim 32 (the reference's wrapper accepts
+    it, delta_kernel.py:268): sorted rows and an unsorted mask, native GQA."""
+    q, k, v = gen_qkv(1, 8, 2, 1500, 32, seed=9, dtype=dtype)
+    rows = torch.tensor([0, 7, 64, 640, 999, 1499], device="cuda")
+    out = _qsa(q[:, :, rows], k, v, rows.unsqueeze(0), 32 ** -0.5)
+    ref = O.qsparse_attention(np64(q)[:, :, rows.cpu().numpy()], np64(k), np64(v), rows.cpu().numpy(),
+                              32 ** -0.5)
+    assert_close(np64(out), ref, what="qsa d32")
+    mask = torch.randperm(1500, generator=torch.Generator().manual_seed(3))[:200].unsqueeze(0)
+    out = _qsa(q[:, :, :200], k, v, mask.cuda(), 32 ** -0.5)
+    ref = O.qsparse_attention(np64(q)[:, :, :200], np64(k), np64(v), mask[0].numpy(), 32 ** -0.5)
+    assert_close(np64(out), ref, what="qsa d32 unsorted")
+
+
+def test_head_dim_256_is_refused(gpu):
+    from delta_attention.delta_kernel import attention
+    q = torch.zeros(1, 2, 8, 256, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="no MI355X kernel"):
+        attention(q, q, q, torch.arange(8, device="cuda")[None], 0.1)

@@ -32,6 +32,8 @@ def _layer(B, H, Hkv, S, D, gamma, window, sink, mode="delta", seed=0, dtype=tor
     (2, 10, 2, 1024, 128, 64, 256, 64),   # Qwen3 geometry (GQA 5, batch 2), shortened
     (1, 4, 4, 1200, 128, 32, 128, 8),     # s % gamma != 0
     (1, 4, 1, 768, 64, 128, 192, 0),      # gamma 128
+    (1, 8, 2, 1300, 32, 64, 256, 16),     # head_dim 32 (fused order)
+    (1, 4, 4, 900, 32, 128, 128, 8),      # head_dim 32, gamma 128 with MHA (fused, 128-row tiles)
 ])
 def test_delta_prefill_parity(gpu, B, H, Hkv, S, D, gamma, window, sink):
     got, ref, _ = _layer(B, H, Hkv, S, D, gamma, window, sink)
