@@ -35,6 +35,7 @@
 //   * Per key tile, 32 MFMAs in one scheduling region keep the matrix pipe
 //     fed: the exponentials of tile t run under the score MFMAs of tile t+1,
 //     then the PV MFMAs of tile t follow with their V reads running ahead.
+//     In the key-sparse modes that region runs at raised wave priority.
 #include <type_traits>
 
 #include "device_common.h"
@@ -450,6 +451,13 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   //   for the DMA, barrier.
   auto step = [&](int t, auto last_tag, f32x16 (&cur)[NH], f32x16 (&nxt)[NH]) {
     constexpr bool LAST = decltype(last_tag)::value;   // t == nt - 1
+    // Key-sparse modes: the wave runs its MFMA block (exponentials, score
+    // MFMAs, PV MFMAs) at raised priority and drops it for the mask, row max,
+    // DMA wait and barrier, so that the other wave on the SIMD fills those
+    // phases instead of competing for issue while this one's MFMAs are ready
+    // (kernel (1) 0.9-1.3 % faster; the query-sparse mode measured neutral
+    // to slower and keeps one priority).
+    if constexpr (KSPARSE) __builtin_amdgcn_s_setprio(1);
     const int P = t & 1;
     if (t + 2 < nt) issue_k(t + 2, P);
     if (t + 1 < nt) issue_v(t + 1, P ^ 1);
@@ -478,6 +486,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
         acc[dt] = E::mfma(va, pf, acc[dt]);
       }
     }
+    if constexpr (KSPARSE) __builtin_amdgcn_s_setprio(0);
 #if DA_SCHED
     if (!LAST) {
       // phase A: K reads run 3 MFMAs ahead, ~6 of the 96 softmax VALU ops
