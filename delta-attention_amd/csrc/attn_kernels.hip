@@ -421,14 +421,17 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     const float mx = __builtin_fmaxf(__builtin_fmaxf(p[0], p[1]), __builtin_fmaxf(p[2], p[3]));
     return max32(mx) * c2;          // scaling by c2 > 0 keeps the max
   };
-  // lazy online-softmax update with the scaled tile max: the running max
-  // moves (and O, l are rescaled) only when some row's tile max exceeds it by
-  // more than 2^RESCALE_THRESH
+  // lazy online-softmax update with the scaled tile max: a row's running max
+  // moves (and its O, l are rescaled) only when its tile max exceeds it by
+  // more than 2^RESCALE_THRESH. The decision is per row (the other rows of the
+  // wave multiply by exactly 1), so a row's result does not depend on which
+  // rows share its wave: every head packing and row grouping gives the same
+  // bits.
   auto update = [&](float mx) {
-    if (__any(mx > m_i + RESCALE_THRESH)) {
-      const float m_new = fmaxf(m_i, mx);
-      const float alpha = fast_exp2(m_i - m_new);
-      m_i = m_new;
+    const bool up = mx > m_i + RESCALE_THRESH;
+    if (__any(up)) {
+      const float alpha = up ? fast_exp2(m_i - mx) : 1.f;
+      m_i = up ? mx : m_i;
       l_i *= alpha;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
@@ -994,7 +997,7 @@ extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, v
 
 extern "C" int da_fused_delta_rows(int Hq, int Hkv) {
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;
-  return BM / tile_heads(Hq / Hkv);
+  return BM;
 }
 
 extern "C" int da_sparse_attn_delta_fwd(const void* q, const void* k, const void* v, void* out,
@@ -1022,6 +1025,10 @@ extern "C" int da_sparse_attn_delta_fwd(const void* q, const void* k, const void
   a.dout = delta_out;
   if (delta_out) { a.dout_b = dl_str[0]; a.dout_h = dl_str[1]; a.dout_a = dl_str[2]; }
   a.gamma = gamma; a.s_p = s_p; a.n_anchor = s_p / gamma;
+  // every stride group needs its anchor in the row tile: a gamma that does not
+  // divide the two-head tile height takes one head per 128-row tile (the
+  // per-row softmax makes the packing invisible in the results)
+  if ((BM / a.Gs) % gamma != 0) { a.Gs = 1; a.n_hs = a.G; }
   if ((rc = sparse_items(a)) != DA_OK) return rc;
   (void)hipGetLastError();
   dispatch_attn<MODE_FUSED>(a, D, dtype, (hipStream_t)stream);

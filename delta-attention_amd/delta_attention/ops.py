@@ -88,8 +88,9 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, windo
 
 
 def fused_delta_rows(H: int, Hkv: int) -> int:
-    """Row-tile height of the key-sparse kernel (64 for an even GQA ratio, 128
-    for an odd one); the fused delta epilogue needs gamma to divide it."""
+    """Largest row-tile height of the fused delta launch (128): the fused
+    order needs gamma to divide it (two heads per 64-row tile when the GQA
+    ratio is even and gamma divides 64, else one head per 128-row tile)."""
     return int(L.lib().da_fused_delta_rows(int(H), int(Hkv)))
 
 

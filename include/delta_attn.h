@@ -100,10 +100,10 @@ int da_sparse_attn_delta_fwd(const void* q, const void* k, const void* v, void* 
                              int dtype, void* stream);
 
 /*
- * Row-tile height of the key-sparse kernel for this head geometry: 64 when
- * Hq / Hkv is even (two heads per tile), 128 when it is odd (one head per
- * tile); 0 for invalid head counts. The fused delta epilogue needs gamma to
- * divide it.
+ * Largest row-tile height the fused delta launch can use for this head
+ * geometry (128; 0 for invalid head counts): gamma must divide it. The launch
+ * packs two heads per 64-row tile when Hq / Hkv is even and gamma divides 64,
+ * else one head per 128-row tile; the results do not depend on the packing.
  */
 int da_fused_delta_rows(int Hq, int Hkv);
 

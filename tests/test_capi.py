@@ -130,10 +130,10 @@ def test_rope_checks(lib):
 
 
 def test_fused_delta_rows_and_checks(lib):
-    assert lib.da_fused_delta_rows(32, 8) == 64      # GQA 4: two heads per 64-row tile
-    assert lib.da_fused_delta_rows(8, 8) == 128      # MHA
-    assert lib.da_fused_delta_rows(6, 3) == 64
-    assert lib.da_fused_delta_rows(40, 8) == 128     # GQA 5: one head per 128-row tile
+    # gamma must divide 128 whatever the head packing (two heads per 64-row
+    # tile for gamma | 64 and an even GQA ratio, else one head per 128 rows)
+    for hq, hkv in ((32, 8), (8, 8), (6, 3), (40, 8)):
+        assert lib.da_fused_delta_rows(hq, hkv) == 128
     assert lib.da_fused_delta_rows(6, 4) == 0 and lib.da_fused_delta_rows(0, 1) == 0
     s3 = _s3(128 * 32 * 128, 128, 32 * 128)
     q3 = _s3(32 * 4096 * 128, 4096 * 128, 128)
@@ -145,7 +145,8 @@ def test_fused_delta_rows_and_checks(lib):
             1, Hq, Hkv, S, 128, q3, k3, k3, s3, 512, 64, 64, 0.1,
             ctypes.c_void_p(dense), s3, gamma, s_p, ctypes.c_void_p(dout), s3, L.DA_BF16, None)
 
-    assert call(gamma=128, s_p=3840) == L.DA_ERR_INVALID_ARG     # gamma must divide the 64-row tile
+    assert call(gamma=256, s_p=3840) == L.DA_ERR_INVALID_ARG     # gamma must divide 128
+    assert call(gamma=48, s_p=3840) == L.DA_ERR_INVALID_ARG
     assert call(s_p=3900) == L.DA_ERR_INVALID_ARG                # s_p % gamma != 0
     assert call(s_p=4160) == L.DA_ERR_INVALID_ARG                # s_p > S
     assert call(dense=0) == L.DA_ERR_INVALID_ARG

@@ -179,6 +179,8 @@ def test_adaptive_stride_path(gpu):
     (1, 6, 3, 777, 128, 32, 100, 0),      # GQA 2
     (1, 8, 2, 600, 128, 1, 128, 16),      # gamma 1: every row before the tail is an anchor
     (2, 10, 2, 1100, 128, 64, 256, 16),   # GQA 5 (Qwen3): one head per 128-row tile
+    (1, 8, 2, 1500, 128, 128, 256, 16),   # GQA 4, gamma 128: one head per 128-row tile,
+                                          # against kernel (1)'s two-head packing
 ])
 def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
     """Kernel (3) fused into kernel (1)'s epilogue (kernel (2) first) gives the
@@ -200,7 +202,8 @@ def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
     assert_close(np64(a), ref, what=f"fused B{B} H{H}/{Hkv} S{S} g{gamma}")
 
 
-@pytest.mark.parametrize("H,Hkv,D,gamma", [(8, 2, 128, 64), (4, 4, 64, 32), (10, 2, 128, 16)])
+@pytest.mark.parametrize("H,Hkv,D,gamma", [(8, 2, 128, 64), (4, 4, 64, 32), (10, 2, 128, 16),
+                                            (8, 2, 64, 128)])
 def test_fused_delta_bit_identical_fp16(gpu, H, Hkv, D, gamma):
     """The fused order in fp16 (the delta and the add round to fp16): same bits
     as the three-kernel sequence, within the T1 gate of the oracle."""
@@ -222,8 +225,8 @@ def test_fused_delta_bit_identical_fp16(gpu, H, Hkv, D, gamma):
 
 
 def test_unfused_when_gamma_exceeds_the_tile(gpu):
-    # gamma 128 with GQA 4 (64-row tiles): the three-kernel path runs
+    # gamma 256 does not divide the largest fused tile: the three-kernel path runs
     from delta_attention import ops
-    assert ops.fused_delta_rows(8, 2) % 128 != 0
-    got, ref, _ = _layer(1, 8, 2, 1024, 128, 128, 256, 16, seed=3)
-    assert_close(got, ref, what="gamma 128, gqa 4")
+    assert ops.fused_delta_rows(8, 2) % 256 != 0
+    got, ref, _ = _layer(1, 8, 2, 1024, 128, 256, 256, 16, seed=3)
+    assert_close(got, ref, what="gamma 256, gqa 4")
