@@ -314,16 +314,22 @@ def model_prefill(a, dev):
         "first_token": int(tok[0]), "init_s": round(init_s, 2),
     }
     if a.decode_tokens > 1:
-        # generation after the prefill: ms per decode token, dense vs delta decode
+        # generation after the prefill: ms per decode token, dense vs delta
+        # decode, each step launched eagerly or replayed from HIP graphs
         dec = {}
         for mode in ("dense", "delta"):
-            cfg.decode_mode, cfg.gamma_dec = mode, a.gamma_dec
-            steps_ms = []
-            toks = model.generate_greedy(ids, a.decode_tokens, step_ms=steps_ms)
-            dec[mode] = {"ms_per_token": round(float(np.median(steps_ms)), 3),
-                         "tokens": int(toks.shape[1])}
+            for graph in (False, True):
+                cfg.decode_mode, cfg.gamma_dec = mode, a.gamma_dec
+                steps_ms = []
+                toks = model.generate_greedy(ids, a.decode_tokens, step_ms=steps_ms, graph=graph)
+                later = steps_ms[2:] or steps_ms     # graphs: the first step of each kind records
+                dec[mode + ("_graph" if graph else "")] = {
+                    "ms_per_token": round(float(np.median(steps_ms)), 3),
+                    "mean_ms_after_step2": round(float(np.mean(later)), 3),
+                    "tokens": int(toks.shape[1])}
         line["decode"] = dict(dec, gamma_dec=a.gamma_dec, context=S,
-                              note="median wall time of one decode step (32 layers + lm_head)")
+                              note="median wall time of one decode step (all layers + lm_head); "
+                                   "_graph: each step kind recorded once and replayed")
     print(json.dumps(line), flush=True)
 
 

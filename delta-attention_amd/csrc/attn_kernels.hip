@@ -104,6 +104,10 @@ struct AttnArgs {
   int64_t rl_b;
   int chunk;        // query-sparse mode: key tiles of the tile list per split item
   int n_splits;
+  // query-sparse mode: when set, the key count is *n_kv_dev (clamped to
+  // [1, n_kv]) and chunk = ceil(list / n_splits): the launch stays valid as a
+  // cache grows (decode rows under graph replay)
+  const int* n_kv_dev;
   float* part_o;    // [item][BM][D]
   float* part_ml;   // [item][2][BM]  (running max, row sum)
   // MODE_FUSED: dense anchor rows [B, n_anchor, Hq, D] (strides batch, head,
@@ -212,6 +216,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   const int b = bh / a.Hkv;
   const int G = a.G;
   const int GT = KSPARSE ? a.Gs : G;   // heads packed in this row tile
+  const int n_kv = (KSPARSE || !a.n_kv_dev) ? a.n_kv : min(max(*a.n_kv_dev, 1), a.n_kv);
   // Fused epilogue: a tile wholly in the dense tail writes nothing. The other
   // tiles keep the row grouping of the plain launch (the wave-wide rescale
   // decisions, hence the rounded results, are the same).
@@ -232,8 +237,8 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     // row_last == NULL: every row sees all keys (a decode row at the end of
     // the cache); window > 0: the row sees sinks + its last `window` keys
     qrow = a.q_rows ? (int)min(max(a.q_rows[irow], (int64_t)0), (int64_t)(a.n_q - 1)) : irow;
-    int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + irow] : (int64_t)a.n_kv - 1;
-    if (lim > a.n_kv - 1) lim = a.n_kv - 1;
+    int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + irow] : (int64_t)n_kv - 1;
+    if (lim > n_kv - 1) lim = n_kv - 1;
     hi = valid ? (int)(lim < -1 ? -1 : lim) : -1;
     lo = a.window > 0 ? hi - a.window + 1 : 0;
   }
@@ -295,9 +300,10 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   tile_list(hi_max, lo_min, sink, n_first, second_t0, n_second);
   int nt = n_first + n_second, t_off = 0;
   if (!KSPARSE) {
-    t_off = split * a.chunk;
+    const int chunk = a.n_kv_dev ? max(1, (nt + a.n_splits - 1) / a.n_splits) : a.chunk;
+    t_off = split * chunk;
     if (t_off >= nt) return;   // past the list: the merge skips this split
-    nt = min(a.chunk, nt - t_off);
+    nt = min(chunk, nt - t_off);
   }
 
   const char* kbase = (const char*)a.k + ((int64_t)b * a.ks_b + (int64_t)hk * a.ks_h) * esz;
@@ -306,8 +312,8 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   // offsets are 32 x 32 -> 64-bit products
   const uint32_t krow_b = (uint32_t)(a.ks_s * (int64_t)esz);
   const uint32_t vrow_b = (uint32_t)(a.vs_s * (int64_t)esz);
-  const uint64_t kend = (uint64_t)kbase + (uint64_t)(uint32_t)a.n_kv * krow_b;
-  const uint64_t vend = (uint64_t)vbase + (uint64_t)(uint32_t)a.n_kv * vrow_b;
+  const uint64_t kend = (uint64_t)kbase + (uint64_t)(uint32_t)n_kv * krow_b;
+  const uint64_t vend = (uint64_t)vbase + (uint64_t)(uint32_t)n_kv * vrow_b;
 
   // ---- DMA source offsets: wave `wave`, chunk c fills LDS slots
   //      (c * NWAVE + wave) * 64 + lane of the tile; slot -> (row, swizzled chunk) ----
@@ -394,7 +400,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   auto mask = [&](int t, f32x16 (&x)[NH]) {
     const int n0 = tile_n0(t);
     const int n1 = n0 + BN - 1;
-    const bool full = (n1 <= hi_min) && (n1 < a.n_kv) && (n1 < sink || n0 >= lo_max);
+    const bool full = (n1 <= hi_min) && (n1 < n_kv) && (n1 < sink || n0 >= lo_max);
     if (!full) {
 #pragma unroll
       for (int hf = 0; hf < NH; ++hf)
@@ -723,6 +729,7 @@ struct MergeArgs {
   const int64_t* row_last;
   int64_t rl_b;
   int n_rows, G, Hkv, n_kv, n_mtiles, n_splits, chunk;
+  const int* n_kv_dev;   // as in AttnArgs
   int window, sink;
   int lanes;        // P: threads sharing one (row, 8-column) task, splits s = p mod P
   int wgs;          // workgroups per row tile
@@ -750,12 +757,13 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   const int G = a.G;
 
   // Same tile list as the split kernel saw, hence the same set of written splits.
+  const int n_kv = a.n_kv_dev ? min(max(*a.n_kv_dev, 1), a.n_kv) : a.n_kv;
   int my_hmax = -1, my_lmin = 0x7fffffff;
   if (tid < BM) {
     const int mflat = mt * BM + tid;
     if (mflat < a.n_rows * G) {
-      int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + mflat / G] : (int64_t)a.n_kv - 1;
-      if (lim > a.n_kv - 1) lim = a.n_kv - 1;
+      int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + mflat / G] : (int64_t)n_kv - 1;
+      if (lim > n_kv - 1) lim = n_kv - 1;
       my_hmax = (int)(lim < -1 ? -1 : lim);
       my_lmin = a.window > 0 ? my_hmax - a.window + 1 : 0;
     }
@@ -774,7 +782,9 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   const int lo_min = min(min(s_lmin[0], s_lmin[1]), min(s_lmin[2], s_lmin[3]));
   int n_first, second_t0, n_second;
   tile_list(hi_max, lo_min, a.window > 0 ? a.sink : 0, n_first, second_t0, n_second);
-  const int nsv = (n_first + n_second + a.chunk - 1) / a.chunk;
+  const int n_list = n_first + n_second;
+  const int chunk = a.n_kv_dev ? max(1, (n_list + a.n_splits - 1) / a.n_splits) : a.chunk;
+  const int nsv = (n_list + chunk - 1) / chunk;
 
   const size_t esz = sizeof(T);
   const int P = a.lanes;
@@ -1043,7 +1053,8 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
                        void* o, const int64_t o_str[3],
                        int epi, int n_anchor, void* delta, const int64_t d_str[3],
                        int window, int sink, float sm_scale, void* workspace,
-                       size_t workspace_bytes, int dtype, void* stream) {
+                       size_t workspace_bytes, int dtype, void* stream,
+                       const int* n_kv_dev = nullptr) {
   if (p.n_items <= 0) return DA_ERR_INVALID_ARG;
   if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
@@ -1059,7 +1070,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   a.n_items = p.n_items;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.q_rows = q_rows; a.row_last = row_last; a.rl_b = rl_bstride;
-  a.chunk = p.chunk; a.n_splits = p.n_splits;
+  a.chunk = p.chunk; a.n_splits = p.n_splits; a.n_kv_dev = n_kv_dev;
   a.window = window; a.sink = sink;
   a.part_o = (float*)workspace;
   a.part_ml = (float*)workspace + (size_t)p.n_items * BM * D;
@@ -1067,7 +1078,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   MergeArgs m = {};
   m.q_rows = q_rows; m.row_last = row_last; m.rl_b = rl_bstride;
   m.n_rows = n; m.n_q = Sq; m.G = a.G; m.Hkv = Hkv; m.n_kv = Skv; m.n_mtiles = p.n_mtiles;
-  m.n_splits = p.n_splits; m.chunk = p.chunk;
+  m.n_splits = p.n_splits; m.chunk = p.chunk; m.n_kv_dev = n_kv_dev;
   m.window = window; m.sink = sink;
   // P threads per (row, column chunk) task: about 4 splits each, up to 16;
   // workgroups per row tile cover its valid rows only
@@ -1168,4 +1179,33 @@ extern "C" int da_decode_attn_fwd(const void* q, const void* k, const void* v, v
   return run_qsparse(p, q, k, v, nullptr, nullptr, 0, 1, B, Hq, Hkv, 1, n_keys, D,
                      q_str, k_str, v_str, out, o_str, DA_EPI_OUTPUT, 0, nullptr, nullptr,
                      window, sink, sm_scale, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" int da_decode_attn_fwd_dev(const void* q, const void* k, const void* v, void* out,
+                                      int B, int Hq, int Hkv, const int32_t* n_keys_dev,
+                                      int max_keys, int D,
+                                      const int64_t q_str[3], const int64_t k_str[3],
+                                      const int64_t v_str[3], const int64_t o_str[3],
+                                      int window, int sink, float sm_scale,
+                                      void* workspace, size_t workspace_bytes, int dtype,
+                                      void* stream) {
+  int rc;
+  if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
+  if (max_keys < 1 || window < 0 || sink < 0) return DA_ERR_INVALID_ARG;
+  if (!q_str || !k_str || !v_str || !o_str) return DA_ERR_INVALID_ARG;
+  if (!q || !k || !v || !out || !n_keys_dev) return DA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
+      ((uintptr_t)n_keys_dev & 3) != 0 ||
+      !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
+    return DA_ERR_ALIGNMENT;
+  if (!kv_rows_ok(k_str, v_str)) return DA_ERR_INVALID_ARG;
+  // launch shape and workspace of the longest cache: the key count is read
+  // on the device when the kernels run
+  const QsparsePlan p = plan_decode(B, Hq, Hkv, max_keys, D, window, sink);
+  if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
+  return run_qsparse(p, q, k, v, nullptr, nullptr, 0, 1, B, Hq, Hkv, 1, max_keys, D,
+                     q_str, k_str, v_str, out, o_str, DA_EPI_OUTPUT, 0, nullptr, nullptr,
+                     window, sink, sm_scale, workspace, workspace_bytes, dtype, stream,
+                     n_keys_dev);
 }

@@ -37,6 +37,7 @@ EXPORTS = (
     "da_delta_add",
     "da_decode_workspace_bytes",
     "da_decode_attn_fwd",
+    "da_decode_attn_fwd_dev",
     "da_rope_qk",
     "da_add_rmsnorm",
     "da_swiglu",
@@ -103,6 +104,9 @@ def lib() -> ctypes.CDLL:
     L.da_decode_attn_fwd.restype = _i
     L.da_decode_attn_fwd.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                      _p3, _p3, _p3, _p3, _i, _i, _f, _vp, _sz, _i, _vp]
+    L.da_decode_attn_fwd_dev.restype = _i
+    L.da_decode_attn_fwd_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i,
+                                         _p3, _p3, _p3, _p3, _i, _i, _f, _vp, _sz, _i, _vp]
     L.da_delta_add.restype = _i
     L.da_delta_add.argtypes = [_vp, _p3, _vp, _p3, _vp, _p3, _vp, _p3, _vp,
                                _i, _i, _i, _i, _i, _i, _i, _vp]

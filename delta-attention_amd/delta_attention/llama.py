@@ -248,14 +248,17 @@ class LlamaAttention(nn.Module):
         0 .. n - s + i (llama.py:498-535) -> ([b, s, h, d], None). One-row
         steps with decode_mode "sparse" / "delta" go to delta_decode_forward."""
         b, h, s, d = query_states.size()
+        n_keys = kwargs.get("n_keys")
         if s == 1 and getattr(self.config, "decode_mode", "dense") != "dense":
             return self.delta_decode_forward(module, query_states, key_states, value_states,
-                                             scaling=scaling)
+                                             scaling=scaling, **kwargs)
         q, k, v = self._half(query_states, key_states, value_states)
         n = k.size(2)
         if s == 1:
-            out = ops.decode_attention(q, k, v, window=0, sink=0, sm_scale=float(scaling))
+            out = ops.decode_attention(q, k, v, window=0, sink=0, sm_scale=float(scaling),
+                                       n_keys=n_keys)
         else:
+            assert n_keys is None, "a device key count serves one-row decode steps"
             mask = torch.arange(n - s, n, device=q.device, dtype=torch.int64)[None]
             out = qsa_kernel(q, k, v, mask, float(scaling))
         return out.transpose(1, 2).contiguous().to(query_states.dtype), None
@@ -266,12 +269,35 @@ class LlamaAttention(nn.Module):
             return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
         return q, k, v
 
-    def _decode_sparse_row(self, q, k, v, scaling):
+    def _decode_sparse_row(self, q, k, v, scaling, n_keys=None):
         """One decode row over the sink tokens + the last sliding_window keys of
         the cache, softmax over exactly that set (llama.py:537-549; every key
         when the cache holds at most sink + window keys). GQA native."""
         return ops.decode_attention(q, k, v, window=int(self.config.sliding_window),
-                                    sink=self._sink(), sm_scale=float(scaling))
+                                    sink=self._sink(), sm_scale=float(scaling), n_keys=n_keys)
+
+    def _delta_decode_recorded(self, q, k, v, scaling, n_keys, anchor: bool, out_dtype):
+        """delta_decode_forward's fixed-policy step in the form a recorded
+        decode step needs: the key count is on the device, the anchor decision
+        comes from the caller (the same schedule: the first step, then every
+        min(gamma_dec, gamma_dec_max) steps), and the cached delta is one
+        persistent buffer per layer, written in place on anchor steps."""
+        sparse_out = self._decode_sparse_row(q, k, v, scaling, n_keys)
+        if self.config.decode_mode == "sparse":
+            out = sparse_out
+        elif anchor:
+            dense_out = ops.decode_attention(q, k, v, window=0, sink=0, sm_scale=float(scaling),
+                                             n_keys=n_keys)
+            st = getattr(self, "_dec_static", None)
+            if st is None:    # first anchor step (run eagerly before any recording)
+                st = self._dec_static = {"last_delta": torch.empty_like(dense_out)}
+            torch.sub(dense_out, sparse_out, out=st["last_delta"])
+            out = dense_out
+        else:
+            st = getattr(self, "_dec_static", None)
+            assert st is not None, "a delta decode step needs an anchor step first"
+            out = sparse_out + st["last_delta"]
+        return out.transpose(1, 2).contiguous().to(out_dtype), None
 
     def delta_decode_forward(self, module, query_states, key_states, value_states,
                              scaling: float = 1.0, **kwargs):
@@ -288,6 +314,9 @@ class LlamaAttention(nn.Module):
         mode = self.config.decode_mode
         assert mode in ("sparse", "delta"), mode
         q, k, v = self._half(query_states, key_states, value_states)
+        if kwargs.get("n_keys") is not None:
+            return self._delta_decode_recorded(q, k, v, scaling, kwargs["n_keys"],
+                                               bool(kwargs.get("decode_anchor")), query_states.dtype)
         sparse_out = self._decode_sparse_row(q, k, v, scaling)
         if mode == "sparse":
             return sparse_out.transpose(1, 2).contiguous().to(query_states.dtype), None
@@ -387,10 +416,15 @@ class LlamaAttention(nn.Module):
         timer = kwargs.get("timer")
         query_states, key_states, value_states = self._qkv_rope(hidden_states, hidden_shape, cos, sin,
                                                                 timer)
+        extra = {}
         if past_key_value is not None:
             key_states, value_states = past_key_value.update(
                 key_states, value_states, self.layer_idx,
                 {"sin": sin, "cos": cos, "cache_position": cache_position})
+            if getattr(past_key_value, "static", False):
+                # recorded decode step: full cache buffers, key count on the device
+                extra = {"n_keys": past_key_value.n_keys,
+                         "decode_anchor": bool(past_key_value.anchor)}
         impl = self.config._attn_implementation
         if impl == "window":
             interface = self.delta_forward
@@ -403,7 +437,8 @@ class LlamaAttention(nn.Module):
         with region(timer, "attention_kernels"):
             attn_output, attn_weights = interface(
                 self, query_states, key_states, value_states, attention_mask,
-                dropout=0.0 if not self.training else self.attention_dropout, scaling=self.scaling)
+                dropout=0.0 if not self.training else self.attention_dropout, scaling=self.scaling,
+                **extra)
         assert attn_output.shape[-2] == self.config.num_attention_heads, attn_output.shape
         b, s, _, _ = attn_output.size()
         attn_output = attn_output.reshape(b, s, -1)

@@ -72,9 +72,39 @@ class KVCache:
         self.v = [torch.empty(shape, device=device, dtype=dtype) for _ in range(n)]
         self.len = [0] * n
         self.max_len = max_len
+        # static mode (decode steps recorded in a HIP graph): the appended row
+        # and the key count live on the device and advance there
+        self.static = False
+        self.pos = None        # int64 [1]: row of the next append
+        self.n_keys = None     # int32 [1]: keys after that append
+        self.anchor = False    # delta decode: whether the recorded step is an anchor step
+
+    def start_static(self):
+        """Switch to device-side positions: one-token appends go to row
+        `pos` and the decode rows read `n_keys` keys of the full buffers."""
+        assert len(set(self.len)) == 1, self.len
+        dev = self.k[0].device
+        self.pos = torch.full((1,), self.len[0], dtype=torch.int64, device=dev)
+        self.n_keys = torch.full((1,), self.len[0] + 1, dtype=torch.int32, device=dev)
+        self.static = True
+
+    def advance_static(self):
+        """Device-side step to the next position (recorded with the step)."""
+        self.pos.add_(1)
+        self.n_keys.add_(1)
+
+    def stop_static(self, n_appended: int):
+        """Back to host-side lengths after n_appended one-token steps."""
+        self.len = [l + n_appended for l in self.len]
+        self.static, self.pos, self.n_keys, self.anchor = False, None, None, False
 
     def update(self, key_states, value_states, layer_idx: int, cache_kwargs=None):
         s = key_states.shape[2]
+        if self.static:
+            assert s == 1, "static mode appends one token per step"
+            self.k[layer_idx].index_copy_(1, self.pos, key_states.transpose(1, 2))
+            self.v[layer_idx].index_copy_(1, self.pos, value_states.transpose(1, 2))
+            return self.k[layer_idx].transpose(1, 2), self.v[layer_idx].transpose(1, 2)
         l0 = self.len[layer_idx]
         assert l0 + s <= self.max_len, (l0, s, self.max_len)
         self.k[layer_idx][:, l0:l0 + s] = key_states.transpose(1, 2)
@@ -167,8 +197,11 @@ class LlamaModel(nn.Module):
         with a cache, positions continue after the cached ones."""
         with _region(timer, "embed"):
             h = self.embed_tokens(input_ids)
-            start = cache.seq_len() if cache is not None else 0
-            pos = torch.arange(start, start + input_ids.shape[1], device=input_ids.device)[None]
+            if cache is not None and cache.static:
+                pos = cache.pos[None]              # device-side position of this token
+            else:
+                start = cache.seq_len() if cache is not None else 0
+                pos = torch.arange(start, start + input_ids.shape[1], device=input_ids.device)[None]
             cos, sin = self.rotary(pos, h.dtype)
         residual = None
         for layer in self.layers:
@@ -201,15 +234,87 @@ class LlamaForCausalLM(nn.Module):
             if isinstance(m, LlamaAttention):
                 m._dec_state = None
                 m._dec_drift_points = None
+                m._dec_static = None
+
+    def graph_decodable(self) -> bool:
+        """Whether decode steps can be recorded once and replayed: dense and
+        sparse decode always; delta decode with the fixed refresh policy and no
+        drift logging (the drift policies decide on host-read cosines)."""
+        cfg = self.config
+        mode = getattr(cfg, "decode_mode", "dense")
+        if mode in ("dense", "sparse"):
+            return True
+        return (mode == "delta" and getattr(cfg, "refresh_policy", "fixed") == "fixed"
+                and not bool(getattr(cfg, "log_drift", False)))
+
+    def _decode_graphed(self, cache: KVCache, tok: torch.Tensor, max_new_tokens: int,
+                        step_ms: Optional[list], logits_out: Optional[list],
+                        record: bool = True) -> torch.Tensor:
+        """Decode steps 1 .. max_new_tokens-1 as HIP graph replays. The cache
+        holds the token's row and key count on the device; each step kind
+        (delta decode: anchor steps every min(gamma_dec, gamma_dec_max) steps,
+        starting with the first; otherwise one kind) runs eagerly once, then is
+        recorded and replayed. Outside the graph per step: the greedy argmax
+        (into the next step's input) and the token copy. record=False runs
+        every step eagerly in the same static form (the replays' reference)."""
+        import time
+        cfg = self.config
+        mode = getattr(cfg, "decode_mode", "dense")
+        period = (min(int(cfg.gamma_dec), int(getattr(cfg, "gamma_dec_max", 128)))
+                  if mode == "delta" else 0)
+        toks = torch.empty((tok.shape[0], max_new_tokens), dtype=torch.int64, device=tok.device)
+        toks[:, 0] = tok
+        tok_buf = tok[:, None].clone()
+        cache.start_static()
+        graphs = {}
+
+        def run_step(anchor: bool) -> torch.Tensor:
+            cache.anchor = anchor
+            h = self.model(tok_buf, None, cache)
+            logits = self.lm_head(h[:, -1])
+            cache.advance_static()
+            return logits
+
+        n = max_new_tokens - 1
+        try:
+            for j in range(n):
+                t0 = time.perf_counter()
+                kind = period > 0 and j % period == 0
+                if kind in graphs:
+                    g, logits = graphs[kind]
+                    g.replay()
+                else:
+                    logits = run_step(kind)
+                    if record:
+                        g = torch.cuda.CUDAGraph()
+                        with torch.cuda.graph(g):
+                            glogits = run_step(kind)
+                        graphs[kind] = (g, glogits)
+                if logits_out is not None:
+                    logits_out.append(logits.float().clone())
+                torch.argmax(logits, dim=-1, keepdim=True, out=tok_buf)
+                toks[:, j + 1] = tok_buf[:, 0]
+                if step_ms is not None:
+                    torch.cuda.synchronize()
+                    step_ms.append((time.perf_counter() - t0) * 1e3)
+        finally:
+            cache.stop_static(n)
+        return toks
 
     @torch.inference_mode()
     def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
-                        timer: Optional[Timer] = None, step_ms: Optional[list] = None) -> torch.Tensor:
+                        timer: Optional[Timer] = None, step_ms: Optional[list] = None,
+                        graph: bool = False, logits_out: Optional[list] = None,
+                        record: bool = True) -> torch.Tensor:
         """Greedy generation as sample.py drives it: the prompt is prefilled
         with the configured attention ("window": delta attention), then each
         new token runs one decode step with `sdpa_rectangle` (dense, or the
         sparse / delta decode of config.decode_mode). -> [b, max_new_tokens].
-        step_ms: receives each decode step's wall time."""
+        step_ms: receives each decode step's wall time; logits_out: each
+        step's fp32 logits, the prefill's first. graph: record the decode step in
+        HIP graphs and replay it (when graph_decodable(); the decode rows then
+        read the key count on the device, so they agree with the eager steps
+        to rounding); record=False runs those static steps eagerly."""
         import time
         cfg = self.config
         b, s = input_ids.shape
@@ -219,13 +324,21 @@ class LlamaForCausalLM(nn.Module):
         out = []
         try:
             h = self.model(input_ids, timer, cache)
-            tok = self.lm_head(h[:, -1]).argmax(-1)
+            logits = self.lm_head(h[:, -1])
+            if logits_out is not None:
+                logits_out.append(logits.float().clone())
+            tok = logits.argmax(-1)
             out.append(tok)
             cfg._attn_implementation = "sdpa_rectangle"
+            if graph and self.graph_decodable() and max_new_tokens > 1:
+                return self._decode_graphed(cache, tok, max_new_tokens, step_ms, logits_out, record)
             for _ in range(max_new_tokens - 1):
                 t0 = time.perf_counter()
                 h = self.model(tok[:, None], timer, cache)
-                tok = self.lm_head(h[:, -1]).argmax(-1)
+                logits = self.lm_head(h[:, -1])
+                if logits_out is not None:
+                    logits_out.append(logits.float().clone())
+                tok = logits.argmax(-1)
                 out.append(tok)
                 if step_ms is not None:
                     torch.cuda.synchronize()

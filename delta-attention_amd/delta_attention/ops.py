@@ -290,10 +290,16 @@ def rope_qk(q: Optional[torch.Tensor], k: Optional[torch.Tensor], cos: torch.Ten
 # decode rows
 
 def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int, sink: int,
-                     sm_scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     sm_scale: float, out: Optional[torch.Tensor] = None,
+                     n_keys: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The query row at the end of the cache: q [B,H,1,D] against k/v
     [B,Hkv,n,D] (GQA native) over keys [0, sink) and the last `window` keys
-    (window 0: all keys; llama.py:537-549, 598-600) -> [B,H,1,D]."""
+    (window 0: all keys; llama.py:537-549, 598-600) -> [B,H,1,D].
+
+    n_keys: an int32 device tensor holding the key count (k/v then hold the
+    cache's capacity, n rows, of which the first *n_keys are valid). The call
+    reads it when the kernels run, so a recorded call (HIP graph) serves every
+    length of a growing cache."""
     assert q.dim() == 4 and q.shape[2] == 1, q.shape
     B, H, _, D = q.shape
     Hkv, n = k.shape[1], k.shape[2]
@@ -307,15 +313,21 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, windo
     w, sk = max(int(window), 0), max(int(sink), 0)
     nbytes = int(L.lib().da_decode_workspace_bytes(B, H, Hkv, n, D, w, sk))
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    strides = (L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+               L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+               L.strides3(v.stride(0), v.stride(1), v.stride(2)),
+               L.strides3(out.stride(0), out.stride(1), out.stride(2)))
     with torch.cuda.device(dev):
-        rc = L.lib().da_decode_attn_fwd(
-            _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, n, D,
-            L.strides3(q.stride(0), q.stride(1), q.stride(2)),
-            L.strides3(k.stride(0), k.stride(1), k.stride(2)),
-            L.strides3(v.stride(0), v.stride(1), v.stride(2)),
-            L.strides3(out.stride(0), out.stride(1), out.stride(2)),
-            w, sk, float(sm_scale), _ptr(ws), nbytes, _code(q), _stream(dev))
-    L.check(rc, "da_decode_attn_fwd")
+        if n_keys is None:
+            rc = L.lib().da_decode_attn_fwd(
+                _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, n, D, *strides,
+                w, sk, float(sm_scale), _ptr(ws), nbytes, _code(q), _stream(dev))
+        else:
+            assert n_keys.dtype == torch.int32 and n_keys.device == dev and n_keys.numel() == 1
+            rc = L.lib().da_decode_attn_fwd_dev(
+                _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, _ptr(n_keys), n, D, *strides,
+                w, sk, float(sm_scale), _ptr(ws), nbytes, _code(q), _stream(dev))
+    L.check(rc, "da_decode_attn_fwd" if n_keys is None else "da_decode_attn_fwd_dev")
     return out
 
 

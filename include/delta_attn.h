@@ -164,6 +164,24 @@ int da_decode_attn_fwd(const void* q, const void* k, const void* v, void* out,
                        void* workspace, size_t workspace_bytes, int dtype, void* stream);
 
 /*
+ * The same decode row with the key count in device memory: *n_keys_dev
+ * (int32, 4-byte aligned, clamped to [1, max_keys] when the kernels run) keys
+ * of k/v buffers that hold max_keys rows. The launch shape and the workspace
+ * (da_decode_workspace_bytes(..., max_keys, ...)) depend on max_keys only, so
+ * one recorded call serves every length of a growing cache: this is the form
+ * a decode step captured in a HIP graph uses (the key count advances on the
+ * device between replays). Same row semantics as da_decode_attn_fwd
+ * (delta_attention/llama.py:537-549, 598-600); the split-KV partition differs
+ * with max_keys, so the two agree to rounding, not bit for bit.
+ */
+int da_decode_attn_fwd_dev(const void* q, const void* k, const void* v, void* out,
+                           int B, int Hq, int Hkv, const int32_t* n_keys_dev, int max_keys, int D,
+                           const int64_t q_str[3], const int64_t k_str[3],
+                           const int64_t v_str[3], const int64_t o_str[3],
+                           int window, int sink, float sm_scale,
+                           void* workspace, size_t workspace_bytes, int dtype, void* stream);
+
+/*
  * Kernel (3): delta broadcast-add over rows 0 .. s_p-1.
  * Replaces the torch broadcast at delta_attention/llama.py:740-755 (uniform
  * stride) and delta_attention/stride.py:26-40 (`apply_delta_variable`).

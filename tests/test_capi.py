@@ -195,6 +195,28 @@ def test_decode_checks(lib):
     assert call(D=80) == L.DA_ERR_HEAD_DIM
 
 
+def test_decode_dev_checks(lib):
+    """The device-key-count decode entry: its plan and workspace follow
+    max_keys, and every refusal happens before a launch."""
+    P = ctypes.c_void_p
+    s3 = _s3(32 * 128, 128, 128)
+    k3 = _s3(8 * 8192 * 128, 8192 * 128, 128)
+    need = lib.da_decode_workspace_bytes(1, 32, 8, 8192, 128, 0, 0)
+
+    def call(nk=64, max_keys=8192, w=16, nbytes=None, D=128, window=0):
+        return lib.da_decode_attn_fwd_dev(P(16), P(16), P(16), P(16), 1, 32, 8,
+                                          P(nk) if nk else None, max_keys, D, s3, k3, k3, s3,
+                                          window, 0, 0.1, P(w), need if nbytes is None else nbytes,
+                                          L.DA_BF16, None)
+    assert call(nk=0) == L.DA_ERR_INVALID_ARG          # no key-count pointer
+    assert call(nk=66) == L.DA_ERR_ALIGNMENT           # int32 needs 4-byte alignment
+    assert call(max_keys=0) == L.DA_ERR_INVALID_ARG
+    assert call(nbytes=need - 1) == L.DA_ERR_WORKSPACE
+    assert call(w=0) == L.DA_ERR_WORKSPACE
+    assert call(window=-1) == L.DA_ERR_INVALID_ARG
+    assert call(D=80) == L.DA_ERR_HEAD_DIM
+
+
 def test_anchor_delta_cos_checks(lib):
     P = ctypes.c_void_p
     a3 = _s3(64 * 8 * 128, 8 * 128, 128)

@@ -46,6 +46,42 @@ def test_decode_row_parity(gpu, B, H, Hkv, n, D, window, sink):
     assert_close(np64(got), ref, what=f"decode n{n} w{window} s{sink} {H}/{Hkv} D{D}")
 
 
+@pytest.mark.parametrize("window,sink", [(0, 0), (512, 16)])
+def test_decode_row_device_key_count(gpu, window, sink):
+    """da_decode_attn_fwd_dev: k/v buffers of the cache's capacity, the key
+    count read on the device when the kernels run. Each count against the
+    oracle's row and the host-count call (to rounding: the split partition
+    follows the capacity); then one recorded call replayed while the count
+    changes gives the eager call's bits for every count."""
+    from delta_attention import ops
+    cap, D = 4096, 128
+    q, k, v = _rand(1, 16, 4, cap, D, seed=31 + window)
+    scale = D ** -0.5
+    nk = torch.zeros(1, dtype=torch.int32, device="cuda")
+    eager = {}
+    for n in (1, 700, 2500, cap):
+        nk.fill_(n)
+        got = ops.decode_attention(q, k, v, window=window, sink=sink, sm_scale=scale, n_keys=nk)
+        host = ops.decode_attention(q, k[:, :, :n], v[:, :, :n], window=window, sink=sink, sm_scale=scale)
+        torch.cuda.synchronize()
+        kn, vn = np64(k)[:, :, :n], np64(v)[:, :, :n]
+        assert_close(np64(got), O.decode_row(np64(q), kn, vn, window, sink, scale),
+                     what=f"device count n{n} w{window}")
+        assert (got.float() - host.float()).abs().max().item() <= 4e-3
+        eager[n] = got
+    out = torch.empty_like(q)
+    nk.fill_(1)
+    ops.decode_attention(q, k, v, window=window, sink=sink, sm_scale=scale, n_keys=nk, out=out)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.decode_attention(q, k, v, window=window, sink=sink, sm_scale=scale, n_keys=nk, out=out)
+    for n in (700, cap, 2500, 1, 700):
+        nk.fill_(n)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[n]), n
+
+
 def test_rectangle_rows(gpu):
     from delta_attention.llama import LlamaAttention
     m = LlamaAttention(_cfg(), 0).cuda().to(torch.bfloat16)
@@ -173,3 +209,39 @@ def test_t9_repeated_generate_is_identical(gpu):
     assert torch.equal(a, b) and a.shape == (1, 10)
     m.config.decode_mode = "sparse"
     assert m.generate_greedy(ids, 10).shape == (1, 10)
+
+
+@pytest.mark.parametrize("mode,gamma_dec", [("dense", 1), ("sparse", 1), ("delta", 3)])
+def test_graph_decode_replays(gpu, mode, gamma_dec):
+    """Greedy decode with each step recorded once per step kind and replayed
+    (delta: anchor steps every gamma_dec steps and plain steps; the token's
+    row and the key count advance on the device). Same logits, bit for bit,
+    as the same static steps run eagerly, over several replays of each kind;
+    and to rounding the logits of the host-length decode steps."""
+    m = _small_model(decode_mode=mode, gamma_dec=gamma_dec)
+    assert m.graph_decodable()
+    ids = torch.randint(0, 512, (1, 700), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(11))
+    lg_graph, lg_static, lg_eager = [], [], []
+    a = m.generate_greedy(ids, 10, graph=True, logits_out=lg_graph)
+    b = m.generate_greedy(ids, 10, graph=True, record=False, logits_out=lg_static)
+    c = m.generate_greedy(ids, 10, logits_out=lg_eager)
+    torch.cuda.synchronize()
+    assert a.shape == (1, 10) and torch.equal(a, b)
+    assert len(lg_graph) == len(lg_static) == 10
+    for x, y in zip(lg_graph, lg_static):
+        assert torch.equal(x, y)
+    # against the host-length steps while both decoded the same tokens
+    n_same = int((a == c).long().cumprod(1).sum())
+    assert n_same >= 2
+    for i in range(n_same):
+        d = (lg_graph[i] - lg_eager[i]).abs().max().item()
+        assert d <= 2e-2 * max(1.0, lg_eager[i].abs().max().item()), (i, d)
+
+
+def test_graph_decode_falls_back_for_drift_policies(gpu):
+    m = _small_model(decode_mode="delta", gamma_dec=4, refresh_policy="drift", drift_threshold=0.9)
+    assert not m.graph_decodable()
+    ids = torch.randint(0, 512, (1, 300), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(12))
+    assert torch.equal(m.generate_greedy(ids, 5, graph=True), m.generate_greedy(ids, 5))
