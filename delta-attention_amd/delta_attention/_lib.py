@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libdelta_attn.so")
@@ -60,6 +61,7 @@ class ExtensionMissing(RuntimeError):
 
 
 _lib = None
+_lib_lock = threading.Lock()
 
 I64x3 = ctypes.c_int64 * 3
 _vp = ctypes.c_void_p
@@ -71,10 +73,18 @@ _p3 = ctypes.POINTER(ctypes.c_int64)
 
 
 def lib() -> ctypes.CDLL:
-    """Load the library once; raise ExtensionMissing if it is not there."""
+    """Load the library once (thread-safe); raise ExtensionMissing if it is
+    not there or lacks an entry point of this binding (a stale build)."""
     global _lib
     if _lib is not None:
         return _lib
+    with _lib_lock:
+        if _lib is None:
+            _lib = _load()
+    return _lib
+
+
+def _load() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ExtensionMissing(
             f"{LIB_PATH} is not built: run `python delta-attention_amd/build_lib.py` "
@@ -83,6 +93,10 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(LIB_PATH)
     except OSError as e:  # pragma: no cover - depends on the machine
         raise ExtensionMissing(f"cannot load {LIB_PATH}: {e}") from e
+    missing = [name for name in EXPORTS if not hasattr(L, name)]
+    if missing:
+        raise ExtensionMissing(f"{LIB_PATH} lacks {', '.join(missing)}: rebuild it "
+                               "(`python delta-attention_amd/build_lib.py`)")
     L.da_sparse_attn_fwd.restype = _i
     L.da_sparse_attn_fwd.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                      _p3, _p3, _p3, _p3, _i, _i, _i, _f, _i, _vp]
@@ -123,7 +137,6 @@ def lib() -> ctypes.CDLL:
                                       _vp, _vp, _i, _f, _f, _i, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
-    _lib = L
     return L
 
 

@@ -111,3 +111,18 @@ def test_product_ops_refuse_cpu_tensors():
                   torch.arange(8)[None], 0.1)
     with pytest.raises(AssertionError):           # mask must be 2-D
         attention(q, q, q, torch.arange(64), 0.1)
+
+
+def test_stale_library_is_extension_missing(tmp_path, monkeypatch):
+    """A library without this binding's entry points (an old build) is refused
+    with ExtensionMissing at load, not with an AttributeError mid-call."""
+    import subprocess
+    from delta_attention import _lib as L
+    src = tmp_path / "old.c"
+    src.write_text("int da_sparse_attn_fwd(void) { return 0; }\n")
+    so = tmp_path / "libold.so"
+    subprocess.run(["gcc", "-shared", "-fPIC", str(src), "-o", str(so)], check=True)
+    monkeypatch.setattr(L, "LIB_PATH", str(so))
+    monkeypatch.setattr(L, "_lib", None)
+    with pytest.raises(L.ExtensionMissing, match="lacks da_sparse_attn_delta_fwd"):
+        L.lib()
