@@ -896,10 +896,12 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
 }
 
 // Causal selected rows: ~8192 items (about half of them past the end of a
-// causal row tile's list), but at least 40 key tiles each: short items pay
-// their prologue and partials (measured at 32K and 128K keys).
+// causal row tile's list), but at least 56 key tiles each: short items pay
+// their prologue and partials, and at 32K keys (638 rows x 32 heads) 56 packs
+// the ~1K useful items into two rounds of resident workgroups (0.258 ms vs
+// 0.269-0.272 at 40; neutral at 128K keys, where the 8K target binds).
 static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
-  return plan_qsparse(B, Hq, Hkv, n, (Skv + BN - 1) / BN, D, DA_ROWS_ITEMS, 40);
+  return plan_qsparse(B, Hq, Hkv, n, (Skv + BN - 1) / BN, D, DA_ROWS_ITEMS, 56);
 }
 
 // One decode row per batch at the end of the cache: its list is the sink
