@@ -22,7 +22,7 @@ import torch
 from torch import nn
 
 from . import ops
-from .llama import LlamaAttention, LlamaRMSNorm, rope_cos_sin
+from .llama import LlamaAttention, LlamaRMSNorm, fuse_linears, fused_params, rope_cos_sin
 from .timing import Timer, region as _region
 
 
@@ -126,11 +126,24 @@ class LlamaMLP(nn.Module):
         self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=bias)
         self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=bias)
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=bias)
+        self._gate_up_fused = None
+
+    def fuse_projections(self):
+        """gate_proj and up_proj as one product (views of one weight buffer;
+        names and values unchanged; see LlamaAttention.fuse_projections)."""
+        self._gate_up_fused = fuse_linears(self.gate_proj, self.up_proj)
 
     def forward(self, x: torch.Tensor, timer: Optional[Timer] = None) -> torch.Tensor:
         with _region(timer, "mlp_gemm"):
-            g = self.gate_proj(x)
-            u = self.up_proj(x)
+            w, b = fused_params(self._gate_up_fused, (self.gate_proj, self.up_proj),
+                                x.numel() // x.shape[-1])
+            if w is None:
+                g = self.gate_proj(x)
+                u = self.up_proj(x)
+            else:
+                gu = nn.functional.linear(x, w, b)
+                n = self.gate_proj.out_features
+                g, u = gu[..., :n], gu[..., n:]
         with _region(timer, "swiglu"):
             if g.dtype in (torch.bfloat16, torch.float16):
                 a = ops.swiglu(g, u, out=g)     # in place over the gate
@@ -370,4 +383,8 @@ def random_llama(config: LlamaConfig, device="cuda", dtype=torch.bfloat16, seed:
     with torch.device("meta"):
         model = LlamaForCausalLM(config)
     model = model.to_empty(device=device).to(dtype)
-    return init_weights_(model, config.initializer_range, seed).eval().requires_grad_(False)
+    model = init_weights_(model, config.initializer_range, seed).eval().requires_grad_(False)
+    for m in model.modules():
+        if isinstance(m, (LlamaAttention, LlamaMLP)):
+            m.fuse_projections()
+    return model

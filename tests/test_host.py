@@ -126,3 +126,30 @@ def test_stale_library_is_extension_missing(tmp_path, monkeypatch):
     monkeypatch.setattr(L, "_lib", None)
     with pytest.raises(L.ExtensionMissing, match="lacks da_sparse_attn_delta_fwd"):
         L.lib()
+
+
+def test_fused_projections_are_views():
+    """fuse_projections keeps names, values and state-dict keys; the fused
+    product equals the separate ones; a replaced parameter (or a long input)
+    falls back to separate products."""
+    from delta_attention.llama import FUSED_MAX_ROWS, LlamaAttention
+    from delta_attention.model import LlamaConfig, LlamaMLP
+    cfg = LlamaConfig(vocab_size=64, hidden_size=256, intermediate_size=512, num_hidden_layers=1,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=64)
+    torch.manual_seed(0)
+    at, mlp = LlamaAttention(cfg, 0), LlamaMLP(cfg)
+    x = torch.randn(3, 256)
+    ref = torch.cat([at.q_proj(x), at.k_proj(x), at.v_proj(x)], -1)
+    keys, vals = list(at.state_dict()), {k: v.clone() for k, v in at.state_dict().items()}
+    at.fuse_projections()
+    mlp.fuse_projections()
+    assert list(at.state_dict()) == keys
+    assert all(torch.equal(at.state_dict()[k], vals[k]) for k in keys)
+    torch.testing.assert_close(at._qkv_product(x), ref)
+    assert at._qkv_product(torch.randn(FUSED_MAX_ROWS + 1, 256)) is None
+    with torch.no_grad():
+        g = mlp.forward(x)
+        mlp._gate_up_fused = None
+        torch.testing.assert_close(g, mlp.forward(x))
+    at.k_proj.weight = torch.nn.Parameter(at.k_proj.weight.detach().clone())
+    assert at._qkv_product(x) is None
