@@ -243,7 +243,7 @@ def prologue(a, dev):
     nbytes = 2 * B * S * (H + Hkv) * D * 2 + 2 * S * D * 2 + (4 * D if a.qk_norm else 0)
     gbs = nbytes / (ms * 1e-3) / 1e9
     print(json.dumps({
-        "metric": "fused RoPE prologue (da_rope_qk, 2 launches: q then k)", "value": round(gbs, 1),
+        "metric": "fused RoPE prologue (da_rope_qk, one launch over the q and k rows)", "value": round(gbs, 1),
         "unit": "GB/s", "ms_per_call": round(ms, 4), "steps": a.steps, "warmup": a.warmup,
         "qk_norm": bool(a.qk_norm), "bytes_per_call": nbytes,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,

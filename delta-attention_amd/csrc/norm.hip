@@ -8,13 +8,27 @@
 //   SwiGLU (delta_attention/llama.py:212-213):
 //       y = rnd(rnd(silu(g)) * u),  silu(g) = g / (1 + exp(-g))          (fp32 inside)
 // Both are HBM-bound: each element is read once and written once with 16-byte
-// non-temporal accesses (4-5 % faster than ordinary ones at the 8B model's
-// shapes); the norm weight is read with ordinary loads (every row reuses it). One wave owns one row of the norm (the sum of squares is a wave
-// reduction, no LDS).
+// accesses, non-temporal for large inputs (4-5 % faster than ordinary ones at
+// the 8B model's prefill shapes) and ordinary below NT_MIN_BYTES (a decode
+// step's single row is read by the next kernel from L2; streamed, it took 9.6
+// us per norm instead of ~4). The norm weight is read with ordinary loads
+// (every row reuses it). One wave owns one row of the norm (the sum of squares
+// is a wave reduction, no LDS).
 #include "device_common.h"
 #include "capi_common.h"
 
 namespace da {
+
+// Inputs of at least this many bytes stream through non-temporal accesses.
+constexpr int64_t NT_MIN_BYTES = 4 << 20;
+
+template <bool NT>
+__device__ __forceinline__ u32x4 ld4(const void* p) { return NT ? ld_nt4(p) : *(const u32x4*)p; }
+template <bool NT>
+__device__ __forceinline__ void st4(void* p, u32x4 v) {
+  if constexpr (NT) st_nt4(p, v);
+  else *(u32x4*)p = v;
+}
 
 struct NormArgs {
   const void* x;      // [rows, n] (row stride xs)
@@ -29,7 +43,7 @@ struct NormArgs {
 };
 
 // CH = 16-byte chunks per lane (n = 64 * 8 * CH elements)
-template <typename T, int CH>
+template <typename T, int CH, bool NT>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormArgs a) {
   using E = Elt<T>;
   const int lane = threadIdx.x & 63;
@@ -39,17 +53,17 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormArgs a) {
   const char* xp = (const char*)a.x + row * a.xs * esz;
   u32x4 v[CH];
 #pragma unroll
-  for (int c = 0; c < CH; ++c) v[c] = ld_nt4(xp + (c * 64 + lane) * 16);
+  for (int c = 0; c < CH; ++c) v[c] = ld4<NT>(xp + (c * 64 + lane) * 16);
   if (a.r) {
     const char* rp = (const char*)a.r + row * a.rs * esz;
     char* hp = (char*)a.h + row * a.hs * esz;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const u32x4 rv = ld_nt4(rp + (c * 64 + lane) * 16);
+      const u32x4 rv = ld4<NT>(rp + (c * 64 + lane) * 16);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         v[c][e] = E::pack2(E::lo(v[c][e]) + E::lo(rv[e]), E::hi(v[c][e]) + E::hi(rv[e]));
-      st_nt4(hp + (c * 64 + lane) * 16, v[c]);
+      st4<NT>(hp + (c * 64 + lane) * 16, v[c]);
     }
   }
   float ss = 0.f;
@@ -74,7 +88,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormArgs a) {
       const uint32_t t = E::pack2(E::lo(v[c][e]) * rinv, E::hi(v[c][e]) * rinv);
       o[e] = E::pack2(E::lo(wv[e]) * E::lo(t), E::hi(wv[e]) * E::hi(t));
     }
-    st_nt4(yp + (c * 64 + lane) * 16, o);
+    st4<NT>(yp + (c * 64 + lane) * 16, o);
   }
 }
 
@@ -87,7 +101,7 @@ struct SwiGluArgs {
   int n;                // row length, multiple of 8
 };
 
-template <typename T>
+template <typename T, bool NT>
 __global__ __launch_bounds__(256) void swiglu_kernel(SwiGluArgs a) {
   using E = Elt<T>;
   const int cpr = a.n / 8;   // 16-byte chunks per row
@@ -97,8 +111,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwiGluArgs a) {
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = i / cpr;
     const int c = (int)(i % cpr);
-    const u32x4 gv = ld_nt4((const char*)a.g + (row * a.gs + 8 * c) * esz);
-    const u32x4 uv = ld_nt4((const char*)a.u + (row * a.us + 8 * c) * esz);
+    const u32x4 gv = ld4<NT>((const char*)a.g + (row * a.gs + 8 * c) * esz);
+    const u32x4 uv = ld4<NT>((const char*)a.u + (row * a.us + 8 * c) * esz);
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -106,20 +120,26 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwiGluArgs a) {
       const uint32_t s = E::pack2(gl / (1.f + __expf(-gl)), gh / (1.f + __expf(-gh)));
       o[e] = E::pack2(E::lo(s) * E::lo(uv[e]), E::hi(s) * E::hi(uv[e]));
     }
-    st_nt4((char*)a.y + (row * a.ys + 8 * c) * esz, o);
+    st4<NT>((char*)a.y + (row * a.ys + 8 * c) * esz, o);
+  }
+}
+
+template <typename T, bool NT>
+static void launch_norm_nt(const NormArgs& a, hipStream_t s) {
+  const int grid = (int)((a.rows + 3) / 4);
+  switch (a.n / 512) {
+    case 4: hipLaunchKernelGGL((add_rmsnorm_kernel<T, 4, NT>), dim3(grid), dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((add_rmsnorm_kernel<T, 8, NT>), dim3(grid), dim3(256), 0, s, a); break;
+    case 10: hipLaunchKernelGGL((add_rmsnorm_kernel<T, 10, NT>), dim3(grid), dim3(256), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((add_rmsnorm_kernel<T, 16, NT>), dim3(grid), dim3(256), 0, s, a); break;
+    default: break;
   }
 }
 
 template <typename T>
 static void launch_norm(const NormArgs& a, hipStream_t s) {
-  const int grid = (int)((a.rows + 3) / 4);
-  switch (a.n / 512) {
-    case 4: hipLaunchKernelGGL((add_rmsnorm_kernel<T, 4>), dim3(grid), dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((add_rmsnorm_kernel<T, 8>), dim3(grid), dim3(256), 0, s, a); break;
-    case 10: hipLaunchKernelGGL((add_rmsnorm_kernel<T, 10>), dim3(grid), dim3(256), 0, s, a); break;
-    case 16: hipLaunchKernelGGL((add_rmsnorm_kernel<T, 16>), dim3(grid), dim3(256), 0, s, a); break;
-    default: break;
-  }
+  if (a.rows * a.n * (int64_t)sizeof(T) >= NT_MIN_BYTES) launch_norm_nt<T, true>(a, s);
+  else launch_norm_nt<T, false>(a, s);
 }
 
 }  // namespace da
@@ -168,7 +188,13 @@ extern "C" int da_swiglu(const void* gate, int64_t g_stride, const void* up, int
   const int grid = (int)(want < 65536 ? want : 65536);
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
-  if (dtype == DA_BF16) hipLaunchKernelGGL((swiglu_kernel<__bf16>), dim3(grid), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((swiglu_kernel<_Float16>), dim3(grid), dim3(256), 0, s, a);
+  const bool nt = rows * n * 2 >= NT_MIN_BYTES;   // both element types are 2 bytes
+  if (dtype == DA_BF16) {
+    if (nt) hipLaunchKernelGGL((swiglu_kernel<__bf16, true>), dim3(grid), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((swiglu_kernel<__bf16, false>), dim3(grid), dim3(256), 0, s, a);
+  } else {
+    if (nt) hipLaunchKernelGGL((swiglu_kernel<_Float16, true>), dim3(grid), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((swiglu_kernel<_Float16, false>), dim3(grid), dim3(256), 0, s, a);
+  }
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }

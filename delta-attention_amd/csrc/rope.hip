@@ -8,29 +8,39 @@
 //   norm:  y = rnd(w * rnd(x * rsqrt(mean(x^2) + eps)))          (fp32 inside)
 //   rope:  out[i]       = rnd(rnd(y[i] * cos[i])       - rnd(y[i+D/2] * sin[i]))
 //          out[i + D/2] = rnd(rnd(y[i+D/2] * cos[i+D/2]) + rnd(y[i] * sin[i+D/2]))
-// HBM-bound: each row is read once and written once with 16-byte
-// non-temporal accesses (the cos/sin rows and the norm weight, shared by every
-// head, with ordinary loads);
-// 8 consecutive threads own one (token, head) row (8 + 8 elements each for D=128).
+// HBM-bound: each row is read once and written once with 16-byte accesses,
+// non-temporal for large inputs and ordinary below NT_MIN_BYTES (a decode
+// step's rows are read next from L2); the cos/sin rows and the norm weight,
+// shared by every head, with ordinary loads. One launch covers the q rows then
+// the k rows; 8 consecutive threads own one (token, head) row (8 + 8 elements
+// each for D=128).
 #include "device_common.h"
 #include "capi_common.h"
 
 namespace da {
 
-struct RopeArgs {
-  void* x;                 // [B, S, H, D] (strides b, s, h in elements)
+// Inputs of at least this many bytes stream through non-temporal accesses.
+constexpr int64_t NT_MIN_BYTES = 4 << 20;
+
+struct RopePart {
+  void* x;                 // [B, S, H, D] (strides b, s, h in elements) or nullptr
   int64_t xs_b, xs_s, xs_h;
   int H;
+  const void* w;           // [D] norm weight or nullptr
+  int64_t rows;            // B * S * H (0 without this part)
+};
+
+struct RopeArgs {
+  RopePart q, k;           // rows [0, q.rows) are q's, the next k.rows are k's
   const void* cos;         // [Bc, S, D], Bc in {1, B}
   const void* sin;
   int64_t cs_b, cs_s;
-  const void* w;           // [D] norm weight or nullptr
   float eps;
   int B, S, D;
-  int64_t rows;            // B * S * H
+  int64_t rows;            // q.rows + k.rows
 };
 
-template <typename T, int D>
+template <typename T, int D, bool NT>
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   using E = Elt<T>;
   constexpr int TPR = 8;              // threads per row
@@ -41,13 +51,22 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int64_t row = gtid / TPR;
   const int part = (int)(gtid % TPR);
   const bool live = row < a.rows;
-  const int64_t rr = live ? row : 0;
-  const int h = (int)(rr % a.H);
-  const int64_t bs = rr / a.H;
+  const bool kpart = live && row >= a.q.rows;
+  const int64_t rr = live ? (kpart ? row - a.q.rows : row) : 0;
+  // the part's fields by selects (dynamic indexing of kernel arguments would
+  // copy them to scratch)
+  const int H = kpart ? a.k.H : a.q.H;
+  const int64_t xs_b = kpart ? a.k.xs_b : a.q.xs_b;
+  const int64_t xs_s = kpart ? a.k.xs_s : a.q.xs_s;
+  const int64_t xs_h = kpart ? a.k.xs_h : a.q.xs_h;
+  const void* w = kpart ? a.k.w : a.q.w;
+  char* const xbase = (char*)(kpart ? a.k.x : a.q.x);
+  const int h = (int)(rr % H);
+  const int64_t bs = rr / H;
   const int s = (int)(bs % a.S);
   const int b = (int)(bs / a.S);
   constexpr size_t esz = sizeof(T);
-  char* xp = (char*)a.x + ((int64_t)b * a.xs_b + (int64_t)s * a.xs_s + (int64_t)h * a.xs_h) * esz;
+  char* xp = xbase + ((int64_t)b * xs_b + (int64_t)s * xs_s + (int64_t)h * xs_h) * esz;
   const int i0 = part * EPT;          // first element of this thread in the low half
 
   float lo[EPT], hi[EPT];
@@ -63,14 +82,14 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     }
   };
   if (live) {
-    load8(xp + i0 * esz, lo, true);
-    load8(xp + (HALF + i0) * esz, hi, true);
+    load8(xp + i0 * esz, lo, NT);
+    load8(xp + (HALF + i0) * esz, hi, NT);
   } else {
 #pragma unroll
     for (int e = 0; e < EPT; ++e) { lo[e] = 0.f; hi[e] = 0.f; }
   }
 
-  if (a.w) {
+  if (w) {
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
@@ -78,8 +97,8 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     for (int off = 1; off < TPR; off <<= 1) ss += __shfl_xor(ss, off);
     const float r = rsqrtf(ss / (float)D + a.eps);
     float wl[EPT], wh[EPT];
-    load8((const char*)a.w + i0 * esz, wl);
-    load8((const char*)a.w + (HALF + i0) * esz, wh);
+    load8((const char*)w + i0 * esz, wl);
+    load8((const char*)w + (HALF + i0) * esz, wh);
 #pragma unroll
     for (int e = 0; e < EPT; e += 2) {
       uint32_t p = E::pack2(lo[e] * r, lo[e + 1] * r);            // x * rsqrt(...) -> dtype
@@ -112,40 +131,54 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   }
   if (!live) return;
   if constexpr (EPT == 8) {
-    st_nt4(xp + i0 * esz, (u32x4){olo[0], olo[1], olo[2], olo[3]});
-    st_nt4(xp + (HALF + i0) * esz, (u32x4){ohi[0], ohi[1], ohi[2], ohi[3]});
+    const u32x4 vl = {olo[0], olo[1], olo[2], olo[3]}, vh = {ohi[0], ohi[1], ohi[2], ohi[3]};
+    if constexpr (NT) {
+      st_nt4(xp + i0 * esz, vl);
+      st_nt4(xp + (HALF + i0) * esz, vh);
+    } else {
+      *(u32x4*)(xp + i0 * esz) = vl;
+      *(u32x4*)(xp + (HALF + i0) * esz) = vh;
+    }
   } else {
-    st_nt2(xp + i0 * esz, (u32x2){olo[0], olo[1]});
-    st_nt2(xp + (HALF + i0) * esz, (u32x2){ohi[0], ohi[1]});
+    const u32x2 vl = {olo[0], olo[1]}, vh = {ohi[0], ohi[1]};
+    if constexpr (NT) {
+      st_nt2(xp + i0 * esz, vl);
+      st_nt2(xp + (HALF + i0) * esz, vh);
+    } else {
+      *(u32x2*)(xp + i0 * esz) = vl;
+      *(u32x2*)(xp + (HALF + i0) * esz) = vh;
+    }
   }
+}
+
+template <typename T, bool NT>
+static void launch_rope_nt(const RopeArgs& a, hipStream_t s) {
+  const int64_t threads = a.rows * 8;
+  const int grid = (int)((threads + 255) / 256);
+  if (a.D == 128) hipLaunchKernelGGL((rope_kernel<T, 128, NT>), dim3(grid), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((rope_kernel<T, 64, NT>), dim3(grid), dim3(256), 0, s, a);
 }
 
 template <typename T>
 static void launch_rope(const RopeArgs& a, hipStream_t s) {
-  const int64_t threads = a.rows * 8;
-  const int grid = (int)((threads + 255) / 256);
-  if (a.D == 128) hipLaunchKernelGGL((rope_kernel<T, 128>), dim3(grid), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((rope_kernel<T, 64>), dim3(grid), dim3(256), 0, s, a);
+  if (a.rows * a.D * (int64_t)sizeof(T) >= NT_MIN_BYTES) launch_rope_nt<T, true>(a, s);
+  else launch_rope_nt<T, false>(a, s);
 }
 
 }  // namespace da
 
 using namespace da;
 
-static int rope_one(void* x, const int64_t x_str[3], int H, int B, int S, int D,
-                    const void* cos, const void* sin, const int64_t cs_str[2], const void* w,
-                    float eps, int dtype, hipStream_t s) {
-  if (!x || !x_str || H < 1) return DA_ERR_INVALID_ARG;
+// One part (q or k) of the launch, checked.
+static int rope_part(RopePart& p, void* x, const int64_t x_str[3], int H, int B, int S,
+                     const void* w) {
+  p = RopePart{};
+  if (!x) return DA_OK;
+  if (!x_str || H < 1) return DA_ERR_INVALID_ARG;
   if (!aligned16(x) || !strides8(x_str)) return DA_ERR_ALIGNMENT;
   if (w && !aligned16(w)) return DA_ERR_ALIGNMENT;
-  RopeArgs a = {};
-  a.x = x; a.xs_b = x_str[0]; a.xs_s = x_str[1]; a.xs_h = x_str[2];
-  a.H = H; a.cos = cos; a.sin = sin; a.cs_b = cs_str[0]; a.cs_s = cs_str[1];
-  a.w = w; a.eps = eps; a.B = B; a.S = S; a.D = D;
-  a.rows = (int64_t)B * S * H;
-  if (a.rows * 8 / 256 > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
-  if (dtype == DA_BF16) launch_rope<__bf16>(a, s);
-  else launch_rope<_Float16>(a, s);
+  p.x = x; p.xs_b = x_str[0]; p.xs_s = x_str[1]; p.xs_h = x_str[2];
+  p.H = H; p.w = w; p.rows = (int64_t)B * S * H;
   return DA_OK;
 }
 
@@ -161,12 +194,18 @@ extern "C" int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
   if (S == 0) return DA_OK;
   if (!cos || !sin || !cs_str || cs_str[0] < 0 || cs_str[1] < D) return DA_ERR_INVALID_ARG;
   if (!aligned16(cos) || !aligned16(sin) || cs_str[0] % 8 || cs_str[1] % 8) return DA_ERR_ALIGNMENT;
+  RopeArgs a = {};
+  int rc;
+  if ((rc = rope_part(a.q, q, q_str, Hq, B, S, q_norm_w)) != DA_OK) return rc;
+  if ((rc = rope_part(a.k, k, k_str, Hkv, B, S, k_norm_w)) != DA_OK) return rc;
+  a.cos = cos; a.sin = sin; a.cs_b = cs_str[0]; a.cs_s = cs_str[1];
+  a.eps = eps; a.B = B; a.S = S; a.D = D;
+  a.rows = a.q.rows + a.k.rows;
+  if (a.rows == 0) return DA_OK;
+  if (a.rows * 8 / 256 > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
-  int rc;
-  if (q && (rc = rope_one(q, q_str, Hq, B, S, D, cos, sin, cs_str, q_norm_w, eps, dtype, s)) != DA_OK)
-    return rc;
-  if (k && (rc = rope_one(k, k_str, Hkv, B, S, D, cos, sin, cs_str, k_norm_w, eps, dtype, s)) != DA_OK)
-    return rc;
+  if (dtype == DA_BF16) launch_rope<__bf16>(a, s);
+  else launch_rope<_Float16>(a, s);
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }
