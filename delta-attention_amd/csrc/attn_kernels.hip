@@ -740,6 +740,10 @@ struct MergeArgs {
   int64_t os_b, os_h, os_s;
   void* delta;
   int64_t ds_b, ds_h, ds_a;
+  // DA_EPI_OUTPUT: optional addend [B, Hq, n, D] (strides batch, head, row):
+  // out = rnd(rnd(merged) + addend), the bf16 add of a cached decode delta
+  const void* add;
+  int64_t as_b, as_h, as_s;
 };
 
 template <typename T, int D>
@@ -836,6 +840,13 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
       char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)h * a.os_h + (int64_t)i * a.os_s + 8 * c) * esz;
       u32x4 pk = {E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3]),
                   E::pack2(acc[4], acc[5]), E::pack2(acc[6], acc[7])};
+      if (a.add) {
+        const u32x4 av = *(const u32x4*)((const char*)a.add +
+            ((int64_t)b * a.as_b + (int64_t)h * a.as_h + (int64_t)i * a.as_s + 8 * c) * esz);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pk[e] = E::pack2(E::lo(pk[e]) + E::lo(av[e]), E::hi(pk[e]) + E::hi(av[e]));
+      }
       *(u32x4*)op = pk;
     } else {
       char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)h * a.os_h + (int64_t)qrow * a.os_s + 8 * c) * esz;
@@ -1056,7 +1067,8 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
                        int epi, int n_anchor, void* delta, const int64_t d_str[3],
                        int window, int sink, float sm_scale, void* workspace,
                        size_t workspace_bytes, int dtype, void* stream,
-                       const int* n_kv_dev = nullptr) {
+                       const int* n_kv_dev = nullptr, const void* add = nullptr,
+                       const int64_t* add_str = nullptr) {
   if (p.n_items <= 0) return DA_ERR_INVALID_ARG;
   if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
@@ -1095,6 +1107,8 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   m.o = o; m.os_b = o_str[0]; m.os_h = o_str[1]; m.os_s = o_str[2];
   m.delta = delta;
   if (d_str) { m.ds_b = d_str[0]; m.ds_h = d_str[1]; m.ds_a = d_str[2]; }
+  m.add = add;
+  if (add) { m.as_b = add_str[0]; m.as_h = add_str[1]; m.as_s = add_str[2]; }
 
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
@@ -1189,11 +1203,13 @@ extern "C" int da_decode_attn_fwd_dev(const void* q, const void* k, const void* 
                                       const int64_t q_str[3], const int64_t k_str[3],
                                       const int64_t v_str[3], const int64_t o_str[3],
                                       int window, int sink, float sm_scale,
+                                      const void* addend, const int64_t add_str[3],
                                       void* workspace, size_t workspace_bytes, int dtype,
                                       void* stream) {
   int rc;
   if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
   if (max_keys < 1 || window < 0 || sink < 0) return DA_ERR_INVALID_ARG;
+  if (addend && (!add_str || !aligned16(addend) || !strides8(add_str))) return DA_ERR_ALIGNMENT;
   if (!q_str || !k_str || !v_str || !o_str) return DA_ERR_INVALID_ARG;
   if (!q || !k || !v || !out || !n_keys_dev) return DA_ERR_INVALID_ARG;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
@@ -1209,5 +1225,5 @@ extern "C" int da_decode_attn_fwd_dev(const void* q, const void* k, const void* 
   return run_qsparse(p, q, k, v, nullptr, nullptr, 0, 1, B, Hq, Hkv, 1, max_keys, D,
                      q_str, k_str, v_str, out, o_str, DA_EPI_OUTPUT, 0, nullptr, nullptr,
                      window, sink, sm_scale, workspace, workspace_bytes, dtype, stream,
-                     n_keys_dev);
+                     n_keys_dev, addend, add_str);
 }

@@ -120,7 +120,8 @@ def _load() -> ctypes.CDLL:
                                      _p3, _p3, _p3, _p3, _i, _i, _f, _vp, _sz, _i, _vp]
     L.da_decode_attn_fwd_dev.restype = _i
     L.da_decode_attn_fwd_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i,
-                                         _p3, _p3, _p3, _p3, _i, _i, _f, _vp, _sz, _i, _vp]
+                                         _p3, _p3, _p3, _p3, _i, _i, _f, _vp, _p3,
+                                         _vp, _sz, _i, _vp]
     L.da_delta_add.restype = _i
     L.da_delta_add.argtypes = [_vp, _p3, _vp, _p3, _vp, _p3, _vp, _p3, _vp,
                                _i, _i, _i, _i, _i, _i, _i, _vp]

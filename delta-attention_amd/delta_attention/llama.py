@@ -345,6 +345,14 @@ class LlamaAttention(nn.Module):
         comes from the caller (the same schedule: the first step, then every
         min(gamma_dec, gamma_dec_max) steps), and the cached delta is one
         persistent buffer per layer, written in place on anchor steps."""
+        if self.config.decode_mode == "delta" and not anchor:
+            st = getattr(self, "_dec_static", None)
+            assert st is not None, "a delta decode step needs an anchor step first"
+            # the sparse row and the cached delta's add in one launch
+            out = ops.decode_attention(q, k, v, window=int(self.config.sliding_window),
+                                       sink=self._sink(), sm_scale=float(scaling),
+                                       n_keys=n_keys, add=st["last_delta"])
+            return out.transpose(1, 2).contiguous().to(out_dtype), None
         sparse_out = self._decode_sparse_row(q, k, v, scaling, n_keys)
         if self.config.decode_mode == "sparse":
             out = sparse_out
@@ -356,10 +364,6 @@ class LlamaAttention(nn.Module):
                 st = self._dec_static = {"last_delta": torch.empty_like(dense_out)}
             torch.sub(dense_out, sparse_out, out=st["last_delta"])
             out = dense_out
-        else:
-            st = getattr(self, "_dec_static", None)
-            assert st is not None, "a delta decode step needs an anchor step first"
-            out = sparse_out + st["last_delta"]
         return out.transpose(1, 2).contiguous().to(out_dtype), None
 
     def delta_decode_forward(self, module, query_states, key_states, value_states,

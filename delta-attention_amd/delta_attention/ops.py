@@ -291,7 +291,8 @@ def rope_qk(q: Optional[torch.Tensor], k: Optional[torch.Tensor], cos: torch.Ten
 
 def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int, sink: int,
                      sm_scale: float, out: Optional[torch.Tensor] = None,
-                     n_keys: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     n_keys: Optional[torch.Tensor] = None,
+                     add: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The query row at the end of the cache: q [B,H,1,D] against k/v
     [B,Hkv,n,D] (GQA native) over keys [0, sink) and the last `window` keys
     (window 0: all keys; llama.py:537-549, 598-600) -> [B,H,1,D].
@@ -299,7 +300,8 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, windo
     n_keys: an int32 device tensor holding the key count (k/v then hold the
     cache's capacity, n rows, of which the first *n_keys are valid). The call
     reads it when the kernels run, so a recorded call (HIP graph) serves every
-    length of a growing cache."""
+    length of a growing cache. add (with n_keys): a [B,H,1,D] tensor added to
+    the row in the same launch, rnd(rnd(row) + add) as the bf16 tensor add."""
     assert q.dim() == 4 and q.shape[2] == 1, q.shape
     B, H, _, D = q.shape
     Hkv, n = k.shape[1], k.shape[2]
@@ -319,14 +321,20 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, windo
                L.strides3(out.stride(0), out.stride(1), out.stride(2)))
     with torch.cuda.device(dev):
         if n_keys is None:
+            assert add is None, "add= goes with a device key count"
             rc = L.lib().da_decode_attn_fwd(
                 _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, n, D, *strides,
                 w, sk, float(sm_scale), _ptr(ws), nbytes, _code(q), _stream(dev))
         else:
             assert n_keys.dtype == torch.int32 and n_keys.device == dev and n_keys.numel() == 1
+            if add is not None:
+                assert add.shape == (B, H, 1, D) and add.dtype == q.dtype and add.device == dev
+                add = _ready(add)
             rc = L.lib().da_decode_attn_fwd_dev(
                 _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, _ptr(n_keys), n, D, *strides,
-                w, sk, float(sm_scale), _ptr(ws), nbytes, _code(q), _stream(dev))
+                w, sk, float(sm_scale), _ptr(add),
+                None if add is None else L.strides3(add.stride(0), add.stride(1), add.stride(2)),
+                _ptr(ws), nbytes, _code(q), _stream(dev))
     L.check(rc, "da_decode_attn_fwd" if n_keys is None else "da_decode_attn_fwd_dev")
     return out
 

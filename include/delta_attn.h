@@ -173,12 +173,16 @@ int da_decode_attn_fwd(const void* q, const void* k, const void* v, void* out,
  * device between replays). Same row semantics as da_decode_attn_fwd
  * (delta_attention/llama.py:537-549, 598-600); the split-KV partition differs
  * with max_keys, so the two agree to rounding, not bit for bit.
+ * addend (NULL: none) [B, Hq, 1, D] with add_str {batch, head, row}: out =
+ * rnd(rnd(row) + addend), the cached-delta add of a delta decode step
+ * (llama.py:612-620 `sparse_out + last_delta`) in the same launch.
  */
 int da_decode_attn_fwd_dev(const void* q, const void* k, const void* v, void* out,
                            int B, int Hq, int Hkv, const int32_t* n_keys_dev, int max_keys, int D,
                            const int64_t q_str[3], const int64_t k_str[3],
                            const int64_t v_str[3], const int64_t o_str[3],
                            int window, int sink, float sm_scale,
+                           const void* addend, const int64_t add_str[3],
                            void* workspace, size_t workspace_bytes, int dtype, void* stream);
 
 /*

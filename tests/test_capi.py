@@ -203,10 +203,13 @@ def test_decode_dev_checks(lib):
     k3 = _s3(8 * 8192 * 128, 8192 * 128, 128)
     need = lib.da_decode_workspace_bytes(1, 32, 8, 8192, 128, 0, 0)
 
-    def call(nk=64, max_keys=8192, w=16, nbytes=None, D=128, window=0):
+    a3 = s3
+
+    def call(nk=64, max_keys=8192, w=16, nbytes=None, D=128, window=0, add=0):
         return lib.da_decode_attn_fwd_dev(P(16), P(16), P(16), P(16), 1, 32, 8,
                                           P(nk) if nk else None, max_keys, D, s3, k3, k3, s3,
-                                          window, 0, 0.1, P(w), need if nbytes is None else nbytes,
+                                          window, 0, 0.1, P(add) if add else None, a3,
+                                          P(w), need if nbytes is None else nbytes,
                                           L.DA_BF16, None)
     assert call(nk=0) == L.DA_ERR_INVALID_ARG          # no key-count pointer
     assert call(nk=66) == L.DA_ERR_ALIGNMENT           # int32 needs 4-byte alignment
@@ -215,6 +218,7 @@ def test_decode_dev_checks(lib):
     assert call(w=0) == L.DA_ERR_WORKSPACE
     assert call(window=-1) == L.DA_ERR_INVALID_ARG
     assert call(D=80) == L.DA_ERR_HEAD_DIM
+    assert call(add=8) == L.DA_ERR_ALIGNMENT            # addend rows 16-byte aligned
 
 
 def test_anchor_delta_cos_checks(lib):

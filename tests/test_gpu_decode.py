@@ -69,6 +69,12 @@ def test_decode_row_device_key_count(gpu, window, sink):
                      what=f"device count n{n} w{window}")
         assert (got.float() - host.float()).abs().max().item() <= 4e-3
         eager[n] = got
+        # the cached-delta add in the same launch: the bf16 tensor add's bits
+        d = torch.randn(q.shape, generator=torch.Generator().manual_seed(n)).to(q.dtype).cuda()
+        fused = ops.decode_attention(q, k, v, window=window, sink=sink, sm_scale=scale, n_keys=nk,
+                                     add=d)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, got + d)
     out = torch.empty_like(q)
     nk.fill_(1)
     ops.decode_attention(q, k, v, window=window, sink=sink, sm_scale=scale, n_keys=nk, out=out)
