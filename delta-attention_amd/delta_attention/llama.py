@@ -70,8 +70,12 @@ def rope_cos_sin(position_ids: torch.Tensor, head_dim: int, theta: float,
                                              device=position_ids.device).float() / head_dim))
     if rope_scaling:
         kw = dict(rope_scaling)
-        assert kw.pop("rope_type", "llama3") == "llama3", rope_scaling
-        inv_freq = llama3_inv_freq(inv_freq, **kw)
+        kind = kw.pop("rope_type", kw.pop("type", "llama3"))
+        kw.pop("type", None)
+        if kind != "default":
+            if kind != "llama3":
+                raise NotImplementedError(f"rope_scaling type {kind!r} (built: default, llama3)")
+            inv_freq = llama3_inv_freq(inv_freq, **kw)
     freqs = position_ids[..., None].float() * inv_freq[None, None, :]
     emb = torch.cat((freqs, freqs), dim=-1)
     return emb.cos().to(dtype), emb.sin().to(dtype)

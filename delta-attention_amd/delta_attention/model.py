@@ -45,6 +45,7 @@ class LlamaConfig:
     attention_bias: bool = False
     mlp_bias: bool = False
     attention_dropout: float = 0.0
+    tie_word_embeddings: bool = False
     _attn_implementation: str = "window"
     mode: str = "delta"
     delta_lambda: int = 64
@@ -193,11 +194,13 @@ class LlamaDecoderLayer(nn.Module):
 
 
 class LlamaModel(nn.Module):
+    layer_cls = LlamaDecoderLayer  # model-family hook (qwen3.py overrides)
+
     def __init__(self, config):
         super().__init__()
         self.config = config
         self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
-        self.layers = nn.ModuleList([LlamaDecoderLayer(config, i) for i in range(config.num_hidden_layers)])
+        self.layers = nn.ModuleList([self.layer_cls(config, i) for i in range(config.num_hidden_layers)])
         self.norm = LlamaRMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
     def rotary(self, position_ids: torch.Tensor, dtype: torch.dtype):
@@ -224,11 +227,20 @@ class LlamaModel(nn.Module):
 
 
 class LlamaForCausalLM(nn.Module):
+    model_cls = LlamaModel  # model-family hook (qwen3.py overrides)
+
     def __init__(self, config):
         super().__init__()
         self.config = config
-        self.model = LlamaModel(config)
+        self.model = self.model_cls(config)
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        self.tie_weights()
+
+    def tie_weights(self):
+        """With tie_word_embeddings, lm_head shares the embedding matrix (again
+        after `to_empty` / `to`, which give each module its own copy)."""
+        if getattr(self.config, "tie_word_embeddings", False):
+            self.lm_head.weight = self.model.embed_tokens.weight
 
     @torch.inference_mode()
     def prefill_next_token(self, input_ids: torch.Tensor, timer: Optional[Timer] = None) -> torch.Tensor:
@@ -262,14 +274,15 @@ class LlamaForCausalLM(nn.Module):
 
     def _decode_graphed(self, cache: KVCache, tok: torch.Tensor, max_new_tokens: int,
                         step_ms: Optional[list], logits_out: Optional[list],
-                        record: bool = True) -> torch.Tensor:
+                        record: bool = True, eos: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Decode steps 1 .. max_new_tokens-1 as HIP graph replays. The cache
         holds the token's row and key count on the device; each step kind
         (delta decode: anchor steps every min(gamma_dec, gamma_dec_max) steps,
         starting with the first; otherwise one kind) runs eagerly once, then is
         recorded and replayed. Outside the graph per step: the greedy argmax
         (into the next step's input) and the token copy. record=False runs
-        every step eagerly in the same static form (the replays' reference)."""
+        every step eagerly in the same static form (the replays' reference).
+        eos: stop once every row has produced one of these ids."""
         import time
         cfg = self.config
         mode = getattr(cfg, "decode_mode", "dense")
@@ -289,6 +302,8 @@ class LlamaForCausalLM(nn.Module):
             return logits
 
         n = max_new_tokens - 1
+        done = _finished(tok, eos)
+        ran = 0
         try:
             for j in range(n):
                 t0 = time.perf_counter()
@@ -305,20 +320,25 @@ class LlamaForCausalLM(nn.Module):
                         graphs[kind] = (g, glogits)
                 if logits_out is not None:
                     logits_out.append(logits.float().clone())
+                ran = j + 1
                 torch.argmax(logits, dim=-1, keepdim=True, out=tok_buf)
                 toks[:, j + 1] = tok_buf[:, 0]
                 if step_ms is not None:
                     torch.cuda.synchronize()
                     step_ms.append((time.perf_counter() - t0) * 1e3)
+                if done is not None:
+                    done |= _finished(tok_buf[:, 0], eos)
+                    if bool(done.all()):
+                        return toks[:, :j + 2]
         finally:
-            cache.stop_static(n)
+            cache.stop_static(ran)
         return toks
 
     @torch.inference_mode()
     def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
                         timer: Optional[Timer] = None, step_ms: Optional[list] = None,
                         graph: bool = False, logits_out: Optional[list] = None,
-                        record: bool = True) -> torch.Tensor:
+                        record: bool = True, eos_token_id=None) -> torch.Tensor:
         """Greedy generation as sample.py drives it: the prompt is prefilled
         with the configured attention ("window": delta attention), then each
         new token runs one decode step with `sdpa_rectangle` (dense, or the
@@ -327,9 +347,16 @@ class LlamaForCausalLM(nn.Module):
         step's fp32 logits, the prefill's first. graph: record the decode step in
         HIP graphs and replay it (when graph_decodable(); the decode rows then
         read the key count on the device, so they agree with the eager steps
-        to rounding); record=False runs those static steps eagerly."""
+        to rounding); record=False runs those static steps eagerly.
+        eos_token_id (int or ids): stop once every row has produced one (the
+        result then has fewer columns; rows that finished earlier keep
+        generating, the caller masks them)."""
         import time
         cfg = self.config
+        eos = None
+        if eos_token_id is not None:
+            ids = [eos_token_id] if isinstance(eos_token_id, int) else list(eos_token_id)
+            eos = torch.tensor(ids, dtype=torch.int64, device=input_ids.device)
         b, s = input_ids.shape
         cache = KVCache(cfg, b, s + max_new_tokens, input_ids.device, self.lm_head.weight.dtype)
         self.reset_decode_state()
@@ -342,9 +369,12 @@ class LlamaForCausalLM(nn.Module):
                 logits_out.append(logits.float().clone())
             tok = logits.argmax(-1)
             out.append(tok)
+            done = _finished(tok, eos)
             cfg._attn_implementation = "sdpa_rectangle"
+            if done is not None and bool(done.all()):
+                return torch.stack(out, dim=1)
             if graph and self.graph_decodable() and max_new_tokens > 1:
-                return self._decode_graphed(cache, tok, max_new_tokens, step_ms, logits_out, record)
+                return self._decode_graphed(cache, tok, max_new_tokens, step_ms, logits_out, record, eos)
             for _ in range(max_new_tokens - 1):
                 t0 = time.perf_counter()
                 h = self.model(tok[:, None], timer, cache)
@@ -356,9 +386,62 @@ class LlamaForCausalLM(nn.Module):
                 if step_ms is not None:
                     torch.cuda.synchronize()
                     step_ms.append((time.perf_counter() - t0) * 1e3)
+                if done is not None:
+                    done |= _finished(tok, eos)
+                    if bool(done.all()):
+                        break
         finally:
             cfg._attn_implementation = impl
         return torch.stack(out, dim=1)
+
+    @torch.inference_mode()
+    def generate(self, input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
+                 max_new_tokens: int = 128, do_sample: bool = False, eos_token_id=None,
+                 pad_token_id: Optional[int] = None, graph: bool = False, **unused) -> torch.Tensor:
+        """The call model_wrapper.py:97 makes (HF `generate` with the greedy
+        `_sample` loop of sample.py:25-262): -> [b, s + n] token ids, the
+        prompt (with its padding) followed by the generated tokens; after a
+        row's first eos token its remaining positions hold pad_token_id, and
+        generation stops once every row has finished. Left-padded rows
+        (attention_mask 0 on the padding) run one at a time over their real
+        tokens: the attention kernels take no padding mask. Only greedy
+        decoding is built (do_sample=True raises); `unused` takes the
+        generation kwargs greedy decoding ignores (temperature, top_k, ...)."""
+        if do_sample:
+            raise NotImplementedError("only greedy decoding (do_sample=False) is built")
+        if unused.get("repetition_penalty") not in (None, 1, 1.0):
+            raise NotImplementedError("repetition_penalty other than 1 is not built")
+        b, s = input_ids.shape
+        if pad_token_id is None:
+            pad_token_id = (eos_token_id if isinstance(eos_token_id, int)
+                            else (list(eos_token_id)[0] if eos_token_id is not None else 0))
+        if attention_mask is None or bool(attention_mask.bool().all()):
+            rows = [self.generate_greedy(input_ids, max_new_tokens, graph=graph,
+                                         eos_token_id=eos_token_id)]
+            rows = list(rows[0].unbind(0))
+        else:
+            rows = []
+            for i in range(b):
+                keep = attention_mask[i].bool()
+                if not bool(keep.any()):
+                    raise ValueError(f"row {i} of the batch has no tokens (attention_mask all 0)")
+                rows.append(self.generate_greedy(input_ids[i:i + 1, keep], max_new_tokens,
+                                                 graph=graph, eos_token_id=eos_token_id)[0])
+        ids = ([eos_token_id] if isinstance(eos_token_id, int) else list(eos_token_id)
+               if eos_token_id is not None else [])
+        n = max(len(r) for r in rows)
+        new = torch.full((b, n), int(pad_token_id), dtype=input_ids.dtype, device=input_ids.device)
+        for i, r in enumerate(rows):
+            hit = (torch.isin(r, torch.tensor(ids, device=r.device)).nonzero()
+                   if ids else torch.empty(0, 1))
+            end = int(hit[0, 0]) + 1 if len(hit) else len(r)
+            new[i, :end] = r[:end]
+        return torch.cat([input_ids, new], dim=1)
+
+
+def _finished(tok: torch.Tensor, eos: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """[b] bool: which rows' token is an eos id (None without eos ids)."""
+    return None if eos is None else torch.isin(tok, eos)
 
 
 def init_weights_(model: nn.Module, std: float, seed: int = 0) -> nn.Module:
@@ -383,7 +466,14 @@ def random_llama(config: LlamaConfig, device="cuda", dtype=torch.bfloat16, seed:
     with torch.device("meta"):
         model = LlamaForCausalLM(config)
     model = model.to_empty(device=device).to(dtype)
+    model.tie_weights()
     model = init_weights_(model, config.initializer_range, seed).eval().requires_grad_(False)
+    return fuse_model_projections(model)
+
+
+def fuse_model_projections(model: nn.Module) -> nn.Module:
+    """fuse_projections on every attention and MLP block (one product each for
+    q/k/v and gate/up on short inputs; names and values unchanged)."""
     for m in model.modules():
         if isinstance(m, (LlamaAttention, LlamaMLP)):
             m.fuse_projections()

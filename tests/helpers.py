@@ -67,3 +67,57 @@ def workload_inputs(B, H, Hkv, S, D, theta, seed=0, qk_norm=False, q_scale=True)
         k[:, :, c0:c1] = kc.to(torch.bfloat16)
         v[:, :, c0:c1] = torch.randn(B, Hkv, c1 - c0, D, device="cuda", generator=g).to(torch.bfloat16)
     return q, k, v
+
+
+def write_checkpoint(path, model_type="llama", seed=0, tied=False, shards=1, tokenizer=True, **cfg):
+    """A small Hugging Face-format checkpoint in `path`: config.json,
+    safetensors weights (one file, or `shards` files with an index; with tied
+    embeddings lm_head.weight is left out, as Hugging Face saves it) and a
+    word-level tokenizer over the words w2 .. w{vocab-1} with </s> (id 1) as
+    eos. -> the float32 state dict written (unfused parameter names)."""
+    import json
+    import os
+    from safetensors.torch import save_file
+    from delta_attention.model import LlamaConfig, LlamaForCausalLM, init_weights_
+    from delta_attention.qwen3 import Qwen3Config, Qwen3ForCausalLM
+    cls, cfg_cls = (Qwen3ForCausalLM, Qwen3Config) if model_type == "qwen3" else (LlamaForCausalLM, LlamaConfig)
+    arch = dict(vocab_size=64, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                num_attention_heads=4, num_key_value_heads=2, head_dim=64, tie_word_embeddings=tied)
+    arch.update(cfg)
+    m = init_weights_(cls(cfg_cls(**arch)), 0.02, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        for n, p in m.named_parameters():
+            if n.endswith("norm.weight"):      # non-trivial norm weights
+                p.uniform_(0.5, 1.5, generator=g)
+    sd = {n: p.detach().contiguous().clone() for n, p in m.named_parameters()}
+    if tied:
+        sd.pop("lm_head.weight", None)
+    hf = dict(model_type=model_type, torch_dtype="bfloat16", **{k: v for k, v in arch.items()})
+    if model_type == "qwen3":
+        hf["rope_scaling"] = None
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "config.json"), "w") as f:
+        json.dump(hf, f)
+    names = sorted(sd)
+    if shards == 1:
+        save_file(sd, os.path.join(path, "model.safetensors"))
+    else:
+        wmap = {}
+        for i in range(shards):
+            fn = f"model-{i + 1:05d}-of-{shards:05d}.safetensors"
+            part = {n: sd[n] for n in names[i::shards]}
+            save_file(part, os.path.join(path, fn))
+            wmap.update({n: fn for n in part})
+        with open(os.path.join(path, "model.safetensors.index.json"), "w") as f:
+            json.dump({"metadata": {}, "weight_map": wmap}, f)
+    if tokenizer:
+        from tokenizers import Tokenizer, models, pre_tokenizers
+        vocab = {"<unk>": 0, "</s>": 1, **{f"w{i}": i for i in range(2, arch["vocab_size"])}}
+        tok = Tokenizer(models.WordLevel(vocab, unk_token="<unk>"))
+        tok.pre_tokenizer = pre_tokenizers.Whitespace()
+        tok.save(os.path.join(path, "tokenizer.json"))
+        with open(os.path.join(path, "tokenizer_config.json"), "w") as f:
+            json.dump({"tokenizer_class": "PreTrainedTokenizerFast", "eos_token": "</s>",
+                       "unk_token": "<unk>"}, f)
+    return sd
