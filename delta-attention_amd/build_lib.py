@@ -15,7 +15,8 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "delta_attention", "libdelta_attn.so")
-SOURCES = ["attn_kernels.hip", "delta_add.hip", "rope.hip", "norm.hip", "anchor_cos.hip"]
+SOURCES = ["attn_kernels.hip", "attn_bwd.hip", "delta_add.hip", "rope.hip", "norm.hip",
+           "anchor_cos.hip"]
 ARCH = "gfx950"
 
 # Packed fp32 VALU ops are disabled: they are not used by hand and must not be

@@ -117,6 +117,9 @@ struct AttnArgs {
   void* dout;
   int64_t dout_b, dout_h, dout_a;
   int gamma, s_p, n_anchor;
+  // MODE_SPARSE: optional row log-sum-exp [B, Hq, n_rows] (log2 domain of the
+  // scaled scores, +inf for a row without visible keys), for the backward
+  float* lse;
 };
 
 // Bytes of LDS that hold a fused tile's dense anchor rows, prefetched with the
@@ -687,6 +690,9 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   if (MODE == MODE_SPARSE) {
     if (!valid) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (a.lse && lg == 0)
+      a.lse[((int64_t)b * a.Hq + hrow) * a.n_rows + irow] =
+          l_tot > 0.f ? m_i + __builtin_log2f(l_tot) : INFINITY;
     char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
                              (int64_t)qrow * a.os_s) * esz;
 #pragma unroll
@@ -744,6 +750,8 @@ struct MergeArgs {
   // out = rnd(rnd(merged) + addend), the bf16 add of a cached decode delta
   const void* add;
   int64_t as_b, as_h, as_s;
+  // DA_EPI_OUTPUT: optional row log-sum-exp [B, Hq, n] (as AttnArgs::lse)
+  float* lse;
 };
 
 template <typename T, int D>
@@ -837,6 +845,8 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
 
     const int qrow = a.q_rows ? (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1)) : i;
     if (a.epi == DA_EPI_OUTPUT) {
+      if (a.lse && c == 0)
+        a.lse[((int64_t)b * a.Hkv * G + h) * a.n_rows + i] = L > 0.f ? M + __builtin_log2f(L) : INFINITY;
       char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)h * a.os_h + (int64_t)i * a.os_s + 8 * c) * esz;
       u32x4 pk = {E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3]),
                   E::pack2(acc[4], acc[5]), E::pack2(acc[6], acc[7])};
@@ -1018,6 +1028,25 @@ extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, v
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }
 
+extern "C" int da_sparse_attn_fwd_lse(const void* q, const void* k, const void* v, void* out,
+                                      int B, int Hq, int Hkv, int S, int D,
+                                      const int64_t q_str[3], const int64_t k_str[3],
+                                      const int64_t v_str[3], const int64_t o_str[3],
+                                      int window, int sink, int q_block, float sm_scale,
+                                      float* lse, int dtype, void* stream) {
+  AttnArgs a;
+  int rc = sparse_args(a, q, k, v, out, B, Hq, Hkv, S, D, q_str, k_str, v_str, o_str,
+                       window, sink, q_block, sm_scale, dtype);
+  if (rc != DA_OK || S == 0) return rc;
+  if (!lse) return DA_ERR_INVALID_ARG;
+  if (((uintptr_t)lse & 3u) != 0) return DA_ERR_ALIGNMENT;
+  a.lse = lse;
+  if ((rc = sparse_items(a)) != DA_OK) return rc;
+  (void)hipGetLastError();
+  dispatch_attn<MODE_SPARSE>(a, D, dtype, (hipStream_t)stream);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}
+
 extern "C" int da_fused_delta_rows(int Hq, int Hkv) {
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;
   return BM;
@@ -1068,7 +1097,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
                        int window, int sink, float sm_scale, void* workspace,
                        size_t workspace_bytes, int dtype, void* stream,
                        const int* n_kv_dev = nullptr, const void* add = nullptr,
-                       const int64_t* add_str = nullptr) {
+                       const int64_t* add_str = nullptr, float* lse = nullptr) {
   if (p.n_items <= 0) return DA_ERR_INVALID_ARG;
   if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
@@ -1109,6 +1138,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   if (d_str) { m.ds_b = d_str[0]; m.ds_h = d_str[1]; m.ds_a = d_str[2]; }
   m.add = add;
   if (add) { m.as_b = add_str[0]; m.as_h = add_str[1]; m.as_s = add_str[2]; }
+  m.lse = lse;
 
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
@@ -1133,14 +1163,14 @@ extern "C" size_t da_qsparse_workspace_bytes(int B, int Hq, int Hkv, int n, int 
   return plan_rows(B, Hq, Hkv, n, Skv, D).ws_bytes;
 }
 
-extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
-                                   const int64_t* q_rows, const int64_t* row_last, int64_t rl_bstride,
-                                   int n, int B, int Hq, int Hkv, int Sq, int Skv, int D,
-                                   const int64_t q_str[3], const int64_t k_str[3], const int64_t v_str[3],
-                                   void* o, const int64_t o_str[3],
-                                   int epi, int n_anchor, void* delta, const int64_t d_str[3],
-                                   float sm_scale, void* workspace, size_t workspace_bytes,
-                                   int dtype, void* stream) {
+static int qsparse_fwd(const void* q, const void* k, const void* v,
+                       const int64_t* q_rows, const int64_t* row_last, int64_t rl_bstride,
+                       int n, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                       const int64_t q_str[3], const int64_t k_str[3], const int64_t v_str[3],
+                       void* o, const int64_t o_str[3],
+                       int epi, int n_anchor, void* delta, const int64_t d_str[3],
+                       float sm_scale, void* workspace, size_t workspace_bytes,
+                       int dtype, void* stream, float* lse) {
   int rc;
   if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
   if (n < 0 || Sq < 0 || Skv < 0 || rl_bstride < 0) return DA_ERR_INVALID_ARG;
@@ -1162,7 +1192,36 @@ extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
   const QsparsePlan p = plan_rows(B, Hq, Hkv, n, Skv, D);
   return run_qsparse(p, q, k, v, q_rows, row_last, rl_bstride, n, B, Hq, Hkv, Sq, Skv, D,
                      q_str, k_str, v_str, o, o_str, epi, n_anchor, delta, d_str, 0, 0,
-                     sm_scale, workspace, workspace_bytes, dtype, stream);
+                     sm_scale, workspace, workspace_bytes, dtype, stream, nullptr, nullptr,
+                     nullptr, lse);
+}
+
+extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
+                                   const int64_t* q_rows, const int64_t* row_last, int64_t rl_bstride,
+                                   int n, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                                   const int64_t q_str[3], const int64_t k_str[3], const int64_t v_str[3],
+                                   void* o, const int64_t o_str[3],
+                                   int epi, int n_anchor, void* delta, const int64_t d_str[3],
+                                   float sm_scale, void* workspace, size_t workspace_bytes,
+                                   int dtype, void* stream) {
+  return qsparse_fwd(q, k, v, q_rows, row_last, rl_bstride, n, B, Hq, Hkv, Sq, Skv, D, q_str,
+                     k_str, v_str, o, o_str, epi, n_anchor, delta, d_str, sm_scale, workspace,
+                     workspace_bytes, dtype, stream, nullptr);
+}
+
+extern "C" int da_qsparse_attn_fwd_lse(const void* q, const void* k, const void* v,
+                                       const int64_t* q_rows, const int64_t* row_last,
+                                       int64_t rl_bstride, int n, int B, int Hq, int Hkv,
+                                       int Sq, int Skv, int D, const int64_t q_str[3],
+                                       const int64_t k_str[3], const int64_t v_str[3],
+                                       void* o, const int64_t o_str[3], float* lse,
+                                       float sm_scale, void* workspace, size_t workspace_bytes,
+                                       int dtype, void* stream) {
+  if (n > 0 && !lse) return DA_ERR_INVALID_ARG;
+  if (((uintptr_t)lse & 3u) != 0) return DA_ERR_ALIGNMENT;
+  return qsparse_fwd(q, k, v, q_rows, row_last, rl_bstride, n, B, Hq, Hkv, Sq, Skv, D, q_str,
+                     k_str, v_str, o, o_str, DA_EPI_OUTPUT, 0, nullptr, nullptr, sm_scale,
+                     workspace, workspace_bytes, dtype, stream, lse);
 }
 
 extern "C" size_t da_decode_workspace_bytes(int B, int Hq, int Hkv, int n_keys, int D, int window,

@@ -43,6 +43,13 @@ EXPORTS = (
     "da_add_rmsnorm",
     "da_swiglu",
     "da_anchor_delta_cos",
+    "da_sparse_attn_fwd_lse",
+    "da_qsparse_attn_fwd_lse",
+    "da_sparse_attn_bwd_workspace_bytes",
+    "da_qsparse_attn_bwd_workspace_bytes",
+    "da_sparse_attn_bwd",
+    "da_qsparse_attn_bwd",
+    "da_delta_compose_bwd",
     "da_build_target",
 )
 
@@ -136,6 +143,28 @@ def _load() -> ctypes.CDLL:
     L.da_anchor_delta_cos.restype = _i
     L.da_anchor_delta_cos.argtypes = [_vp, _p3, _vp, _p3, _vp, _i64, _i, _i, _i, _i,
                                       _vp, _vp, _i, _f, _f, _i, _vp]
+    L.da_sparse_attn_fwd_lse.restype = _i
+    L.da_sparse_attn_fwd_lse.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                         _p3, _p3, _p3, _p3, _i, _i, _i, _f, _vp, _i, _vp]
+    L.da_qsparse_attn_fwd_lse.restype = _i
+    L.da_qsparse_attn_fwd_lse.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _i, _i, _i, _i,
+                                          _i, _p3, _p3, _p3, _vp, _p3, _vp, _f, _vp, _sz, _i, _vp]
+    L.da_sparse_attn_bwd_workspace_bytes.restype = _sz
+    L.da_sparse_attn_bwd_workspace_bytes.argtypes = [_i, _i, _i, _i, _i, _i, _i, _i]
+    L.da_qsparse_attn_bwd_workspace_bytes.restype = _sz
+    L.da_qsparse_attn_bwd_workspace_bytes.argtypes = [_i, _i, _i, _i, _i, _i]
+    L.da_sparse_attn_bwd.restype = _i
+    L.da_sparse_attn_bwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _i, _i, _i, _i, _i, _p3, _p3, _p3, _p3, _p3, _p3, _p3, _p3,
+                                     _i, _i, _i, _f, _i, _vp, _sz, _i, _vp]
+    L.da_qsparse_attn_bwd.restype = _i
+    L.da_qsparse_attn_bwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                                      _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
+                                      _p3, _p3, _p3, _p3, _p3, _p3, _p3, _p3,
+                                      _f, _i, _vp, _sz, _i, _vp]
+    L.da_delta_compose_bwd.restype = _i
+    L.da_delta_compose_bwd.argtypes = [_vp, _p3, _vp, _p3, _vp, _p3, _i, _i, _i, _i, _i, _i,
+                                       _f, _i, _i, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
     return L

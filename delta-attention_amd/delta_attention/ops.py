@@ -247,6 +247,143 @@ def delta_add(sparse: torch.Tensor, *, s_p: int, out: Optional[torch.Tensor] = N
 
 
 # ---------------------------------------------------------------------------
+# training path: forward with saved row log-sum-exp, and the backward
+
+def _s3(t: torch.Tensor, a: int, b: int, c: int):
+    return L.strides3(t.stride(a), t.stride(b), t.stride(c))
+
+
+def sparse_attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int,
+                         sink: int, sm_scale: float, q_block: int = Q_BLOCK
+                         ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """sparse_attention plus each row's log2-domain log-sum-exp:
+    -> (out [B,S,H,D], lse float32 [B,H,S])."""
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    assert k.shape == (B, Hkv, S, D) and v.shape == k.shape and H % Hkv == 0
+    dev = _on_gpu(q, k, v)
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    out = torch.empty((B, S, H, D), device=dev, dtype=q.dtype)
+    lse = torch.empty((B, H, S), device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_sparse_attn_fwd_lse(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, S, D,
+            _s3(q, 0, 1, 2), _s3(k, 0, 1, 2), _s3(v, 0, 1, 2), _s3(out, 0, 2, 1),
+            int(window), int(sink), int(q_block), float(sm_scale), _ptr(lse), _code(q),
+            _stream(dev))
+    L.check(rc, "da_sparse_attn_fwd_lse")
+    return out, lse
+
+
+def rows_attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rows: torch.Tensor,
+                       sm_scale: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Rows `rows` (int64 [n]) of q attending keys 0 .. rows[i] (causal):
+    -> (out [B,n,H,D], lse float32 [B,H,n])."""
+    B, H, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    assert k.shape == (B, Hkv, Skv, D) and v.shape == k.shape and H % Hkv == 0
+    dev = _on_gpu(q, k, v, rows)
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    rows = rows.reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
+    n = rows.numel()
+    out = torch.empty((B, n, H, D), device=dev, dtype=q.dtype)
+    lse = torch.empty((B, H, n), device=dev, dtype=torch.float32)
+    ws = qsparse_workspace(B, H, Hkv, n, Skv, D, dev)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_qsparse_attn_fwd_lse(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(rows), _ptr(rows), 0, n, B, H, Hkv, Sq, Skv, D,
+            _s3(q, 0, 1, 2), _s3(k, 0, 1, 2), _s3(v, 0, 1, 2), _ptr(out), _s3(out, 0, 2, 1),
+            _ptr(lse), float(sm_scale), _ptr(ws), ws.numel(), _code(q), _stream(dev))
+    L.check(rc, "da_qsparse_attn_fwd_lse")
+    return out, lse
+
+
+def _grads_like(q, k, dq, dk, dv):
+    dq = torch.empty_like(q) if dq is None else dq
+    dk = torch.empty_like(k) if dk is None else dk
+    dv = torch.empty_like(k) if dv is None else dv
+    for t in (dq, dk, dv):
+        assert t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(x % 8 == 0 for x in t.stride()[:-1])
+    return dq, dk, dv
+
+
+def sparse_attention_bwd(q, k, v, out, dout, lse, *, window: int, sink: int, sm_scale: float,
+                         q_block: int = Q_BLOCK, dq=None, dk=None, dv=None,
+                         accumulate: bool = False):
+    """Gradients of sparse_attention: q [B,H,S,D], k/v [B,Hkv,S,D], out/dout
+    [B,S,H,D], lse [B,H,S] -> (dq, dk, dv) shaped like q, k, v (new, or the
+    given tensors; accumulate=True adds into them)."""
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    dev = _on_gpu(q, k, v, out, dout, lse)
+    q, k, v, out, dout = _ready(q), _ready(k), _ready(v), _ready(out), _ready(dout)
+    lse = lse.contiguous()
+    assert out.shape == dout.shape == (B, S, H, D) and lse.shape == (B, H, S)
+    dq, dk, dv = _grads_like(q, k, dq, dk, dv)
+    nbytes = int(L.lib().da_sparse_attn_bwd_workspace_bytes(B, H, Hkv, S, D, int(window),
+                                                            int(sink), int(q_block)))
+    ws = torch.empty(max(nbytes, 16), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_sparse_attn_bwd(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse),
+            _ptr(dq), _ptr(dk), _ptr(dv), B, H, Hkv, S, D,
+            _s3(q, 0, 1, 2), _s3(k, 0, 1, 2), _s3(v, 0, 1, 2), _s3(out, 0, 2, 1),
+            _s3(dout, 0, 2, 1), _s3(dq, 0, 1, 2), _s3(dk, 0, 1, 2), _s3(dv, 0, 1, 2),
+            int(window), int(sink), int(q_block), float(sm_scale), int(bool(accumulate)),
+            _ptr(ws), ws.numel(), _code(q), _stream(dev))
+    L.check(rc, "da_sparse_attn_bwd")
+    return dq, dk, dv
+
+
+def rows_attention_bwd(q, k, v, rows, out, dout, lse, *, sm_scale: float, dq=None, dk=None,
+                       dv=None, accumulate: bool = False):
+    """Gradients of rows_attention_lse (rows ascending and distinct): out/dout
+    [B,n,H,D], lse [B,H,n] -> (dq, dk, dv) shaped like q, k, v; dq rows outside
+    `rows` are zero (or untouched with accumulate=True)."""
+    B, H, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    dev = _on_gpu(q, k, v, rows, out, dout, lse)
+    q, k, v, out, dout = _ready(q), _ready(k), _ready(v), _ready(out), _ready(dout)
+    rows = rows.reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
+    lse = lse.contiguous()
+    n = rows.numel()
+    assert out.shape == dout.shape == (B, n, H, D) and lse.shape == (B, H, n)
+    if dq is None and not accumulate:
+        dq = torch.zeros_like(q)
+    dq, dk, dv = _grads_like(q, k, dq, dk, dv)
+    nbytes = int(L.lib().da_qsparse_attn_bwd_workspace_bytes(B, H, Hkv, n, Skv, D))
+    ws = torch.empty(max(nbytes, 16), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_qsparse_attn_bwd(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(rows), _ptr(rows), n,
+            _ptr(dq), _ptr(dk), _ptr(dv), B, H, Hkv, Sq, Skv, D,
+            _s3(q, 0, 1, 2), _s3(k, 0, 1, 2), _s3(v, 0, 1, 2), _s3(out, 0, 2, 1),
+            _s3(dout, 0, 2, 1), _s3(dq, 0, 1, 2), _s3(dk, 0, 1, 2), _s3(dv, 0, 1, 2),
+            float(sm_scale), int(bool(accumulate)), _ptr(ws), ws.numel(), _code(q), _stream(dev))
+    L.check(rc, "da_qsparse_attn_bwd")
+    return dq, dk, dv
+
+
+def delta_compose_bwd(grad: torch.Tensor, *, gamma: int, s_p: int, delta_grad_scale: float = 1.0,
+                      detach_delta: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Backward of the delta composition: grad [B,S,H,D] -> (dsparse [B,S,H,D],
+    ddense [B, s_p/gamma + S - s_p, H, D]) (include/delta_attn.h)."""
+    B, S, H, D = grad.shape
+    dev = _on_gpu(grad)
+    grad = _ready(grad)
+    n_sel = s_p // gamma + S - s_p
+    dsparse = torch.empty((B, S, H, D), device=dev, dtype=grad.dtype)
+    ddense = torch.empty((B, n_sel, H, D), device=dev, dtype=grad.dtype)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_delta_compose_bwd(
+            _ptr(grad), _s3(grad, 0, 2, 1), _ptr(dsparse), _s3(dsparse, 0, 2, 1),
+            _ptr(ddense), _s3(ddense, 0, 2, 1), B, H, S, D, int(gamma), int(s_p),
+            float(delta_grad_scale), int(bool(detach_delta)), _code(grad), _stream(dev))
+    L.check(rc, "da_delta_compose_bwd")
+    return dsparse, ddense
+
+
+# ---------------------------------------------------------------------------
 # attention prologue: per-head RMSNorm (optional) + RoPE, in place
 
 def rope_qk(q: Optional[torch.Tensor], k: Optional[torch.Tensor], cos: torch.Tensor,

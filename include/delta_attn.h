@@ -274,6 +274,94 @@ int da_anchor_delta_cos(const void* a, const int64_t a_str[3],
                         float* cos_out, int* hist, int bins, float lo, float hi,
                         int dtype, void* stream);
 
+/*
+ * Training path: forward with saved row statistics, and the backward.
+ * Together they replace the autograd of delta_forward_train
+ * (delta_attention/train/flex_delta.py:95-196): its flex_attention sparse
+ * branch (:167-170), the masked-SDPA anchor/tail rows (:175-184) and the
+ * composition (:186-196).
+ *
+ * lse: fp32 [B, Hq, rows] (contiguous), the log-sum-exp of each row's scaled
+ * scores in the log2 domain (scores times sm_scale * log2(e)): lse = m + log2(l);
+ * +inf for a row with no visible key.
+ *
+ * da_sparse_attn_fwd_lse: da_sparse_attn_fwd plus lse ([B, Hq, S]).
+ */
+int da_sparse_attn_fwd_lse(const void* q, const void* k, const void* v, void* out,
+                           int B, int Hq, int Hkv, int S, int D,
+                           const int64_t q_str[3], const int64_t k_str[3],
+                           const int64_t v_str[3], const int64_t o_str[3],
+                           int window, int sink, int q_block, float sm_scale,
+                           float* lse, int dtype, void* stream);
+
+/* da_qsparse_attn_fwd with epi == DA_EPI_OUTPUT, plus lse ([B, Hq, n]). */
+int da_qsparse_attn_fwd_lse(const void* q, const void* k, const void* v,
+                            const int64_t* q_rows, const int64_t* row_last, int64_t rl_bstride,
+                            int n, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                            const int64_t q_str[3], const int64_t k_str[3],
+                            const int64_t v_str[3], void* o, const int64_t o_str[3],
+                            float* lse, float sm_scale, void* workspace, size_t workspace_bytes,
+                            int dtype, void* stream);
+
+/*
+ * Gradients of key-sparse attention (the mask of da_sparse_attn_fwd; the
+ * backward of flex_delta.py:167-170). o/dout: the forward output and its
+ * gradient, [B, S, Hq, D] with o_str/do_str = {batch, head, row}; lse from
+ * da_sparse_attn_fwd_lse. dq [B, Hq, S, D], dk/dv [B, Hkv, S, D] (strides
+ * {batch, head, row}) receive the gradients (GQA: summed over each KV head's
+ * query heads); accumulate != 0 adds them instead: x = rnd(x + rnd(grad)).
+ * Workspace: da_sparse_attn_bwd_workspace_bytes.
+ */
+size_t da_sparse_attn_bwd_workspace_bytes(int B, int Hq, int Hkv, int S, int D,
+                                          int window, int sink, int q_block);
+int da_sparse_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                       const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                       int B, int Hq, int Hkv, int S, int D,
+                       const int64_t q_str[3], const int64_t k_str[3],
+                       const int64_t v_str[3], const int64_t o_str[3],
+                       const int64_t do_str[3], const int64_t dq_str[3],
+                       const int64_t dk_str[3], const int64_t dv_str[3],
+                       int window, int sink, int q_block, float sm_scale, int accumulate,
+                       void* workspace, size_t workspace_bytes, int dtype, void* stream);
+
+/*
+ * Gradients of selected rows attending their causal keys (the backward of the
+ * masked SDPA at flex_delta.py:178-184). Row i is q row q_rows[i] (distinct
+ * rows) and sees keys 0 .. row_last[i]; row_last must be ascending (the
+ * anchor-then-tail order is). o/dout [B, n, Hq, D] with {batch, head, i}
+ * strides, lse [B, Hq, n] from da_qsparse_attn_fwd_lse; dq is [B, Hq, Sq, D]
+ * (rows q_rows[i] written or, with accumulate, added to), dk/dv as above.
+ */
+size_t da_qsparse_attn_bwd_workspace_bytes(int B, int Hq, int Hkv, int n, int Skv, int D);
+int da_qsparse_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                        const void* dout, const float* lse,
+                        const int64_t* q_rows, const int64_t* row_last, int n,
+                        void* dq, void* dk, void* dv,
+                        int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                        const int64_t q_str[3], const int64_t k_str[3],
+                        const int64_t v_str[3], const int64_t o_str[3],
+                        const int64_t do_str[3], const int64_t dq_str[3],
+                        const int64_t dk_str[3], const int64_t dv_str[3],
+                        float sm_scale, int accumulate, void* workspace,
+                        size_t workspace_bytes, int dtype, void* stream);
+
+/*
+ * Backward of the composition (flex_delta.py:186-196, and the _ScaleGrad /
+X [B, S, H, D] ->
+ *   dsparse [B, S, H, D]: grad[r] for r < s_p, rnd(grad[r] - ddelta[r / gamma])
+ *                         at anchor rows, 0 for r >= s_p;
+ *   ddense [B, n_anchor + S - s_p, H, D]: ddelta[i] for the anchors, then
+ *                         grad[s_p + t] for the tail rows;
+ * with ddelta[i] = rnd(delta_grad_scale * rnd(sum_j grad[i gamma + j])) (the
+ * scale multiply only when it is not 1), 0 when detach_delta. Strides
+ * {batch, head, row}; requires s_p % gamma == 0.
+ */
+int da_delta_compose_bwd(const void* grad, const int64_t g_str[3],
+                         void* dsparse, const int64_t sp_str[3],
+                         void* ddense, const int64_t dd_str[3],
+                         int B, int H, int S, int D, int gamma, int s_p,
+                         float delta_grad_scale, int detach_delta, int dtype, void* stream);
+
 /* Library identification: the gfx target the code objects were built for. */
 const char* da_build_target(void);
 

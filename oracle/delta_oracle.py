@@ -29,6 +29,11 @@ prefill (file:line cite the reference, singhh5050/delta-attention):
                          each norm clamped to eps = 1e-8)
   histc                  drift.py:33: torch.histc's binning (bins over [lo, hi],
                          x == hi in the last bin, out-of-range and NaN dropped)
+  masked_attention_grads the attention backward that autograd forms for the
+                         FlexAttention / masked SDPA branches of flex_delta.py:167-184
+  compose_grads          the composition's backward (flex_delta.py:186-196, the
+                         detach / gradient-scale arms at :187-190)
+  delta_train_grads      gradients of delta_forward_train (flex_delta.py:95-196)
 
 Pinning (tests/test_oracle.py): every function is checked against brute force
 on tiny inputs, library routines (torch scaled_dot_product_attention in
@@ -322,6 +327,83 @@ def delta_forward(q: np.ndarray, k: np.ndarray, v: np.ndarray, gamma: int, windo
         return out
     assert mode == "delta", mode
     return compose_uniform(sparse, dense, s, gamma)
+
+
+# ---------------------------------------------------------------------------
+# training path: gradients of the delta composition (flex_delta.py:95-196
+# under autograd)
+
+def masked_attention_grads(q: np.ndarray, k: np.ndarray, v: np.ndarray, allowed: np.ndarray,
+                           scale: float, dout: np.ndarray):
+    """Gradients of masked_attention for the upstream gradient dout [B,H,n,d]:
+    P = softmax(scale q k^T + mask), O = P v;
+      dV = P^T dO, dP = dO V^T, dS = P * (dP - rowsum(dO * O)),
+      dQ = scale dS K, dK = scale dS^T Q,
+    dK / dV summed over the query heads of each KV head (the backward of
+    repeat_interleave). -> (dq [B,H,n,d], dk [B,Hkv,N,d], dv [B,Hkv,N,d])."""
+    B, H, n, d = q.shape
+    Hkv, N = k.shape[1], k.shape[2]
+    kk, vv = _expand_kv(k, H), _expand_kv(v, H)
+    sc = np.matmul(q, kk.swapaxes(-1, -2)) * scale
+    sc = np.where(allowed[None, None], sc, -np.inf)
+    p = _softmax_rows(sc)
+    o = np.matmul(p, vv)
+    dv_e = np.matmul(p.swapaxes(-1, -2), dout)
+    dp = np.matmul(dout, vv.swapaxes(-1, -2))
+    di = (dout * o).sum(-1, keepdims=True)
+    ds = p * (dp - di)
+    dq = scale * np.matmul(ds, kk)
+    dk_e = scale * np.matmul(ds.swapaxes(-1, -2), q)
+    G = H // Hkv
+    return dq, dk_e.reshape(B, Hkv, G, N, d).sum(2), dv_e.reshape(B, Hkv, G, N, d).sum(2)
+
+
+def compose_grads(g: np.ndarray, gamma: int, s_p: int, grad_scale: float = 1.0,
+                  detach: bool = False):
+    """Backward of compose_uniform (flex_delta.py:186-196 with the detach and
+    _ScaleGrad arms of :187-190): g [B,s,H,d] -> (dsparse [B,s,H,d], ddense
+    [B, n_anchor + s - s_p, H, d]). ddelta[i] = grad_scale * sum of g over
+    group i (0 when detached); dsparse = g on rows < s_p minus ddelta at the
+    anchors, 0 on the tail; ddense = (ddelta, g of the tail rows)."""
+    B, s, H, d = g.shape
+    s_p = max(s_p, 0)
+    n = s_p // gamma
+    ddelta = g[:, :s_p].reshape(B, n, gamma, H, d).sum(2) * grad_scale
+    if detach:
+        ddelta = np.zeros_like(ddelta)
+    dsparse = np.zeros_like(g)
+    dsparse[:, :s_p] = g[:, :s_p]
+    dsparse[:, np.arange(0, s_p, gamma)] -= ddelta
+    ddense = np.concatenate([ddelta, g[:, s_p:]], axis=1)
+    return dsparse, ddense
+
+
+def delta_train_grads(q: np.ndarray, k: np.ndarray, v: np.ndarray, gamma: int, window: int,
+                      sink: int, scale: float, g: np.ndarray, grad_scale: float = 1.0,
+                      detach: bool = False, q_block: int = Q_BLOCK, parts: bool = False):
+    """Gradients of delta_forward_train for the upstream gradient g [B,s,H,d]:
+    the composition's backward, then the key-sparse attention's (mask of
+    sparse_visible) and the anchor/tail rows' causal attention's, their dq,
+    dk, dv added. q [B,H,s,d], k/v [B,Hkv,s,d] -> (dq, dk, dv); with
+    parts=True also each branch's (dq, dk, dv) (the sparse branch's, then the
+    anchor/tail rows' with dq scattered to the full rows). Dense masks: small
+    sizes only."""
+    B, H, s, d = q.shape
+    anchors, tail, s_p, _ = anchor_layout(s, gamma)
+    sel = np.concatenate([anchors, tail])
+    dsparse, ddense = compose_grads(g, gamma, s_p, grad_scale, detach)
+    r = np.arange(s)
+    allowed = sparse_visible(r[:, None], r[None, :], window, sink, q_block)
+    dq, dk, dv = masked_attention_grads(q, k, v, allowed, scale, dsparse.transpose(0, 2, 1, 3))
+    allowed_d = r[None, :] <= sel[:, None]
+    dq2, dk2, dv2 = masked_attention_grads(q[:, :, sel], k, v, allowed_d, scale,
+                                           ddense.transpose(0, 2, 1, 3))
+    dq_full2 = np.zeros_like(dq)
+    dq_full2[:, :, sel] = dq2
+    total = (dq + dq_full2, dk + dk2, dv + dv2)
+    if parts:
+        return total, (dq, dk, dv), (dq_full2, dk2, dv2)
+    return total
 
 
 # ---------------------------------------------------------------------------
