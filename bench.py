@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -77,6 +78,9 @@ def parse():
     p.add_argument("--decode-tokens", type=int, default=0,
                    help="with --model: also generate this many tokens after the prefill, with "
                         "dense and with delta decode, and report ms per decode token")
+    p.add_argument("--train", action="store_true",
+                   help="time delta_forward_train's forward and backward (the training "
+                        "path) at --seq/--gamma/--window/--sink instead of the prefill")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -466,6 +470,47 @@ def load_traffic(name):
         return None
 
 
+def train_step(a, q, k, v):
+    """delta_forward_train forward and backward on the workload's q/k/v with
+    a seeded N(0,1) upstream gradient: median ms of each over --steps after
+    --warmup, from HIP events on the current stream. Work: the forward's
+    algorithmic FLOPs (both attentions); the backward's counted as 2.5x
+    (five products per attended pair against two; the kernels recompute S
+    and dP, 3.5x in MFMA work)."""
+    import torch
+    from delta_attention.train.flex_delta import delta_forward_train
+    from oracle import delta_oracle as O
+    B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
+    g = torch.Generator(device=q.device).manual_seed(a.seed + 1)
+    up = torch.randn(B, S, H, D, device=q.device, generator=g).to(torch.bfloat16)
+    qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    f_fwd = (O.flops_sparse(B, H, D, S, a.window, a.sink)
+             + O.flops_qsparse(B, H, D, O.selected_rows(S, a.gamma)))
+    fw, bw = [], []
+    for i in range(a.warmup + a.steps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        qq.grad = kk.grad = vv.grad = None
+        e[0].record()
+        out = delta_forward_train(qq, kk, vv, a.gamma, a.window, a.sink, D ** -0.5)
+        e[1].record()
+        out.backward(up)
+        e[2].record()
+        torch.cuda.synchronize()
+        if i >= a.warmup:
+            fw.append(e[0].elapsed_time(e[1]))
+            bw.append(e[1].elapsed_time(e[2]))
+    fm, bm = statistics.median(fw), statistics.median(bw)
+    print(json.dumps({
+        "metric": "delta_forward_train forward + backward ms per layer",
+        "forward_ms": round(fm, 3), "backward_ms": round(bm, 3), "step_ms": round(fm + bm, 3),
+        "forward_tflops": round(f_fwd / (fm * 1e-3) / 1e12, 1),
+        "backward_tflops": round(2.5 * f_fwd / (bm * 1e-3) / 1e12, 1),
+        "flop_forward": f_fwd, "steps": a.steps, "warmup": a.warmup, "dtype": "bf16",
+        "config": {"workload": a.workload or "delta_forward_train layer", "batch": B, "heads": H,
+                   "kv_heads": Hkv, "seq_len": S, "head_dim": D, "gamma": a.gamma,
+                   "window": a.window, "sink": a.sink}}), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -499,6 +544,9 @@ def main():
 
     if a.gamma_sweep:
         gamma_sweep(a, q, k, v, [int(x) for x in a.gamma_sweep.split(",")])
+        return
+    if a.train:
+        train_step(a, q, k, v)
         return
 
     cut_n, s_p, n_anchor = ops.anchor_layout(S, a.gamma)

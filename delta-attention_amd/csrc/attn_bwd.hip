@@ -15,7 +15,9 @@
 // Two kernels per attention:
 //   * dq_kernel: one workgroup per 128 flattened (row, head) pairs (the G
 //     query heads of a KV head packed, as in the forward) and a chunk of their
-//     key-tile list; K and V tiles staged in LDS; S^T = K Q^T and dP^T = V dO^T
+//     key-tile list; K and V tiles arrive in LDS by buffer-load DMA through a
+//     three-stage ring (two tiles in flight), tiles wholly visible skip the
+//     per-key mask; S^T = K Q^T and dP^T = V dO^T
 //     with Q and dO fragments in registers, dQ^T += K^T dS^T from transposed
 //     LDS reads. It also writes rowsum(dO * O) for the other kernel. Long
 //     key lists (selected rows) are split; the splits' fp32 partial dQ are
@@ -40,8 +42,10 @@ namespace bwd {
 constexpr int NWAVE = 4;
 constexpr int NTHR = 64 * NWAVE;
 constexpr int BM = 32 * NWAVE;   // dq kernel: flattened (row, head) pairs per workgroup
-constexpr int BN = 64;           // dq kernel: keys per tile
-constexpr int NH = BN / 32;
+// dq kernel: keys per tile (32 at head_dim 128 keeps the score registers
+// small enough for two waves per SIMD; 64 otherwise)
+template <int D>
+constexpr int dq_bn() { return D == 128 ? 32 : 64; }
 constexpr int KT = 32 * NWAVE;   // dkdv kernel: keys per workgroup
 constexpr int RT = 32;           // dkdv kernel: rows per step
 constexpr int RPC_MAX = 4096;    // dkdv kernel: rows per chunk at most
@@ -83,6 +87,7 @@ struct BwdArgs {
 
 // Key tiles (BN keys) a row tile visits, in order: the sink tiles, then the
 // tiles from the one holding lo_min to the one holding hi_max.
+template <int BN>
 __device__ __forceinline__ void tile_list(int hi_max, int lo_min, int sink, int& n_first,
                                           int& second_t0, int& n_second) {
   int sink_end = min(min(sink, lo_min), hi_max + 1);
@@ -129,6 +134,19 @@ __device__ __forceinline__ int win_lo(int r, int q_block, int window) {
   return (r / q_block) * q_block + q_block - window;
 }
 
+// Wait until this wave's DMAs (and other vector memory operations) are done
+// (s_waitcnt vmcnt(0), gfx9 encoding; LDS and export counters not waited on).
+__device__ __forceinline__ void wait_dma() {
+  __builtin_amdgcn_s_waitcnt((0 & 15) | ((0 >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// ... until at most N vector memory operations are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+constexpr int NST = 3;   // LDS stages of the dq kernel's DMA ring
+
 template <typename T>
 __device__ __forceinline__ uint32_t acc_pack(uint32_t old, float lo, float hi, bool accumulate) {
   using E = Elt<T>;
@@ -138,16 +156,21 @@ __device__ __forceinline__ uint32_t acc_pack(uint32_t old, float lo, float hi, b
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool ROWS>
-__global__ __launch_bounds__(NTHR, 1) void dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(NTHR, 2) void dq_kernel(BwdArgs a) {
   using E = Elt<T>;
+  constexpr int BN = dq_bn<D>(), NH = BN / 32;
   constexpr int NDS = D / 16, NDT = D / 32, DCH = D / 8, RB = 2 * D;
   constexpr int TB = BN * RB;
-  constexpr int NLD = TB / (NTHR * 16);
+  constexpr int NLD = TB / (NTHR * 16);   // 16-byte DMA chunks per thread per K (or V) tile
   static_assert(NLD >= 1, "tile load");
-  __shared__ __attribute__((aligned(1024))) char smem[2][TB];
+  // [stage][K, V][tile]
+  __shared__ __attribute__((aligned(1024))) char smem[NST][2][TB];
   __shared__ int red[4][NWAVE];
   const size_t esz = sizeof(T);
 
+  // `wave` stays a vector value: a scalar one makes the compiler treat the
+  // DMA's LDS destination as aliasing the fragment reads and wait for every
+  // DMA right after issuing it; the loop orders DMA and reads itself
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 31, lg = lane >> 5;
   const int w = blockIdx.x;
@@ -225,7 +248,7 @@ __global__ __launch_bounds__(NTHR, 1) void dq_kernel(BwdArgs a) {
     lo_max = max(lo_max, red[3][i]);
   }
   int n_first, second_t0, n_second;
-  tile_list(hi_max, lo_min, sink, n_first, second_t0, n_second);
+  tile_list<BN>(hi_max, lo_min, sink, n_first, second_t0, n_second);
   int nt = n_first + n_second;
   const int t_off = split * a.chunk;
   nt = max(0, min(a.chunk, nt - t_off));
@@ -233,6 +256,37 @@ __global__ __launch_bounds__(NTHR, 1) void dq_kernel(BwdArgs a) {
   const char* kbase = (const char*)a.k + ((int64_t)b * a.ks_b + (int64_t)hk * a.ks_h) * esz;
   const char* vbase = (const char*)a.v + ((int64_t)b * a.vs_b + (int64_t)hk * a.vs_h) * esz;
   const float c2 = a.scale_log2;
+  // DMA of key tile t: lane chunk c fills LDS slot (c NWAVE + wave) 64 + lane,
+  // i.e. row slot / DCH, position slot % DCH, from the source chunk that
+  // position holds under the swizzle; keys past the last read as zero
+  const uint32_t krow_b = (uint32_t)(a.ks_s * (int64_t)esz);
+  const uint32_t vrow_b = (uint32_t)(a.vs_s * (int64_t)esz);
+  const uint64_t kend = (uint64_t)kbase + (uint64_t)(uint32_t)a.n_kv * krow_b;
+  const uint64_t vend = (uint64_t)vbase + (uint64_t)(uint32_t)a.n_kv * vrow_b;
+  uint32_t koff[NLD], voff[NLD];
+#pragma unroll
+  for (int c = 0; c < NLD; ++c) {
+    const int slot = (c * NWAVE + wave) * 64 + lane;
+    const int row = slot / DCH, pc = slot % DCH;
+    koff[c] = (uint32_t)row * krow_b + (uint32_t)((pc ^ swz<D>(row)) * 16);
+    voff[c] = (uint32_t)row * vrow_b + (uint32_t)((pc ^ swz<D>(row)) * 16);
+  }
+  auto tile_n0 = [&](int t) -> int {
+    const int u = t + t_off;
+    return (u < n_first ? u : second_t0 + (u - n_first)) * BN;
+  };
+  auto issue = [&](int t, int st) {
+    const int n0 = tile_n0(t);
+    const uint64_t pk = (uint64_t)kbase + (uint64_t)(uint32_t)n0 * krow_b;
+    const uint64_t pv = (uint64_t)vbase + (uint64_t)(uint32_t)n0 * vrow_b;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc((const void*)pk, ((kend - pk) >> 32) ? 0xffffffffu : (uint32_t)(kend - pk));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc((const void*)pv, ((vend - pv) >> 32) ? 0xffffffffu : (uint32_t)(vend - pv));
+#pragma unroll
+    for (int c = 0; c < NLD; ++c) {
+      dma16(rk, (DA_LDS void*)(&smem[st][0][(c * NWAVE + wave) * 1024]), koff[c]);
+      dma16(rv, (DA_LDS void*)(&smem[st][1][(c * NWAVE + wave) * 1024]), voff[c]);
+    }
+  };
 
   f32x16 acc[NDT];
 #pragma unroll
@@ -242,25 +296,21 @@ __global__ __launch_bounds__(NTHR, 1) void dq_kernel(BwdArgs a) {
   int tro[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) tro[dt] = tr_offset<D>(lane, dt);
-  const DA_LDS char* ks = (const DA_LDS char*)&smem[0][0];
-  const DA_LDS char* vs = (const DA_LDS char*)&smem[1][0];
-
-  for (int t = 0; t < nt; ++t) {
-    const int u = t + t_off;
-    const int n0 = (u < n_first ? u : second_t0 + (u - n_first)) * BN;
-    // stage K and V rows n0 .. n0 + BN - 1 (zero past the last key)
-#pragma unroll
-    for (int c = 0; c < NLD; ++c) {
-      const int slot = c * NTHR + tid;
-      const int row = slot / DCH, pc = slot % DCH;
-      const int key = n0 + row;
-      const bool in = key < a.n_kv;
-      const u32x4 kv = in ? *(const u32x4*)(kbase + (int64_t)key * a.ks_s * esz + pc * 16) : (u32x4){0, 0, 0, 0};
-      const u32x4 vv = in ? *(const u32x4*)(vbase + (int64_t)key * a.vs_s * esz + pc * 16) : (u32x4){0, 0, 0, 0};
-      *(DA_LDS u32x4*)((DA_LDS char*)&smem[0][0] + row * RB + ((pc ^ swz<D>(row)) * 16)) = kv;
-      *(DA_LDS u32x4*)((DA_LDS char*)&smem[1][0] + row * RB + ((pc ^ swz<D>(row)) * 16)) = vv;
-    }
+  // ring of NST stages: tiles t + 1 and t + 2 are in flight while tile t is
+  // consumed (the stage tile t + 2 lands in was last read in step t - 1,
+  // before its barrier); each issue is 2 NLD DMAs per lane
+  if (nt > 0) {
+    issue(0, 0);
+    if (nt > 1) issue(1, 1);
+    if (nt > 1) wait_vm<2 * NLD>();
+    else wait_dma();
     __syncthreads();
+  }
+  for (int t = 0; t < nt; ++t) {
+    const int n0 = tile_n0(t);
+    if (t + 2 < nt) issue(t + 2, (t + 2) % NST);
+    const DA_LDS char* ks = (const DA_LDS char*)&smem[t % NST][0][0];
+    const DA_LDS char* vs = (const DA_LDS char*)&smem[t % NST][1][0];
 
     // S^T = K Q^T and dP^T = V dO^T; element j of half hf is key
     // n0 + 32 hf + 16 (j / 8) + 8 lg + j % 8 (rows sigma(ln) of the A tiles)
@@ -280,6 +330,9 @@ __global__ __launch_bounds__(NTHR, 1) void dq_kernel(BwdArgs a) {
         x[hf] = E::mfma(read_rows<D>(ks, r, ds, lg), qf[ds], x[hf]);
         y[hf] = E::mfma(read_rows<D>(vs, r, ds, lg), df[ds], y[hf]);
       }
+    // every key of the tile visible to every valid row: no per-key test
+    const int n1 = n0 + BN - 1;
+    const bool full = n1 <= hi_min && n1 < a.n_kv && (n1 < sink || n0 >= lo_max);
     uint32_t dsp[8 * NH];
 #pragma unroll
     for (int hf = 0; hf < NH; ++hf)
@@ -290,7 +343,7 @@ __global__ __launch_bounds__(NTHR, 1) void dq_kernel(BwdArgs a) {
         for (int e = 0; e < 2; ++e) {
           const int jj = 2 * j + e;
           const int key = n0 + 32 * hf + 16 * (jj >> 3) + 8 * lg + (jj & 7);
-          const bool vis = key <= hi && (key < sink || key >= lo);
+          const bool vis = full || (key <= hi && (key < sink || key >= lo));
           const float p = vis ? fast_exp2(fmaf(x[hf][jj], c2, -lse)) : 0.f;
           d2[e] = p * (y[hf][jj] - Di);
         }
@@ -303,6 +356,9 @@ __global__ __launch_bounds__(NTHR, 1) void dq_kernel(BwdArgs a) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) acc[dt] = E::mfma(read_tr<D>(ks, tro[dt], kk), sf, acc[dt]);
     }
+    // tile t + 1 must have landed (tile t + 2 may still be in flight)
+    if (t + 2 < nt) wait_vm<2 * NLD>();
+    else wait_dma();
     __syncthreads();
   }
 
@@ -751,14 +807,18 @@ KvPlan plan_kv(int n_rows, int n_kv, int window, int sink, bool rows) {
   return p;
 }
 
+// Workspace: rowsum(dO * O) [B, Hq, n_rows] fp32; the dq split partials; the
+// dkdv partials.
 size_t bwd_ws_bytes(int B, int Hq, int Hkv, int n_rows, int n_kv, int D, const DqPlan& dq,
-                    const KvPlan& kv) {
+                    const KvPlan& kv, bool rows, size_t esz = 2) {
   size_t bytes = (size_t)B * Hq * n_rows * sizeof(float);        // rowsum(dO * O)
   bytes = (bytes + 255) / 256 * 256;
   if (dq.n_splits > 1)
     bytes += (size_t)B * Hkv * dq.n_splits * dq.n_mtiles * BM * D * sizeof(float);
   bytes = (bytes + 255) / 256 * 256;
   bytes += (size_t)B * Hkv * kv.items_per_bh * 2 * KT * D * sizeof(float);
+  (void)rows;
+  (void)esz;
   return bytes;
 }
 
@@ -815,6 +875,10 @@ int bwd_args(BwdArgs& a, const void* q, const void* k, const void* v, const void
   for (const void* p : ps)
     if (!aligned16(p)) return DA_ERR_ALIGNMENT;
   if (((uintptr_t)lse & 3u) != 0) return DA_ERR_ALIGNMENT;
+  // the DMA tiles address rows with 32-bit byte offsets
+  const int64_t rs[] = {q_str[2], k_str[2], v_str[2], do_str[2]};
+  for (int64_t r : rs)
+    if (r < D || r >= (1 << 23)) return DA_ERR_INVALID_ARG;
   a = BwdArgs{};
   a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.lse = lse;
   a.dq = dq; a.dk = dk; a.dv = dv;
@@ -843,19 +907,21 @@ extern "C" size_t da_sparse_attn_bwd_workspace_bytes(int B, int Hq, int Hkv, int
     return 0;
   const DqPlan dq = plan_dq(B, Hkv, Hq / Hkv, S, 0, false);
   const KvPlan kv = plan_kv(S, S, window, sink, false);
-  return bwd_ws_bytes(B, Hq, Hkv, S, S, D, dq, kv);
+  return bwd_ws_bytes(B, Hq, Hkv, S, S, D, dq, kv, false);
 }
 
 extern "C" size_t da_qsparse_attn_bwd_workspace_bytes(int B, int Hq, int Hkv, int n, int Skv, int D) {
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n < 1 || Skv < 1 ||
       (D != 32 && D != 64 && D != 128))
     return 0;
-  const DqPlan dq = plan_dq(B, Hkv, Hq / Hkv, n, ((int64_t)Skv + BN - 1) / BN, true);
+  const int bn = D == 128 ? 32 : 64;
+  const DqPlan dq = plan_dq(B, Hkv, Hq / Hkv, n, ((int64_t)Skv + bn - 1) / bn, true);
   const KvPlan kv = plan_kv(n, Skv, 0, 0, true);
-  return bwd_ws_bytes(B, Hq, Hkv, n, Skv, D, dq, kv);
+  return bwd_ws_bytes(B, Hq, Hkv, n, Skv, D, dq, kv, true);
 }
 
-static void place_workspace(BwdArgs& a, const DqPlan& dq, const KvPlan& kv, int D, void* ws) {
+static void place_workspace(BwdArgs& a, const DqPlan& dq, const KvPlan& kv, int D, void* ws,
+                            bool rows) {
   a.n_mtiles = dq.n_mtiles; a.n_splits = dq.n_splits; a.chunk = dq.chunk;
   a.n_blk = kv.n_blk; a.nsb = kv.nsb; a.ncs = kv.ncs; a.nco = kv.nco; a.rpc = kv.rpc;
   a.items_per_bh = kv.items_per_bh;
@@ -867,6 +933,7 @@ static void place_workspace(BwdArgs& a, const DqPlan& dq, const KvPlan& kv, int 
   if (dq.n_splits > 1) off += (size_t)a.B * a.Hkv * dq.n_splits * dq.n_mtiles * BM * D * sizeof(float);
   off = (off + 255) / 256 * 256;
   a.kv_part = (float*)(p + off);
+  (void)rows;
 }
 
 extern "C" int da_sparse_attn_bwd(const void* q, const void* k, const void* v, const void* o,
@@ -888,13 +955,13 @@ extern "C" int da_sparse_attn_bwd(const void* q, const void* k, const void* v, c
   a.window = window; a.sink = sink; a.q_block = q_block;
   const DqPlan dqp = plan_dq(B, Hkv, a.G, S, 0, false);
   const KvPlan kvp = plan_kv(S, S, window, sink, false);
-  const size_t need = bwd_ws_bytes(B, Hq, Hkv, S, S, D, dqp, kvp);
+  const size_t need = bwd_ws_bytes(B, Hq, Hkv, S, S, D, dqp, kvp, false);
   if (!workspace || workspace_bytes < need) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
   if ((int64_t)B * Hkv * kvp.items_per_bh > 0x7fffff00LL ||
       (int64_t)B * Hkv * dqp.n_mtiles * dqp.n_splits > 0x7fffff00LL)
     return DA_ERR_INVALID_ARG;
-  place_workspace(a, dqp, kvp, D, workspace);
+  place_workspace(a, dqp, kvp, D, workspace, false);
   return dispatch_bwd<false>(a, D, dtype, (hipStream_t)stream);
 }
 
@@ -917,15 +984,16 @@ extern "C" int da_qsparse_attn_bwd(const void* q, const void* k, const void* v, 
   if (rc != DA_OK) return rc;
   a.q_rows = q_rows; a.row_last = row_last;
   a.window = 0; a.sink = 0; a.q_block = 1;
-  const DqPlan dqp = plan_dq(B, Hkv, a.G, n, ((int64_t)Skv + BN - 1) / BN, true);
+  const int bn = D == 128 ? 32 : 64;
+  const DqPlan dqp = plan_dq(B, Hkv, a.G, n, ((int64_t)Skv + bn - 1) / bn, true);
   const KvPlan kvp = plan_kv(n, Skv, 0, 0, true);
-  const size_t need = bwd_ws_bytes(B, Hq, Hkv, n, Skv, D, dqp, kvp);
+  const size_t need = bwd_ws_bytes(B, Hq, Hkv, n, Skv, D, dqp, kvp, true);
   if (!workspace || workspace_bytes < need) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
   if ((int64_t)B * Hkv * kvp.items_per_bh > 0x7fffff00LL ||
       (int64_t)B * Hkv * dqp.n_mtiles * dqp.n_splits > 0x7fffff00LL)
     return DA_ERR_INVALID_ARG;
-  place_workspace(a, dqp, kvp, D, workspace);
+  place_workspace(a, dqp, kvp, D, workspace, true);
   return dispatch_bwd<true>(a, D, dtype, (hipStream_t)stream);
 }
 
