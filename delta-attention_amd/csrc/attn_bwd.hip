@@ -434,8 +434,11 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
   using E = Elt<T>;
   constexpr int NDS = D / 16, NDT = D / 32, DCH = D / 8, RB = 2 * D;
   constexpr int TB = RT * RB;
-  __shared__ __attribute__((aligned(1024))) char smem[2][TB];   // Q, dO
-  __shared__ __attribute__((aligned(16))) float s_lse[RT], s_d[RT];
+  // Q and dO rows of up to HGM query heads per step: one load round trip and
+  // one barrier pair serve HGM heads' products
+  constexpr int HGM = 4;
+  __shared__ __attribute__((aligned(1024))) char smem[2][HGM][TB];   // Q, dO
+  __shared__ __attribute__((aligned(16))) float s_lse[HGM][RT], s_d[HGM][RT];
   __shared__ __attribute__((aligned(16))) int s_lim[RT], s_lo[RT];
   const size_t esz = sizeof(T);
 
@@ -507,17 +510,18 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
   int tro[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) tro[dt] = tr_offset<D>(lane, dt);
-  const DA_LDS char* qs = (const DA_LDS char*)&smem[0][0];
-  const DA_LDS char* gs = (const DA_LDS char*)&smem[1][0];
   const float c2 = a.scale_log2;
   const int sink = ROWS ? 0 : a.sink;
 
   for (int r0 = c_start; r0 <= c_end; r0 += RT) {
-    for (int g = 0; g < a.G; ++g) {
-      const int h = hk * a.G + g;
-      // stage Q and dO rows of list positions r0 .. r0 + RT - 1 of head h
-      for (int slot = tid; slot < RT * DCH; slot += NTHR) {
-        const int rr = slot / DCH, pc = slot % DCH;
+    for (int g0 = 0; g0 < a.G; g0 += HGM) {
+      const int hg = min(HGM, a.G - g0);
+      // stage Q and dO rows of list positions r0 .. r0 + RT - 1 of heads
+      // g0 .. g0 + hg - 1 (zero past the chunk end)
+      for (int slot = tid; slot < hg * RT * DCH; slot += NTHR) {
+        const int gg = slot / (RT * DCH), rem = slot % (RT * DCH);
+        const int rr = rem / DCH, pc = rem % DCH;
+        const int h = hk * a.G + g0 + gg;
         const int i = r0 + rr;
         const bool ok = i <= c_end;
         u32x4 qv = {0, 0, 0, 0}, gv = {0, 0, 0, 0};
@@ -526,29 +530,35 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
           qv = *(const u32x4*)((const char*)a.q + ((int64_t)b * a.qs_b + (int64_t)h * a.qs_h + (int64_t)qrow * a.qs_s) * esz + pc * 16);
           gv = *(const u32x4*)((const char*)a.dout + ((int64_t)b * a.gs_b + (int64_t)h * a.gs_h + (int64_t)i * a.gs_s) * esz + pc * 16);
         }
-        *(DA_LDS u32x4*)((DA_LDS char*)&smem[0][0] + rr * RB + ((pc ^ swz<D>(rr)) * 16)) = qv;
-        *(DA_LDS u32x4*)((DA_LDS char*)&smem[1][0] + rr * RB + ((pc ^ swz<D>(rr)) * 16)) = gv;
+        *(DA_LDS u32x4*)((DA_LDS char*)&smem[0][gg][0] + rr * RB + ((pc ^ swz<D>(rr)) * 16)) = qv;
+        *(DA_LDS u32x4*)((DA_LDS char*)&smem[1][gg][0] + rr * RB + ((pc ^ swz<D>(rr)) * 16)) = gv;
       }
-      if (tid < RT) {
-        const int i = r0 + tid;
+      if (tid < hg * RT) {
+        const int gg = tid / RT, t = tid % RT;
+        const int i = r0 + t;
         const bool ok = i <= c_end;
-        const int64_t rix = ((int64_t)b * a.Hq + h) * a.n_rows + i;
-        s_lse[tid] = ok ? a.lse[rix] : INFINITY;
-        s_d[tid] = ok ? a.dvec[rix] : 0.f;
-        int lim = -1, lo = 0;
-        if (ok) {
-          if (ROWS) {
-            const int64_t l = min(a.row_last[i], (int64_t)(a.n_kv - 1));
-            lim = (int)(l < -1 ? -1 : l);
-          } else {
-            lim = i;
-            lo = win_lo(i, a.q_block, a.window);
+        const int64_t rix = ((int64_t)b * a.Hq + hk * a.G + g0 + gg) * a.n_rows + i;
+        s_lse[gg][t] = ok ? a.lse[rix] : INFINITY;
+        s_d[gg][t] = ok ? a.dvec[rix] : 0.f;
+        if (gg == 0) {
+          int lim = -1, lo = 0;
+          if (ok) {
+            if (ROWS) {
+              const int64_t l = min(a.row_last[i], (int64_t)(a.n_kv - 1));
+              lim = (int)(l < -1 ? -1 : l);
+            } else {
+              lim = i;
+              lo = win_lo(i, a.q_block, a.window);
+            }
           }
+          s_lim[t] = lim;
+          s_lo[t] = lo;
         }
-        s_lim[tid] = lim;
-        s_lo[tid] = lo;
       }
       __syncthreads();
+      for (int gg = 0; gg < hg; ++gg) {
+      const DA_LDS char* qs = (const DA_LDS char*)&smem[0][gg][0];
+      const DA_LDS char* gs = (const DA_LDS char*)&smem[1][gg][0];
 
       // S = Q K^T and dP = dO V^T (rows x keys); element e of this lane is
       // row 16 (e / 8) + 8 lg + e % 8 of the step, key `key`
@@ -568,8 +578,8 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int rb = 16 * half + 8 * lg;
-        const f32x4 l0 = *(const DA_LDS f32x4*)&s_lse[rb], l1 = *(const DA_LDS f32x4*)&s_lse[rb + 4];
-        const f32x4 d0 = *(const DA_LDS f32x4*)&s_d[rb], d1 = *(const DA_LDS f32x4*)&s_d[rb + 4];
+        const f32x4 l0 = *(const DA_LDS f32x4*)&s_lse[gg][rb], l1 = *(const DA_LDS f32x4*)&s_lse[gg][rb + 4];
+        const f32x4 d0 = *(const DA_LDS f32x4*)&s_d[gg][rb], d1 = *(const DA_LDS f32x4*)&s_d[gg][rb + 4];
         const u32x4 m0 = *(const DA_LDS u32x4*)&s_lim[rb], m1 = *(const DA_LDS u32x4*)&s_lim[rb + 4];
         const u32x4 o0 = *(const DA_LDS u32x4*)&s_lo[rb], o1 = *(const DA_LDS u32x4*)&s_lo[rb + 4];
         float pv[8], dv[8];
@@ -602,6 +612,7 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
           adk[dt] = E::mfma(read_tr<D>(qs, tro[dt], kk), sf, adk[dt]);
         }
       }
+      }   // heads of the step
       __syncthreads();
     }
   }
