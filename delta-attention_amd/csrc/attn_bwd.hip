@@ -556,6 +556,12 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
         }
       }
       __syncthreads();
+      // this wave's 32 keys visible to every row of the step (wave-uniform):
+      // the per-key test is skipped
+      const int kw = k0 + wave * 32;
+      const bool full = r0 + RT - 1 <= c_end &&
+                        (ROWS ? kw + 31 <= s_lim[0]
+                              : kw + 31 <= r0 && (kw + 31 < sink || kw >= s_lo[RT - 1]));
       for (int gg = 0; gg < hg; ++gg) {
       const DA_LDS char* qs = (const DA_LDS char*)&smem[0][gg][0];
       const DA_LDS char* gs = (const DA_LDS char*)&smem[1][gg][0];
@@ -589,7 +595,7 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
           const float de = e < 4 ? d0[e] : d1[e - 4];
           const int lim = (int)(e < 4 ? m0[e] : m1[e - 4]);
           const int lo = (int)(e < 4 ? o0[e] : o1[e - 4]);
-          const bool vis = key <= lim && (key < sink || key >= lo);
+          const bool vis = full || (key <= lim && (key < sink || key >= lo));
           const int jj = 8 * half + e;
           const float p = vis ? fast_exp2(fmaf(x[jj], c2, -le)) : 0.f;
           pv[e] = p;
