@@ -407,7 +407,7 @@ def delta_train_grads(q: np.ndarray, k: np.ndarray, v: np.ndarray, gamma: int, w
 
 
 # ---------------------------------------------------------------------------
-# input generation helpers (the BASELINE workloads' prologue)
+# input generation helpers (the benchmark workloads' prologue)
 
 def rope_cos_sin(s: int, d: int, theta: float) -> Tuple[np.ndarray, np.ndarray]:
     """Default-rope cos/sin tables [s, d] (llama.py:129-158: inv_freq =
