@@ -248,3 +248,68 @@ def test_split_plans_refuse_grid_overflow(lib):
     # a selected-rows launch whose work items would not fit a 32-bit grid
     assert lib.da_qsparse_workspace_bytes(1, 32, 8, 2_000_000_000, 131072, 128) == 0
     assert lib.da_qsparse_workspace_bytes(1, 32, 8, 2174, 131072, 128) > 0
+
+
+def test_training_entry_checks(lib):
+    """The training-path entries: workspace sizes, and every refusal happens
+    before a launch (null pointers, head_dim, dtype, row alignment, lse
+    alignment, workspace, composition stride rules)."""
+    P = ctypes.c_void_p
+    B, H, Hkv, S, D = 1, 8, 2, 1024, 128
+    q3 = _s3(H * S * D, S * D, D)
+    k3 = _s3(Hkv * S * D, S * D, D)
+    o3 = _s3(S * H * D, D, H * D)
+    need = lib.da_sparse_attn_bwd_workspace_bytes(B, H, Hkv, S, D, 256, 16, 64)
+    assert need > 0
+    assert lib.da_sparse_attn_bwd_workspace_bytes(B, H, 3, S, D, 256, 16, 64) == 0   # H % Hkv
+    assert lib.da_sparse_attn_bwd_workspace_bytes(B, H, Hkv, S, 80, 256, 16, 64) == 0
+    # sink blocks are cut into row chunks: more sinks, more partial slots
+    assert lib.da_sparse_attn_bwd_workspace_bytes(B, H, Hkv, S, D, 256, 512, 64) > need
+    nr = lib.da_qsparse_attn_bwd_workspace_bytes(B, H, Hkv, 200, S, D)
+    assert nr > 0 and lib.da_qsparse_attn_bwd_workspace_bytes(B, H, Hkv, 0, S, D) == 0
+
+    def sparse(q=16, lse=16, D=D, dtype=L.DA_BF16, ws=16, nbytes=None, q_block=64, k_row=None):
+        kk = k3 if k_row is None else _s3(Hkv * S * D, S * D, k_row)
+        return lib.da_sparse_attn_bwd(P(q) if q else None, P(16), P(16), P(16), P(16),
+                                      P(lse) if lse else None, P(16), P(16), P(16),
+                                      B, H, Hkv, S, D, q3, kk, kk, o3, o3, q3, k3, k3,
+                                      256, 16, q_block, 0.1, 0, P(ws) if ws else None,
+                                      need if nbytes is None else nbytes, dtype, None)
+    assert sparse(q=0) == L.DA_ERR_INVALID_ARG
+    assert sparse(lse=0) == L.DA_ERR_INVALID_ARG
+    assert sparse(lse=18) == L.DA_ERR_ALIGNMENT
+    assert sparse(q=24) == L.DA_ERR_ALIGNMENT
+    assert sparse(D=80) == L.DA_ERR_HEAD_DIM
+    assert sparse(dtype=7) == L.DA_ERR_DTYPE
+    assert sparse(q_block=0) == L.DA_ERR_INVALID_ARG
+    assert sparse(k_row=1 << 23) == L.DA_ERR_INVALID_ARG     # row offsets beyond 32 bits
+    assert sparse(ws=0) == L.DA_ERR_WORKSPACE
+    assert sparse(nbytes=need - 1) == L.DA_ERR_WORKSPACE
+
+    def rows(rl=16, n=200, nbytes=None):
+        return lib.da_qsparse_attn_bwd(P(16), P(16), P(16), P(16), P(16), P(16),
+                                       P(16), P(rl) if rl else None, n, P(16), P(16), P(16),
+                                       B, H, Hkv, S, S, D, q3, k3, k3, o3, o3, q3, k3, k3,
+                                       0.1, 1, P(16), nr if nbytes is None else nbytes,
+                                       L.DA_BF16, None)
+    assert rows(rl=0) == L.DA_ERR_INVALID_ARG
+    assert rows(n=0) == L.DA_ERR_INVALID_ARG
+    assert rows(nbytes=nr - 1) == L.DA_ERR_WORKSPACE
+
+    def compose(gamma=64, s_p=896, D=D, g=16):
+        return lib.da_delta_compose_bwd(P(g), o3, P(16), o3, P(16), o3, B, H, S, D, gamma, s_p,
+                                        1.0, 0, L.DA_BF16, None)
+    assert compose(s_p=900) == L.DA_ERR_INVALID_ARG        # s_p % gamma
+    assert compose(s_p=S + 64) == L.DA_ERR_INVALID_ARG
+    assert compose(gamma=0) == L.DA_ERR_INVALID_ARG
+    assert compose(D=48) == L.DA_ERR_HEAD_DIM
+    assert compose(g=8) == L.DA_ERR_ALIGNMENT
+
+    # forward with row statistics: lse required and 4-byte aligned
+    f = lib.da_sparse_attn_fwd_lse(P(16), P(16), P(16), P(16), B, H, Hkv, S, D, q3, k3, k3, o3,
+                                   256, 16, 64, 0.1, None, L.DA_BF16, None)
+    assert f == L.DA_ERR_INVALID_ARG
+    f = lib.da_qsparse_attn_fwd_lse(P(16), P(16), P(16), P(16), P(16), 0, 10, B, H, Hkv, S, S, D,
+                                    q3, k3, k3, P(16), q3, P(18), 0.1, P(16), 1 << 30,
+                                    L.DA_BF16, None)
+    assert f == L.DA_ERR_ALIGNMENT
