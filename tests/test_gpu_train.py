@@ -115,3 +115,30 @@ def test_backward_is_deterministic(gpu):
     torch.cuda.synchronize()
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+def test_full_size_properties(gpu):
+    """Llama-3.1-8B layer at 32K tokens (32/8 heads, head_dim 128, window 2048
+    + 128 sinks, gamma 64): the training forward equals the inference layer
+    bit for bit, and the backward is linear in the upstream gradient exactly
+    for a power-of-two scale (every fp32 product and bf16 rounding scales by
+    2 without error), over every row."""
+    from delta_attention import ops
+    from delta_attention.train.flex_delta import delta_forward_train
+    B, H, Hkv, S, D = 1, 32, 8, 32768, 128
+    print("full-size training properties: Llama 32K", flush=True)
+    q, k, v, up = _inputs(B, H, Hkv, S, D, seed=77)
+    q, k = q * D ** -0.25, k * D ** -0.25         # moderate logits, as after RoPE'd projections
+    scale = D ** -0.5
+    grads = []
+    for mult in (1.0, 2.0):
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        out = delta_forward_train(qq, kk, vv, 64, 2048, 128, scale)
+        out.backward(up * mult)
+        grads.append((out.detach(), qq.grad, kk.grad, vv.grad))
+    torch.cuda.synchronize()
+    ref = ops.delta_prefill(q, k, v, gamma=64, window=2048, sink=128, sm_scale=scale, fused=False)
+    assert torch.equal(grads[0][0], ref)
+    for a, b in zip(grads[0][1:], grads[1][1:]):
+        assert torch.isfinite(a).all()
+        assert torch.equal(a * 2, b)
