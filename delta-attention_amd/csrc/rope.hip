@@ -37,7 +37,18 @@ struct RopeArgs {
   int64_t cs_b, cs_s;
   float eps;
   int B, S, D;
-  int64_t rows;            // q.rows + k.rows
+  int64_t rows;            // q.rows + k.rows + v_rows
+  // one-token KV-cache append (S == 1): k rows are written to kc at cache
+  // row *pos instead of in place, and rows [q.rows + k.rows, rows) copy v
+  // into vc at the same row
+  const int64_t* pos;
+  void* kc;
+  int64_t kc_b, kc_s, kc_h;
+  const void* v;
+  int64_t v_b, v_s, v_h;
+  void* vc;
+  int64_t vc_b, vc_s, vc_h;
+  int64_t v_rows;
 };
 
 template <typename T, int D, bool NT>
@@ -50,6 +61,24 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int64_t gtid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = gtid / TPR;
   const int part = (int)(gtid % TPR);
+  constexpr size_t esz = sizeof(T);
+  if (a.v_rows > 0 && row >= a.q.rows + a.k.rows) {
+    // cache append of v: this thread's 2 x EPT elements, no arithmetic
+    if (row >= a.rows) return;
+    const int64_t vr = row - a.q.rows - a.k.rows;
+    const int hv = (int)(vr % a.k.H), bv = (int)(vr / a.k.H);   // S == 1
+    const char* src = (const char*)a.v + ((int64_t)bv * a.v_b + (int64_t)hv * a.v_h) * esz;
+    char* dst = (char*)a.vc + ((int64_t)bv * a.vc_b + *a.pos * a.vc_s + (int64_t)hv * a.vc_h) * esz;
+    const int j0 = part * EPT;
+    if constexpr (EPT == 8) {
+      *(u32x4*)(dst + j0 * esz) = *(const u32x4*)(src + j0 * esz);
+      *(u32x4*)(dst + (HALF + j0) * esz) = *(const u32x4*)(src + (HALF + j0) * esz);
+    } else {
+      *(u32x2*)(dst + j0 * esz) = *(const u32x2*)(src + j0 * esz);
+      *(u32x2*)(dst + (HALF + j0) * esz) = *(const u32x2*)(src + (HALF + j0) * esz);
+    }
+    return;
+  }
   const bool live = row < a.rows;
   const bool kpart = live && row >= a.q.rows;
   const int64_t rr = live ? (kpart ? row - a.q.rows : row) : 0;
@@ -65,7 +94,6 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int64_t bs = rr / H;
   const int s = (int)(bs % a.S);
   const int b = (int)(bs / a.S);
-  constexpr size_t esz = sizeof(T);
   char* xp = xbase + ((int64_t)b * xs_b + (int64_t)s * xs_s + (int64_t)h * xs_h) * esz;
   const int i0 = part * EPT;          // first element of this thread in the low half
 
@@ -130,6 +158,8 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     ohi[e / 2] = E::pack2(E::lo(b1) + E::lo(b2), E::hi(b1) + E::hi(b2));
   }
   if (!live) return;
+  if (kpart && a.kc)   // rotated k goes to its cache row
+    xp = (char*)a.kc + ((int64_t)b * a.kc_b + *a.pos * a.kc_s + (int64_t)h * a.kc_h) * esz;
   if constexpr (EPT == 8) {
     const u32x4 vl = {olo[0], olo[1], olo[2], olo[3]}, vh = {ohi[0], ohi[1], ohi[2], ohi[3]};
     if constexpr (NT) {
@@ -207,5 +237,43 @@ extern "C" int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
   (void)hipGetLastError();
   if (dtype == DA_BF16) launch_rope<__bf16>(a, s);
   else launch_rope<_Float16>(a, s);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}
+
+extern "C" int da_rope_qk_append(void* q, const int64_t q_str[3], int Hq,
+                                 const void* k, const int64_t k_str[3], int Hkv,
+                                 const void* v, const int64_t v_str[3],
+                                 int B, int D,
+                                 const void* cos, const void* sin, const int64_t cs_str[2],
+                                 const void* q_norm_w, const void* k_norm_w, float eps,
+                                 void* k_cache, const int64_t kc_str[3],
+                                 void* v_cache, const int64_t vc_str[3],
+                                 const int64_t* pos, int dtype, void* stream) {
+  if (dtype != DA_BF16 && dtype != DA_FP16) return DA_ERR_DTYPE;
+  if (D != 64 && D != 128) return DA_ERR_HEAD_DIM;
+  if (B < 1 || Hq < 1 || Hkv < 1) return DA_ERR_INVALID_ARG;
+  if (!q || !k || !v || !k_cache || !v_cache || !pos || !v_str || !kc_str || !vc_str)
+    return DA_ERR_INVALID_ARG;
+  if (!cos || !sin || !cs_str || cs_str[0] < 0 || cs_str[1] < D) return DA_ERR_INVALID_ARG;
+  if (!aligned16(cos) || !aligned16(sin) || cs_str[0] % 8 || cs_str[1] % 8) return DA_ERR_ALIGNMENT;
+  if (!aligned16(v) || !aligned16(k_cache) || !aligned16(v_cache) || !strides8(v_str) ||
+      !strides8(kc_str) || !strides8(vc_str) || ((uintptr_t)pos & 7u))
+    return DA_ERR_ALIGNMENT;
+  RopeArgs a = {};
+  int rc;
+  if ((rc = rope_part(a.q, q, q_str, Hq, B, 1, q_norm_w)) != DA_OK) return rc;
+  if ((rc = rope_part(a.k, const_cast<void*>(k), k_str, Hkv, B, 1, k_norm_w)) != DA_OK) return rc;
+  a.cos = cos; a.sin = sin; a.cs_b = cs_str[0]; a.cs_s = cs_str[1];
+  a.eps = eps; a.B = B; a.S = 1; a.D = D;
+  a.pos = pos;
+  a.kc = k_cache; a.kc_b = kc_str[0]; a.kc_s = kc_str[1]; a.kc_h = kc_str[2];
+  a.v = v; a.v_b = v_str[0]; a.v_s = v_str[1]; a.v_h = v_str[2];
+  a.vc = v_cache; a.vc_b = vc_str[0]; a.vc_s = vc_str[1]; a.vc_h = vc_str[2];
+  a.v_rows = (int64_t)B * Hkv;
+  a.rows = a.q.rows + a.k.rows + a.v_rows;
+  hipStream_t s = (hipStream_t)stream;
+  (void)hipGetLastError();
+  if (dtype == DA_BF16) launch_rope_nt<__bf16, false>(a, s);
+  else launch_rope_nt<_Float16, false>(a, s);
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }

@@ -50,6 +50,7 @@ EXPORTS = (
     "da_sparse_attn_bwd",
     "da_qsparse_attn_bwd",
     "da_delta_compose_bwd",
+    "da_rope_qk_append",
     "da_build_target",
 )
 
@@ -165,6 +166,9 @@ def _load() -> ctypes.CDLL:
     L.da_delta_compose_bwd.restype = _i
     L.da_delta_compose_bwd.argtypes = [_vp, _p3, _vp, _p3, _vp, _p3, _i, _i, _i, _i, _i, _i,
                                        _f, _i, _i, _vp]
+    L.da_rope_qk_append.restype = _i
+    L.da_rope_qk_append.argtypes = [_vp, _p3, _i, _vp, _p3, _i, _vp, _p3, _i, _i, _vp, _vp,
+                                    _vp, _vp, _vp, _f, _vp, _p3, _vp, _p3, _vp, _i, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
     return L

@@ -458,10 +458,13 @@ class LlamaAttention(nn.Module):
         """(q_norm weight, k_norm weight, eps) applied before RoPE, or Nones."""
         return None, None, 1e-6
 
-    def _qkv_rope(self, hidden_states, hidden_shape, cos, sin, timer=None):
+    def _qkv_rope(self, hidden_states, hidden_shape, cos, sin, timer=None, append=None):
         """Projections, then the fused prologue kernel (optional per-head q/k
         RMSNorm + RoPE) in place on the [b, s, h, d] projection outputs; returns
-        [b, h, s, d] views, the layout the attention kernels read without copies."""
+        [b, h, s, d] views, the layout the attention kernels read without copies.
+        append: a cache in static (one-token, device-held row) mode; the same
+        launch then writes the rotated k and v into it and (q, None, None) is
+        returned."""
         if hidden_states.dtype not in (torch.bfloat16, torch.float16):
             # float32 models keep the reference's float32 RoPE (torch ops); the
             # attention kernels then run in bf16 as delta_forward casts
@@ -483,6 +486,11 @@ class LlamaAttention(nn.Module):
                 v = qkv[..., nq + nk:].unflatten(-1, (-1, self.head_dim))
         with region(timer, "rope_prologue"):
             qw, kw, eps = self._qk_norm()
+            if append is not None:
+                ops.rope_qk_append(q, k, v, cos, sin, append.k[self.layer_idx],
+                                   append.v[self.layer_idx], append.pos, q_norm_w=qw,
+                                   k_norm_w=kw, eps=eps)
+                return q.transpose(1, 2), None, None
             ops.rope_qk(q, k, cos, sin, q_norm_w=qw, k_norm_w=kw, eps=eps)
         return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
 
@@ -494,13 +502,18 @@ class LlamaAttention(nn.Module):
         hidden_shape = (*input_shape, -1, self.head_dim)
         cos, sin = position_embeddings
         timer = kwargs.get("timer")
-        query_states, key_states, value_states = self._qkv_rope(hidden_states, hidden_shape, cos, sin,
-                                                                timer)
+        static = (past_key_value is not None and getattr(past_key_value, "static", False)
+                  and hidden_states.dtype in (torch.bfloat16, torch.float16))
+        query_states, key_states, value_states = self._qkv_rope(
+            hidden_states, hidden_shape, cos, sin, timer, append=past_key_value if static else None)
         extra = {}
         if past_key_value is not None:
-            key_states, value_states = past_key_value.update(
-                key_states, value_states, self.layer_idx,
-                {"sin": sin, "cos": cos, "cache_position": cache_position})
+            if key_states is None:   # appended by the prologue launch
+                key_states, value_states = past_key_value.views(self.layer_idx)
+            else:
+                key_states, value_states = past_key_value.update(
+                    key_states, value_states, self.layer_idx,
+                    {"sin": sin, "cos": cos, "cache_position": cache_position})
             if getattr(past_key_value, "static", False):
                 # recorded decode step: full cache buffers, key count on the device
                 extra = {"n_keys": past_key_value.n_keys,

@@ -99,6 +99,12 @@ class KVCache:
         self.len = [l + n_appended for l in self.len]
         self.static, self.pos, self.n_keys, self.anchor = False, None, None, False
 
+    def views(self, layer_idx: int):
+        """Static mode: [B, Hkv, max_len, D] views of a layer's full buffers
+        (the decode rows read the device-held key count of them)."""
+        assert self.static
+        return self.k[layer_idx].transpose(1, 2), self.v[layer_idx].transpose(1, 2)
+
     def update(self, key_states, value_states, layer_idx: int, cache_kwargs=None):
         s = key_states.shape[2]
         if self.static:

@@ -386,6 +386,36 @@ def delta_compose_bwd(grad: torch.Tensor, *, gamma: int, s_p: int, delta_grad_sc
 # ---------------------------------------------------------------------------
 # attention prologue: per-head RMSNorm (optional) + RoPE, in place
 
+def rope_qk_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                   sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                   pos: torch.Tensor, *, q_norm_w: Optional[torch.Tensor] = None,
+                   k_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6) -> None:
+    """One-token decode step: rope_qk on q (in place) and k, with the rotated k
+    and v written to the [B, max_len, Hkv, D] caches at row pos (int64 [1] on
+    the device) instead of a separate cache update. q/k/v [B, 1, H, D]."""
+    B, S, Hq, D = q.shape
+    Hkv = k.shape[2]
+    assert S == 1 and k.shape == (B, 1, Hkv, D) and v.shape == k.shape
+    assert k_cache.shape[0] == B and k_cache.shape[2:] == (Hkv, D) and v_cache.shape == k_cache.shape
+    dev = _on_gpu(q, k, v, k_cache, v_cache, pos)
+    assert pos.dtype == torch.int64 and pos.numel() == 1
+    cos = cos.to(device=dev, dtype=q.dtype)
+    sin = sin.to(device=dev, dtype=q.dtype)
+    if cos.dim() == 2:
+        cos, sin = cos.unsqueeze(0), sin.unsqueeze(0)
+    assert cos.shape[1:] == (1, D) and cos.shape[0] in (1, B)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    ws = [None if w is None else w.to(device=dev, dtype=q.dtype).contiguous() for w in (q_norm_w, k_norm_w)]
+    cs = (ctypes.c_int64 * 2)(0 if cos.shape[0] == 1 else cos.stride(0), cos.stride(1))
+    with torch.cuda.device(dev):
+        rc = L.lib().da_rope_qk_append(
+            _ptr(q), _s3(q, 0, 1, 2), Hq, _ptr(k), _s3(k, 0, 1, 2), Hkv, _ptr(v), _s3(v, 0, 1, 2),
+            B, D, _ptr(cos), _ptr(sin), cs, _ptr(ws[0]), _ptr(ws[1]), float(eps),
+            _ptr(k_cache), _s3(k_cache, 0, 1, 2), _ptr(v_cache), _s3(v_cache, 0, 1, 2),
+            _ptr(pos), _code(q), _stream(dev))
+    L.check(rc, "da_rope_qk_append")
+
+
 def rope_qk(q: Optional[torch.Tensor], k: Optional[torch.Tensor], cos: torch.Tensor,
             sin: torch.Tensor, *, q_norm_w: Optional[torch.Tensor] = None,
             k_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6):

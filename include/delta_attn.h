@@ -253,6 +253,27 @@ int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
                const void* q_norm_w, const void* k_norm_w, float eps,
                int dtype, void* stream);
 
+/*
+ * One-token decode step variant (S == 1) of da_rope_qk that also appends to
+ * the KV cache, replacing the cache update that follows RoPE in a decode step
+ * (the reference's DynamicCache.update after apply_rotary_pos_emb,
+ * llama.py:851-862): the rotated k is written to k_cache at row *pos (k itself
+ * is not modified) and v is copied to v_cache at row *pos; q is rotated in
+ * place. pos is an int64 in device memory (a graph-recorded step reads the
+ * current row at replay). Caches are [B, max_len, Hkv, D] with strides
+ * kc_str / vc_str = {batch, row, head}; k and v [B, 1, Hkv, D] with k_str /
+ * v_str = {batch, seq, head}. The caller keeps *pos below max_len.
+ */
+int da_rope_qk_append(void* q, const int64_t q_str[3], int Hq,
+                      const void* k, const int64_t k_str[3], int Hkv,
+                      const void* v, const int64_t v_str[3],
+                      int B, int D,
+                      const void* cos, const void* sin, const int64_t cs_str[2],
+                      const void* q_norm_w, const void* k_norm_w, float eps,
+                      void* k_cache, const int64_t kc_str[3],
+                      void* v_cache, const int64_t vc_str[3],
+                      const int64_t* pos, int dtype, void* stream);
+
 /* Consecutive-anchor delta cosine (stride.py:43-52 interanchor_cos, the
  * adaptive stride's drift signal, llama.py:784-788; drift.py:23-49
  * drift_summary's cosines and histogram). For deltas d_0 .. d_{n-1} per

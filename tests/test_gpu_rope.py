@@ -131,3 +131,36 @@ def test_module_fused_prologue_matches_torch_prologue(gpu):
         y_ref = m.o_proj(a.reshape(1, 1100, -1))
     torch.cuda.synchronize()
     assert torch.equal(y, y_ref)
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_rope_qk_append_equals_rope_then_cache_update(gpu, norm):
+    """The one-token decode prologue with the cache append in the same launch:
+    q rotated in place and the cache rows at the device-held position hold
+    exactly what rope_qk followed by the cache update (index_copy_) writes;
+    other cache rows untouched."""
+    from delta_attention import ops
+    from delta_attention.llama import rope_cos_sin
+    B, Hq, Hkv, D, L_max, pos = 2, 8, 2, 128, 40, 17
+    print(f"rope append B{B} H{Hq}/{Hkv} D{D} pos {pos} norm {norm}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    qkv = torch.randn(B, 1, (Hq + 2 * Hkv) * D, device="cuda", generator=g).to(torch.bfloat16)
+    q = qkv[..., :Hq * D].unflatten(-1, (Hq, D))
+    k = qkv[..., Hq * D:(Hq + Hkv) * D].unflatten(-1, (Hkv, D))
+    v = qkv[..., (Hq + Hkv) * D:].unflatten(-1, (Hkv, D))
+    cos, sin = rope_cos_sin(torch.full((1, 1), pos, device="cuda"), D, 5e5, torch.bfloat16)
+    w = [torch.rand(D, device="cuda", generator=g).to(torch.bfloat16) + 0.5 for _ in range(2)] if norm else [None, None]
+    kc = torch.randn(B, L_max, Hkv, D, device="cuda", generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, L_max, Hkv, D, device="cuda", generator=g).to(torch.bfloat16)
+    kc2, vc2 = kc.clone(), vc.clone()
+    q_ref, k_ref = q.clone(), k.clone()
+    ops.rope_qk(q_ref, k_ref, cos, sin, q_norm_w=w[0], k_norm_w=w[1], eps=1e-6)
+    p = torch.tensor([pos], device="cuda", dtype=torch.int64)
+    kc2.index_copy_(1, p, k_ref)
+    vc2.index_copy_(1, p, v)
+    k_before = k.clone()
+    ops.rope_qk_append(q, k, v, cos, sin, kc, vc, p, q_norm_w=w[0], k_norm_w=w[1], eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q_ref)
+    assert torch.equal(k, k_before)            # k itself is not modified
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
