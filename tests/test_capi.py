@@ -313,3 +313,25 @@ def test_training_entry_checks(lib):
                                     q3, k3, k3, P(16), q3, P(18), 0.1, P(16), 1 << 30,
                                     L.DA_BF16, None)
     assert f == L.DA_ERR_ALIGNMENT
+
+
+def test_rope_append_checks(lib):
+    """da_rope_qk_append refuses bad arguments before a launch."""
+    P = ctypes.c_void_p
+    x3 = _s3(12 * 128, 12 * 128, 128)
+    c3 = _s3(40 * 2 * 128, 2 * 128, 128)
+    cs = (ctypes.c_int64 * 2)(0, 128)
+
+    def call(pos=16, D=128, dtype=L.DA_BF16, v=16, kc=16, cos=16):
+        return lib.da_rope_qk_append(P(16), x3, 8, P(16), x3, 2, P(v) if v else None, x3, 1, D,
+                                     P(cos) if cos else None, P(16), cs, None, None, 1e-6,
+                                     P(kc) if kc else None, c3, P(16), c3,
+                                     P(pos) if pos else None, dtype, None)
+    assert call(pos=0) == L.DA_ERR_INVALID_ARG
+    assert call(pos=20) == L.DA_ERR_ALIGNMENT          # int64 position
+    assert call(v=0) == L.DA_ERR_INVALID_ARG
+    assert call(kc=0) == L.DA_ERR_INVALID_ARG
+    assert call(kc=24) == L.DA_ERR_ALIGNMENT
+    assert call(cos=0) == L.DA_ERR_INVALID_ARG
+    assert call(D=96) == L.DA_ERR_HEAD_DIM
+    assert call(dtype=3) == L.DA_ERR_DTYPE
