@@ -434,9 +434,10 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
   using E = Elt<T>;
   constexpr int NDS = D / 16, NDT = D / 32, DCH = D / 8, RB = 2 * D;
   constexpr int TB = RT * RB;
-  // Q and dO rows of up to HGM query heads per step: one load round trip and
-  // one barrier pair serve HGM heads' products
-  constexpr int HGM = 4;
+  // Q and dO rows of up to HGM query heads per step (all of a KV head's query
+  // heads for GQA up to 8): one load round trip and one barrier pair serve
+  // that many heads' products
+  constexpr int HGM = 8;
   __shared__ __attribute__((aligned(1024))) char smem[2][HGM][TB];   // Q, dO
   __shared__ __attribute__((aligned(16))) float s_lse[HGM][RT], s_d[HGM][RT];
   __shared__ __attribute__((aligned(16))) int s_lim[RT], s_lo[RT];
