@@ -108,8 +108,9 @@ struct AttnArgs {
   // [1, n_kv]) and chunk = ceil(list / n_splits): the launch stays valid as a
   // cache grows (decode rows under graph replay)
   const int* n_kv_dev;
-  float* part_o;    // [item][BM][D]
-  float* part_ml;   // [item][2][BM]  (running max, row sum)
+  float* part_o;    // [item][ws_rows][D]
+  float* part_ml;   // [item][2][ws_rows]  (running max, row sum)
+  int ws_rows;      // workspace rows per item: min(BM, n_rows * G) (a tile's valid rows)
   // MODE_FUSED: dense anchor rows [B, n_anchor, Hq, D] (strides batch, head,
   // anchor), optional delta output (same layout), stride and rows < s_p
   const void* dsel;
@@ -125,6 +126,11 @@ struct AttnArgs {
 // Bytes of LDS that hold a fused tile's dense anchor rows, prefetched with the
 // first K/V tiles (tiles with more anchor rows read them in the epilogue).
 constexpr int DPRE_BYTES = 4096;
+// The deltas those rows give, one 16-byte-padded slot per (group, head): the
+// lanes of a wave read the slots of two heads at once, which the padding puts
+// on different LDS banks.
+constexpr int DPAD = 16;
+constexpr int DLT_BYTES = DPRE_BYTES + 64 * DPAD;
 
 // sigma: swaps bits 2 and 3 of a key index within a 32-key half tile. Using
 // K row sigma(r) as A-operand row r puts keys 8*g .. 8*g+7 (g = lane / 32) in
@@ -186,6 +192,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE][2][TL::BYTES];
   __shared__ int red[4][NWAVE];
   __shared__ __attribute__((aligned(16))) char dpre[MODE == MODE_FUSED ? DPRE_BYTES : 16];
+  __shared__ __attribute__((aligned(16))) char dlt[MODE == MODE_FUSED ? DLT_BYTES : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -579,6 +586,42 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
 
   // ---- epilogue ----
   const float l_tot = sum32(l_i);
+  // Output rows leave through LDS: each lane parks its 4-element pieces (dims
+  // 32 dt + 8 jq + 4 lg .. +3 of wave row ln) in the wave's 32-row block of K/V
+  // stage 1, with the 16-byte chunks XOR-swizzled by the row so that neither
+  // the writes nor the reads conflict, then stores whole 16-byte chunks of
+  // consecutive rows: every store instruction writes complete rows, which
+  // measured faster than each one writing 16-byte pieces of 32 rows. The
+  // caller has a barrier behind it (stage 1 is no longer read by any wave);
+  // row_dst(r) gives row r's destination, or nullptr for a row not written.
+  auto stage_rows = [&](const u32x2 (&val)[NDT][4], auto row_dst) {
+    static_assert(NWAVE * 32 * RB <= 2 * TL::BYTES, "staging fits K/V stage 1");
+    DA_LDS char* sbuf = (DA_LDS char*)&smem[1][0][0] + wave * 32 * RB;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        *(DA_LDS u32x2*)(sbuf + ln * RB + (((4 * dt + jq) ^ (ln & (DCH - 1))) * 16) + 8 * lg) =
+            val[dt][jq];
+    constexpr int RPI = 1024 / RB;     // rows per store instruction
+    const int c = lane % DCH;
+#pragma unroll
+    for (int k = 0; k < 32 / RPI; ++k) {
+      const int r = k * RPI + lane / DCH;
+      const u32x4 x = *(const DA_LDS u32x4*)(sbuf + r * RB + ((c ^ (r & (DCH - 1))) * 16));
+      char* dst = row_dst(r);
+      if (dst) *(u32x4*)(dst + c * 16) = x;
+    }
+  };
+  // destination of wave row r in the [B, S, Hq, D] output (nullptr past the
+  // tile's rows, or, with `limit`, at rows >= limit)
+  auto out_row = [&](int r, int limit) -> char* {
+    const int mf = mt * BM + wave * 32 + r;
+    const int ir = mf / GT;
+    if (mf >= a.n_rows * GT || ir >= limit) return nullptr;
+    const int hr = hk * G + hs * GT + mf % GT;
+    return (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hr * a.os_h + (int64_t)ir * a.os_s) * esz;
+  };
   if (MODE == MODE_FUSED) {
     // out[r] = rnd(rnd(sparse[r]) + delta[r / gamma]) for rows r < s_p, with
     // delta[g] = rnd(dense[g] - rnd(sparse[g * gamma])) formed by the anchor
@@ -597,13 +640,16 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
     const int row0 = mt * (BM / GT);                 // first row of the tile
     const bool live = valid && irow < a.s_p;
     const int gl = (irow - row0) / a.gamma;          // group within the tile
-    // delta rows in LDS. With the dense rows prefetched, each anchor lane
-    // replaces its own dense elements in dpre ([group][head][D]) by the delta,
+    // delta rows in LDS. With the dense rows prefetched (dpre, [group][head][D]),
+    // each anchor lane writes its delta elements to the padded slots of dlt,
     // so one barrier suffices. Otherwise they go to the K/V stage memory
     // ([group][head][lg][D/2]) once every wave is done with it.
     DA_LDS u32x2* dl;
+    DA_LDS u32x2* dn_pre = nullptr;
     if (pre) {
-      dl = (DA_LDS u32x2*)&dpre[0] + ((gl * GT + mflat % GT) * D) / 4 + lg;
+      static_assert(DLT_BYTES >= DPRE_BYTES + (DPRE_BYTES / (2 * 32)) * DPAD, "padded slots fit");
+      dn_pre = (DA_LDS u32x2*)&dpre[0] + ((gl * GT + mflat % GT) * D) / 4 + lg;
+      dl = (DA_LDS u32x2*)&dlt[(gl * GT + mflat % GT) * (D * (int)esz + DPAD)] + lg;
       if (nt == 0) {     // no key tile ran: make every wave's dpre DMA visible
         wait_vmcnt<0>();
         __syncthreads();
@@ -628,7 +674,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-            for (int jq = 0; jq < 4; ++jq) dn[dt][jq] = *dslot(dt, jq);
+            for (int jq = 0; jq < 4; ++jq) dn[dt][jq] = dn_pre[8 * dt + 2 * jq];
         } else {
           const char* dp = (const char*)a.dsel +
                            ((int64_t)b * a.dsel_b + (int64_t)hrow * a.dsel_h + g * a.dsel_a) * esz;
@@ -662,53 +708,45 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
         }
       }
       __syncthreads();
-      if (live) {
-        char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
-                                 (int64_t)qrow * a.os_s) * esz;
-        u32x2 dv[NDT][4];
+      // every lane forms its row's output (rows >= s_p are not stored)
+      u32x2 dv[NDT][4], o[NDT][4];
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-          for (int jq = 0; jq < 4; ++jq) dv[dt][jq] = *dslot(dt, jq);
+        for (int jq = 0; jq < 4; ++jq) dv[dt][jq] = *dslot(dt, jq);
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-          for (int jq = 0; jq < 4; ++jq) {
-            u32x2 o;
+        for (int jq = 0; jq < 4; ++jq)
 #pragma unroll
-            for (int e = 0; e < 2; ++e)
-              o[e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[dt][jq][e]),
-                              E::hi(sp[dt][jq][e]) + E::hi(dv[dt][jq][e]));
-            *(u32x2*)(op + (32 * dt + 8 * jq + 4 * lg) * esz) = o;
-          }
-      }
+          for (int e = 0; e < 2; ++e)
+            o[dt][jq][e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[dt][jq][e]),
+                                    E::hi(sp[dt][jq][e]) + E::hi(dv[dt][jq][e]));
+      stage_rows(o, [&](int r) { return out_row(r, a.s_p); });
     };
     if (pre) fused_out(std::true_type());
     else fused_out(std::false_type());
     return;
   }
   if (MODE == MODE_SPARSE) {
-    if (!valid) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (a.lse && lg == 0)
+    if (valid && a.lse && lg == 0)
       a.lse[((int64_t)b * a.Hq + hrow) * a.n_rows + irow] =
           l_tot > 0.f ? m_i + __builtin_log2f(l_tot) : INFINITY;
-    char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
-                             (int64_t)qrow * a.os_s) * esz;
+    u32x2 o[NDT][4];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
-        const int d = 32 * dt + 8 * jq + 4 * lg;
-        u32x2 pkd;
-        pkd[0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
-        pkd[1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
-        *(u32x2*)(op + d * esz) = pkd;
+        o[dt][jq][0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
+        o[dt][jq][1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
       }
+    __syncthreads();   // every wave is done with the K/V stages
+    stage_rows(o, [&](int r) { return out_row(r, a.n_rows); });
   } else {
     if (!valid) return;   // the merge reads the rows of the selection only
     const int r = wave * 32 + ln;
-    float* po = a.part_o + ((int64_t)w * BM + r) * D;
+    float* po = a.part_o + ((int64_t)w * a.ws_rows + r) * D;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -718,8 +756,8 @@ __global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
                                      acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]};
       }
     if (lg == 0) {
-      a.part_ml[(int64_t)w * 2 * BM + r] = m_i;
-      a.part_ml[(int64_t)w * 2 * BM + BM + r] = l_tot;
+      a.part_ml[(int64_t)w * 2 * a.ws_rows + r] = m_i;
+      a.part_ml[(int64_t)w * 2 * a.ws_rows + a.ws_rows + r] = l_tot;
     }
   }
 }
@@ -741,6 +779,7 @@ struct MergeArgs {
   int wgs;          // workgroups per row tile
   const float* part_o;
   const float* part_ml;
+  int ws_rows;      // as in AttnArgs
   int epi, n_anchor, n_q;
   void* o;
   int64_t os_b, os_h, os_s;
@@ -814,7 +853,7 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
     float M = NEG_BIG;
     for (int s = p; s < nsv; s += P) {
       const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
-      M = fmaxf(M, a.part_ml[w * 2 * BM + r]);
+      M = fmaxf(M, a.part_ml[w * 2 * a.ws_rows + r]);
     }
     for (int off = 1; off < P; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
     float L = 0.f;
@@ -823,9 +862,9 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
     for (int s = p; s < nsv; s += P) {
       const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
-      const float sc = fast_exp2(a.part_ml[w * 2 * BM + r] - M);
-      L += sc * a.part_ml[w * 2 * BM + BM + r];
-      const f32x4* po = (const f32x4*)(a.part_o + (w * BM + r) * D + 8 * c);
+      const float sc = fast_exp2(a.part_ml[w * 2 * a.ws_rows + r] - M);
+      L += sc * a.part_ml[w * 2 * a.ws_rows + a.ws_rows + r];
+      const f32x4* po = (const f32x4*)(a.part_o + (w * a.ws_rows + r) * D + 8 * c);
       const f32x4 x0 = po[0], x1 = po[1];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -888,6 +927,7 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
 
 struct QsparsePlan {
   int n_mtiles, n_splits, chunk, n_items;
+  int ws_rows;      // workspace rows per item: a tile's valid (row, head) pairs at most
   size_t ws_bytes;
 };
 
@@ -912,7 +952,8 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
   // are refused by the entry points (n_items = 0)
   const bool fits = items <= 0x7fffff00LL && base * 128 <= 0x7fffff00LL;
   p.n_items = fits ? (int)items : 0;
-  p.ws_bytes = fits ? (size_t)p.n_items * BM * (D + 2) * sizeof(float) : 0;
+  p.ws_rows = (int)min((int64_t)BM, (int64_t)n * G);
+  p.ws_bytes = fits ? (size_t)p.n_items * p.ws_rows * (D + 2) * sizeof(float) : 0;
   return p;
 }
 
@@ -1116,7 +1157,8 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   a.chunk = p.chunk; a.n_splits = p.n_splits; a.n_kv_dev = n_kv_dev;
   a.window = window; a.sink = sink;
   a.part_o = (float*)workspace;
-  a.part_ml = (float*)workspace + (size_t)p.n_items * BM * D;
+  a.part_ml = (float*)workspace + (size_t)p.n_items * p.ws_rows * D;
+  a.ws_rows = p.ws_rows;
 
   MergeArgs m = {};
   m.q_rows = q_rows; m.row_last = row_last; m.rl_b = rl_bstride;
@@ -1131,7 +1173,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
     const int64_t rows = min((int64_t)BM, (int64_t)n * a.G);
     m.wgs = (int)((rows * (D / 8) * m.lanes + MTHR - 1) / MTHR);
   }
-  m.part_o = a.part_o; m.part_ml = a.part_ml;
+  m.part_o = a.part_o; m.part_ml = a.part_ml; m.ws_rows = p.ws_rows;
   m.epi = epi; m.n_anchor = (epi == DA_EPI_DELTA || epi == DA_EPI_DENSE) ? n_anchor : 0;
   m.o = o; m.os_b = o_str[0]; m.os_h = o_str[1]; m.os_s = o_str[2];
   m.delta = delta;
