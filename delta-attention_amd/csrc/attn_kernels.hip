@@ -36,6 +36,7 @@
 //     fed: the exponentials of tile t run under the score MFMAs of tile t+1,
 //     then the PV MFMAs of tile t follow with their V reads running ahead.
 //     In the key-sparse modes that region runs at raised wave priority.
+#include <mutex>
 #include <type_traits>
 
 #include "device_common.h"
@@ -1327,4 +1328,58 @@ extern "C" int da_decode_attn_fwd_dev(const void* q, const void* k, const void* 
                      q_str, k_str, v_str, out, o_str, DA_EPI_OUTPUT, 0, nullptr, nullptr,
                      window, sink, sm_scale, workspace, workspace_bytes, dtype, stream,
                      n_keys_dev, addend, add_str);
+}
+
+// ---------------------------------------------------------------------------
+// Decode row without a caller workspace (da_decode_attn_fwd_dev_noalloc): the
+// split-KV partials live in `scratch`, a file-scope device array of
+// DA_DECODE_SCRATCH_BYTES of which each GPU holds its own copy until the
+// process ends. Host code never passes the array's name to a kernel (on the
+// host it is a stand-in, not a device address): the address comes from
+// hipGetSymbolAddress, once per device with that device current, and is kept
+// per device. Nothing in the scratch needs to start at zero (the merge reads
+// only the partials the split kernel of the same call wrote); calls that
+// overlap on one GPU share the array and race.
+static __device__ __align__(256) char scratch[DA_DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES];
+}  // namespace
+
+// This device's address of `scratch` (looked up on the first call on it).
+static int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return DA_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return DA_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DA_OK;
+}
+
+extern "C" size_t da_decode_scratch_bytes(void) { return DA_DECODE_SCRATCH_BYTES; }
+
+extern "C" int da_decode_attn_fwd_dev_noalloc(const void* q, const void* k, const void* v,
+                                              void* out, int B, int Hq, int Hkv,
+                                              const int32_t* n_keys_dev, int max_keys, int D,
+                                              const int64_t q_str[3], const int64_t k_str[3],
+                                              const int64_t v_str[3], const int64_t o_str[3],
+                                              int window, int sink, float sm_scale,
+                                              const void* addend, const int64_t add_str[3],
+                                              int dtype, void* stream) {
+  int rc;
+  if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
+  if (max_keys < 1 || window < 0 || sink < 0) return DA_ERR_INVALID_ARG;
+  const size_t need = plan_decode(B, Hq, Hkv, max_keys, D, window, sink).ws_bytes;
+  if (need == 0 || need > DA_DECODE_SCRATCH_BYTES) return DA_ERR_SCRATCH;
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws)) != DA_OK) return rc;
+  return da_decode_attn_fwd_dev(q, k, v, out, B, Hq, Hkv, n_keys_dev, max_keys, D, q_str, k_str,
+                                v_str, o_str, window, sink, sm_scale, addend, add_str, ws,
+                                DA_DECODE_SCRATCH_BYTES, dtype, stream);
 }

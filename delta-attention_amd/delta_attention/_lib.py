@@ -20,6 +20,7 @@ DA_ERR_DTYPE = -3
 DA_ERR_ALIGNMENT = -4
 DA_ERR_WORKSPACE = -5
 DA_ERR_LAUNCH = -6
+DA_ERR_SCRATCH = -7
 
 DA_BF16 = 0
 DA_FP16 = 1
@@ -52,6 +53,8 @@ EXPORTS = (
     "da_delta_compose_bwd",
     "da_rope_qk_append",
     "da_build_target",
+    "da_decode_scratch_bytes",
+    "da_decode_attn_fwd_dev_noalloc",
 )
 
 _ERR_TEXT = {
@@ -61,6 +64,7 @@ _ERR_TEXT = {
     DA_ERR_ALIGNMENT: "tensor rows must be 16-byte aligned (strides multiple of 8 elements)",
     DA_ERR_WORKSPACE: "workspace missing or too small",
     DA_ERR_LAUNCH: "kernel launch failed",
+    DA_ERR_SCRATCH: "sizes need more than the library's static scratch holds",
 }
 
 
@@ -169,6 +173,12 @@ def _load() -> ctypes.CDLL:
     L.da_rope_qk_append.restype = _i
     L.da_rope_qk_append.argtypes = [_vp, _p3, _i, _vp, _p3, _i, _vp, _p3, _i, _i, _vp, _vp,
                                     _vp, _vp, _vp, _f, _vp, _p3, _vp, _p3, _vp, _i, _vp]
+    L.da_decode_scratch_bytes.restype = _sz
+    L.da_decode_scratch_bytes.argtypes = []
+    L.da_decode_attn_fwd_dev_noalloc.restype = _i
+    L.da_decode_attn_fwd_dev_noalloc.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i,
+                                                 _p3, _p3, _p3, _p3, _i, _i, _f, _vp, _p3,
+                                                 _i, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
     return L

@@ -21,7 +21,8 @@
  *     stream). No entry point synchronises, allocates or frees; the caller
  *     owns all memory, including workspaces.
  *   - Return 0 on success or a negative DA_ERR_* code. No entry point keeps
- *     a pointer after it returns and there is no mutable global state, so
+ *     a pointer after it returns and, apart from the static scratch of
+ *     da_decode_attn_fwd_dev_noalloc, there is no mutable global state, so
  *     calls are re-entrant.
  */
 #ifndef DELTA_ATTN_H
@@ -41,6 +42,7 @@ extern "C" {
 #define DA_ERR_ALIGNMENT (-4)        /* pointer or stride breaks 16-byte row alignment */
 #define DA_ERR_WORKSPACE (-5)        /* workspace missing or smaller than required */
 #define DA_ERR_LAUNCH (-6)           /* hipGetLastError reported a launch failure */
+#define DA_ERR_SCRATCH (-7)          /* sizes need more than the library's static scratch holds */
 
 #define DA_BF16 0
 #define DA_FP16 1
@@ -184,6 +186,30 @@ int da_decode_attn_fwd_dev(const void* q, const void* k, const void* v, void* ou
                            int window, int sink, float sm_scale,
                            const void* addend, const int64_t add_str[3],
                            void* workspace, size_t workspace_bytes, int dtype, void* stream);
+
+/*
+ * da_decode_attn_fwd_dev without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The split-KV partials go to a static device array of
+ * DA_DECODE_SCRATCH_BYTES (16 MiB; each GPU the library runs on holds its own
+ * copy until the process ends); sizes whose partials
+ * (da_decode_workspace_bytes(B, Hq, Hkv, max_keys, D, window, sink)) exceed
+ * it return DA_ERR_SCRATCH. Allocates nothing. Calls that overlap on one GPU
+ * (e.g. on two streams at once) share the array and race. The current device
+ * must be the device of `stream`. Results equal da_decode_attn_fwd_dev's on
+ * the same arguments bit for bit.
+ */
+#define DA_DECODE_SCRATCH_BYTES (16u << 20)
+size_t da_decode_scratch_bytes(void);
+int da_decode_attn_fwd_dev_noalloc(const void* q, const void* k, const void* v, void* out,
+                                   int B, int Hq, int Hkv, const int32_t* n_keys_dev,
+                                   int max_keys, int D,
+                                   const int64_t q_str[3], const int64_t k_str[3],
+                                   const int64_t v_str[3], const int64_t o_str[3],
+                                   int window, int sink, float sm_scale,
+                                   const void* addend, const int64_t add_str[3],
+                                   int dtype, void* stream);
 
 /*
  * Kernel (3): delta broadcast-add over rows 0 .. s_p-1.

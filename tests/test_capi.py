@@ -221,6 +221,28 @@ def test_decode_dev_checks(lib):
     assert call(add=8) == L.DA_ERR_ALIGNMENT            # addend rows 16-byte aligned
 
 
+def test_decode_noalloc_checks(lib):
+    """The no-workspace decode entry refuses bad arguments, and sizes whose
+    partials exceed its static scratch, before it looks up the scratch or
+    launches anything."""
+    P = ctypes.c_void_p
+    assert lib.da_decode_scratch_bytes() == 16 << 20
+
+    def call(H=32, Hkv=8, max_keys=8192, D=128, window=0, dtype=L.DA_BF16):
+        s3 = _s3(H * D, D, D)
+        k3 = _s3(Hkv * max_keys * D, max_keys * D, D)
+        return lib.da_decode_attn_fwd_dev_noalloc(P(16), P(16), P(16), P(16), 1, H, Hkv, P(16),
+                                                  max_keys, D, s3, k3, k3, s3, window, 0, 0.1,
+                                                  None, None, dtype, None)
+    assert call(dtype=5) == L.DA_ERR_DTYPE
+    assert call(D=80) == L.DA_ERR_HEAD_DIM
+    assert call(max_keys=0) == L.DA_ERR_INVALID_ARG
+    assert call(window=-1) == L.DA_ERR_INVALID_ARG
+    assert call(H=1024, max_keys=131072) == L.DA_ERR_SCRATCH
+    need = lib.da_decode_workspace_bytes(1, 1024, 8, 131072, 128, 0, 0)
+    assert need > lib.da_decode_scratch_bytes()
+
+
 def test_anchor_delta_cos_checks(lib):
     P = ctypes.c_void_p
     a3 = _s3(64 * 8 * 128, 8 * 128, 128)
