@@ -883,6 +883,7 @@ int bwd_args(BwdArgs& a, const void* q, const void* k, const void* v, const void
              int dtype) {
   int rc;
   if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
+  if (D > 128) return DA_ERR_HEAD_DIM;   // the backward kernels take 32, 64 and 128
   if (n_rows < 1 || n_q < 1 || n_kv < 1) return DA_ERR_INVALID_ARG;
   if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv) return DA_ERR_INVALID_ARG;
   if (!ok3(q_str) || !ok3(k_str) || !ok3(v_str) || !ok3(o_str) || !ok3(do_str) ||

@@ -177,8 +177,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Scheduling-group barrier masks (LLVM AMDGPU IGroupLP).
 enum : int { SG_VALU = 0x2, SG_MFMA = 0x8, SG_DS_READ = 0x100 };
 
+// Workgroups per CU: two at head_dim <= 128; one at 256, whose accumulator
+// and fragments need a whole SIMD's registers and whose K/V stages take 128 KB.
+constexpr int attn_occupancy(int D) { return D > 128 ? 1 : 2; }
+
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(NTHR, 2) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnArgs a) {
   using TL = Tile<D>;
   constexpr int DCH = TL::DCH;
   constexpr int RB = TL::RB;
@@ -987,10 +991,12 @@ static void dispatch_attn(const AttnArgs& a, int D, int dtype, hipStream_t s) {
   if (dtype == DA_BF16) {
     if (D == 128) launch_attn<__bf16, 128, MODE>(a, s);
     else if (D == 64) launch_attn<__bf16, 64, MODE>(a, s);
+    else if (D == 256) launch_attn<__bf16, 256, MODE>(a, s);
     else launch_attn<__bf16, 32, MODE>(a, s);
   } else {
     if (D == 128) launch_attn<_Float16, 128, MODE>(a, s);
     else if (D == 64) launch_attn<_Float16, 64, MODE>(a, s);
+    else if (D == 256) launch_attn<_Float16, 256, MODE>(a, s);
     else launch_attn<_Float16, 32, MODE>(a, s);
   }
 }
@@ -1190,10 +1196,12 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   if (dtype == DA_BF16) {
     if (D == 128) launch_merge<__bf16, 128>(m, n_tiles, s);
     else if (D == 64) launch_merge<__bf16, 64>(m, n_tiles, s);
+    else if (D == 256) launch_merge<__bf16, 256>(m, n_tiles, s);
     else launch_merge<__bf16, 32>(m, n_tiles, s);
   } else {
     if (D == 128) launch_merge<_Float16, 128>(m, n_tiles, s);
     else if (D == 64) launch_merge<_Float16, 64>(m, n_tiles, s);
+    else if (D == 256) launch_merge<_Float16, 256>(m, n_tiles, s);
     else launch_merge<_Float16, 32>(m, n_tiles, s);
   }
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
@@ -1201,7 +1209,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
 
 extern "C" size_t da_qsparse_workspace_bytes(int B, int Hq, int Hkv, int n, int Skv, int D) {
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n < 1 || Skv < 1 ||
-      (D != 32 && D != 64 && D != 128))
+      !head_dim_ok(D))
     return 0;
   return plan_rows(B, Hq, Hkv, n, Skv, D).ws_bytes;
 }
@@ -1269,7 +1277,7 @@ extern "C" int da_qsparse_attn_fwd_lse(const void* q, const void* k, const void*
 
 extern "C" size_t da_decode_workspace_bytes(int B, int Hq, int Hkv, int n_keys, int D, int window,
                                             int sink) {
-  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n_keys < 1 || (D != 32 && D != 64 && D != 128) ||
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n_keys < 1 || !head_dim_ok(D) ||
       window < 0 || sink < 0)
     return 0;
   return plan_decode(B, Hq, Hkv, n_keys, D, window, sink).ws_bytes;

@@ -12,8 +12,8 @@
 // non-temporal for large inputs and ordinary below NT_MIN_BYTES (a decode
 // step's rows are read next from L2); the cos/sin rows and the norm weight,
 // shared by every head, with ordinary loads. One launch covers the q rows then
-// the k rows; 8 consecutive threads own one (token, head) row (8 + 8 elements
-// each for D=128).
+// the k rows; D/16 consecutive threads own one (token, head) row, 8 + 8
+// elements each (one 16-byte access per half), for D in {32, 64, 128, 256}.
 #include "device_common.h"
 #include "capi_common.h"
 
@@ -40,8 +40,10 @@ struct RopeArgs {
   int64_t rows;            // q.rows + k.rows + v_rows
   // one-token KV-cache append (S == 1): k rows are written to kc at cache
   // row *pos instead of in place, and rows [q.rows + k.rows, rows) copy v
-  // into vc at the same row
+  // into vc at the same row; a row *pos outside [0, max_len) writes neither
+  // cache (q is still rotated)
   const int64_t* pos;
+  int64_t max_len;
   void* kc;
   int64_t kc_b, kc_s, kc_h;
   const void* v;
@@ -51,32 +53,33 @@ struct RopeArgs {
   int64_t v_rows;
 };
 
+// threads per (token, head) row
+constexpr int rope_tpr(int D) { return D / 16; }
+
 template <typename T, int D, bool NT>
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   using E = Elt<T>;
-  constexpr int TPR = 8;              // threads per row
+  constexpr int TPR = rope_tpr(D);    // threads per row
   constexpr int HALF = D / 2;
-  constexpr int EPT = HALF / TPR;     // elements per thread in each half (8 for D=128)
-  static_assert(EPT == 8 || EPT == 4, "D must be 64 or 128");
+  constexpr int EPT = HALF / TPR;     // elements per thread in each half
+  static_assert(EPT == 8, "one 16-byte access per half");
   const int64_t gtid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = gtid / TPR;
   const int part = (int)(gtid % TPR);
   constexpr size_t esz = sizeof(T);
+  // cache row of an append launch, and whether it lies inside the caches
+  const int64_t crow = a.pos ? *a.pos : 0;
+  const bool crow_ok = crow >= 0 && crow < a.max_len;
   if (a.v_rows > 0 && row >= a.q.rows + a.k.rows) {
     // cache append of v: this thread's 2 x EPT elements, no arithmetic
-    if (row >= a.rows) return;
+    if (row >= a.rows || !crow_ok) return;
     const int64_t vr = row - a.q.rows - a.k.rows;
     const int hv = (int)(vr % a.k.H), bv = (int)(vr / a.k.H);   // S == 1
     const char* src = (const char*)a.v + ((int64_t)bv * a.v_b + (int64_t)hv * a.v_h) * esz;
-    char* dst = (char*)a.vc + ((int64_t)bv * a.vc_b + *a.pos * a.vc_s + (int64_t)hv * a.vc_h) * esz;
+    char* dst = (char*)a.vc + ((int64_t)bv * a.vc_b + crow * a.vc_s + (int64_t)hv * a.vc_h) * esz;
     const int j0 = part * EPT;
-    if constexpr (EPT == 8) {
-      *(u32x4*)(dst + j0 * esz) = *(const u32x4*)(src + j0 * esz);
-      *(u32x4*)(dst + (HALF + j0) * esz) = *(const u32x4*)(src + (HALF + j0) * esz);
-    } else {
-      *(u32x2*)(dst + j0 * esz) = *(const u32x2*)(src + j0 * esz);
-      *(u32x2*)(dst + (HALF + j0) * esz) = *(const u32x2*)(src + (HALF + j0) * esz);
-    }
+    *(u32x4*)(dst + j0 * esz) = *(const u32x4*)(src + j0 * esz);
+    *(u32x4*)(dst + (HALF + j0) * esz) = *(const u32x4*)(src + (HALF + j0) * esz);
     return;
   }
   const bool live = row < a.rows;
@@ -99,15 +102,9 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
 
   float lo[EPT], hi[EPT];
   auto load8 = [&](const char* p, float* dst, bool nt = false) {
-    if constexpr (EPT == 8) {
-      const u32x4 v = nt ? ld_nt4(p) : *(const u32x4*)p;
+    const u32x4 v = nt ? ld_nt4(p) : *(const u32x4*)p;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) { dst[2 * e] = E::lo(v[e]); dst[2 * e + 1] = E::hi(v[e]); }
-    } else {
-      const u32x2 v = nt ? ld_nt2(p) : *(const u32x2*)p;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) { dst[2 * e] = E::lo(v[e]); dst[2 * e + 1] = E::hi(v[e]); }
-    }
+    for (int e = 0; e < 4; ++e) { dst[2 * e] = E::lo(v[e]); dst[2 * e + 1] = E::hi(v[e]); }
   };
   if (live) {
     load8(xp + i0 * esz, lo, NT);
@@ -158,36 +155,36 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     ohi[e / 2] = E::pack2(E::lo(b1) + E::lo(b2), E::hi(b1) + E::hi(b2));
   }
   if (!live) return;
-  if (kpart && a.kc)   // rotated k goes to its cache row
-    xp = (char*)a.kc + ((int64_t)b * a.kc_b + *a.pos * a.kc_s + (int64_t)h * a.kc_h) * esz;
-  if constexpr (EPT == 8) {
-    const u32x4 vl = {olo[0], olo[1], olo[2], olo[3]}, vh = {ohi[0], ohi[1], ohi[2], ohi[3]};
-    if constexpr (NT) {
-      st_nt4(xp + i0 * esz, vl);
-      st_nt4(xp + (HALF + i0) * esz, vh);
-    } else {
-      *(u32x4*)(xp + i0 * esz) = vl;
-      *(u32x4*)(xp + (HALF + i0) * esz) = vh;
-    }
-  } else {
-    const u32x2 vl = {olo[0], olo[1]}, vh = {ohi[0], ohi[1]};
-    if constexpr (NT) {
-      st_nt2(xp + i0 * esz, vl);
-      st_nt2(xp + (HALF + i0) * esz, vh);
-    } else {
-      *(u32x2*)(xp + i0 * esz) = vl;
-      *(u32x2*)(xp + (HALF + i0) * esz) = vh;
-    }
+  if (kpart && a.kc) {   // rotated k goes to its cache row (k itself is kept)
+    if (!crow_ok) return;
+    xp = (char*)a.kc + ((int64_t)b * a.kc_b + crow * a.kc_s + (int64_t)h * a.kc_h) * esz;
   }
+  const u32x4 vl = {olo[0], olo[1], olo[2], olo[3]}, vh = {ohi[0], ohi[1], ohi[2], ohi[3]};
+  if constexpr (NT) {
+    st_nt4(xp + i0 * esz, vl);
+    st_nt4(xp + (HALF + i0) * esz, vh);
+  } else {
+    *(u32x4*)(xp + i0 * esz) = vl;
+    *(u32x4*)(xp + (HALF + i0) * esz) = vh;
+  }
+}
+
+template <typename T, int D, bool NT>
+static void launch_rope_d(const RopeArgs& a, hipStream_t s) {
+  const int64_t threads = a.rows * rope_tpr(D);
+  const int grid = (int)((threads + 255) / 256);
+  hipLaunchKernelGGL((rope_kernel<T, D, NT>), dim3(grid), dim3(256), 0, s, a);
 }
 
 template <typename T, bool NT>
 static void launch_rope_nt(const RopeArgs& a, hipStream_t s) {
-  const int64_t threads = a.rows * 8;
-  const int grid = (int)((threads + 255) / 256);
-  if (a.D == 128) hipLaunchKernelGGL((rope_kernel<T, 128, NT>), dim3(grid), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((rope_kernel<T, 64, NT>), dim3(grid), dim3(256), 0, s, a);
+  if (a.D == 128) launch_rope_d<T, 128, NT>(a, s);
+  else if (a.D == 64) launch_rope_d<T, 64, NT>(a, s);
+  else if (a.D == 256) launch_rope_d<T, 256, NT>(a, s);
+  else launch_rope_d<T, 32, NT>(a, s);
 }
+
+static bool rope_dim_ok(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
 
 template <typename T>
 static void launch_rope(const RopeArgs& a, hipStream_t s) {
@@ -219,7 +216,7 @@ extern "C" int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
                           const void* q_norm_w, const void* k_norm_w, float eps,
                           int dtype, void* stream) {
   if (dtype != DA_BF16 && dtype != DA_FP16) return DA_ERR_DTYPE;
-  if (D != 64 && D != 128) return DA_ERR_HEAD_DIM;
+  if (!rope_dim_ok(D)) return DA_ERR_HEAD_DIM;
   if (B < 1 || S < 0) return DA_ERR_INVALID_ARG;
   if (S == 0) return DA_OK;
   if (!cos || !sin || !cs_str || cs_str[0] < 0 || cs_str[1] < D) return DA_ERR_INVALID_ARG;
@@ -232,7 +229,7 @@ extern "C" int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
   a.eps = eps; a.B = B; a.S = S; a.D = D;
   a.rows = a.q.rows + a.k.rows;
   if (a.rows == 0) return DA_OK;
-  if (a.rows * 8 / 256 > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
+  if (a.rows * rope_tpr(D) / 256 > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
   if (dtype == DA_BF16) launch_rope<__bf16>(a, s);
@@ -247,11 +244,11 @@ extern "C" int da_rope_qk_append(void* q, const int64_t q_str[3], int Hq,
                                  const void* cos, const void* sin, const int64_t cs_str[2],
                                  const void* q_norm_w, const void* k_norm_w, float eps,
                                  void* k_cache, const int64_t kc_str[3],
-                                 void* v_cache, const int64_t vc_str[3],
+                                 void* v_cache, const int64_t vc_str[3], int64_t max_len,
                                  const int64_t* pos, int dtype, void* stream) {
   if (dtype != DA_BF16 && dtype != DA_FP16) return DA_ERR_DTYPE;
-  if (D != 64 && D != 128) return DA_ERR_HEAD_DIM;
-  if (B < 1 || Hq < 1 || Hkv < 1) return DA_ERR_INVALID_ARG;
+  if (!rope_dim_ok(D)) return DA_ERR_HEAD_DIM;
+  if (B < 1 || Hq < 1 || Hkv < 1 || max_len < 1) return DA_ERR_INVALID_ARG;
   if (!q || !k || !v || !k_cache || !v_cache || !pos || !v_str || !kc_str || !vc_str)
     return DA_ERR_INVALID_ARG;
   if (!cos || !sin || !cs_str || cs_str[0] < 0 || cs_str[1] < D) return DA_ERR_INVALID_ARG;
@@ -265,7 +262,7 @@ extern "C" int da_rope_qk_append(void* q, const int64_t q_str[3], int Hq,
   if ((rc = rope_part(a.k, const_cast<void*>(k), k_str, Hkv, B, 1, k_norm_w)) != DA_OK) return rc;
   a.cos = cos; a.sin = sin; a.cs_b = cs_str[0]; a.cs_s = cs_str[1];
   a.eps = eps; a.B = B; a.S = 1; a.D = D;
-  a.pos = pos;
+  a.pos = pos; a.max_len = max_len;
   a.kc = k_cache; a.kc_b = kc_str[0]; a.kc_s = kc_str[1]; a.kc_h = kc_str[2];
   a.v = v; a.v_b = v_str[0]; a.v_s = v_str[1]; a.v_h = v_str[2];
   a.vc = v_cache; a.vc_b = vc_str[0]; a.vc_s = vc_str[1]; a.vc_h = vc_str[2];

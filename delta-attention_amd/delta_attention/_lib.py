@@ -59,7 +59,7 @@ EXPORTS = (
 
 _ERR_TEXT = {
     DA_ERR_INVALID_ARG: "invalid argument (shape, stride, range or null pointer)",
-    DA_ERR_HEAD_DIM: "unsupported head_dim (32, 64 and 128 are supported)",
+    DA_ERR_HEAD_DIM: "unsupported head_dim",
     DA_ERR_DTYPE: "unsupported dtype (bfloat16 and float16 are supported)",
     DA_ERR_ALIGNMENT: "tensor rows must be 16-byte aligned (strides multiple of 8 elements)",
     DA_ERR_WORKSPACE: "workspace missing or too small",
@@ -172,7 +172,7 @@ def _load() -> ctypes.CDLL:
                                        _f, _i, _i, _vp]
     L.da_rope_qk_append.restype = _i
     L.da_rope_qk_append.argtypes = [_vp, _p3, _i, _vp, _p3, _i, _vp, _p3, _i, _i, _vp, _vp,
-                                    _vp, _vp, _vp, _f, _vp, _p3, _vp, _p3, _vp, _i, _vp]
+                                    _vp, _vp, _vp, _f, _vp, _p3, _vp, _p3, _i64, _vp, _i, _vp]
     L.da_decode_scratch_bytes.restype = _sz
     L.da_decode_scratch_bytes.argtypes = []
     L.da_decode_attn_fwd_dev_noalloc.restype = _i

@@ -36,29 +36,39 @@ def drift_summary(dense_sparse_diff, layer_idx: int, gamma: int, seq_len: int) -
     }
 
 
+def _check_binning(summary: Dict[str, Any]) -> None:
+    """A summary binned differently from this module (another version wrote
+    it) cannot be summed with the others."""
+    bins, rng, hist = summary["hist_bins"], list(summary["hist_range"]), summary["hist"]
+    if bins != HIST_BINS or rng != list(HIST_RANGE) or len(hist) != HIST_BINS:
+        raise ValueError(
+            f"drift sidecar bins/range {bins}/{rng} do not match {HIST_BINS}/{list(HIST_RANGE)} "
+            "(mixed-version sidecar files)")
+
+
 def aggregate_drift(lines: Iterable[Dict[str, Any]]) -> Dict[int, Dict[str, Any]]:
-    """One entry per layer: n-weighted mean, summed histograms; mismatched bins
-    are an error (drift.py:52-77)."""
-    out: Dict[int, Dict[str, Any]] = {}
-    for s in lines:
-        if s["hist_bins"] != HIST_BINS or list(s["hist_range"]) != list(HIST_RANGE):
-            raise ValueError(
-                f"drift sidecar bins/range {s['hist_bins']}/{s['hist_range']} do not match "
-                f"{HIST_BINS}/{list(HIST_RANGE)} (mixed-version sidecar files)")
-        layer = int(s["layer"])
-        agg = out.setdefault(layer, {"layer": layer, "n": 0, "mean": 0.0, "requests": 0,
-                                     "hist": [0] * HIST_BINS, "hist_bins": HIST_BINS,
-                                     "hist_range": list(HIST_RANGE), "gamma": s["gamma"]})
-        total = agg["n"] + s["n"]
-        if total > 0:
-            agg["mean"] = (agg["mean"] * agg["n"] + s["mean"] * s["n"]) / total
-        agg["n"] = total
-        agg["requests"] += 1
-        agg["hist"] = [x + y for x, y in zip(agg["hist"], s["hist"])]
-    return out
+    """Per-request summaries -> one entry per layer, the reference's schema
+    (drift.py:52-77): `n` and `hist` summed, `mean` the n-weighted mean (0.0
+    for a layer without cosines), `requests` the number of summaries, `gamma`
+    the first summary's. Pure Python; a summary with other bins is an error."""
+    groups: Dict[int, List[Dict[str, Any]]] = {}
+    for summary in lines:
+        _check_binning(summary)
+        groups.setdefault(int(summary["layer"]), []).append(summary)
+    result: Dict[int, Dict[str, Any]] = {}
+    for layer, group in groups.items():
+        n = sum(int(g["n"]) for g in group)
+        weighted = sum(float(g["mean"]) * int(g["n"]) for g in group)
+        result[layer] = {
+            "layer": layer, "n": n, "mean": weighted / n if n else 0.0,
+            "requests": len(group),
+            "hist": [sum(col) for col in zip(*(g["hist"] for g in group))],
+            "hist_bins": HIST_BINS, "hist_range": list(HIST_RANGE), "gamma": group[0]["gamma"],
+        }
+    return result
 
 
 def hist_bin_edges() -> List[float]:
+    """The HIST_BINS + 1 bin edges over HIST_RANGE (torch.histc's equal bins)."""
     lo, hi = HIST_RANGE
-    step = (hi - lo) / HIST_BINS
-    return [lo + i * step for i in range(HIST_BINS + 1)]
+    return [lo + (hi - lo) * i / HIST_BINS for i in range(HIST_BINS + 1)]

@@ -109,8 +109,13 @@ FUSED_MAX_ROWS = 64
 def fused_params(fused, mods, rows: int = 1):
     """(weight, bias) of a fuse_linears product while every module's parameters
     are still its slices and the input has at most FUSED_MAX_ROWS rows;
-    (None, None) otherwise."""
+    (None, None) otherwise. The fused buffer is not an autograd leaf, so with
+    gradients enabled for any of the modules' parameters the separate products
+    (which give each parameter its gradient) are used."""
     if fused is None or rows > FUSED_MAX_ROWS:
+        return None, None
+    if torch.is_grad_enabled() and any(
+            p.requires_grad for m in mods for p in (m.weight, m.bias) if p is not None):
         return None, None
     w, b = fused
     o = 0
@@ -234,7 +239,10 @@ class LlamaAttention(nn.Module):
         b, h, s, d = query_states.size()
         assert h == cfg.num_attention_heads, (h, s)
 
-        if getattr(cfg, "stride_policy", "fixed") == "adaptive" and mode == "delta":
+        # the reference's branch order (llama.py:695-711): "sparse-only" returns
+        # the sparse pass, then the adaptive policy replaces the uniform stride
+        # for every other mode ("recompute" included)
+        if getattr(cfg, "stride_policy", "fixed") == "adaptive" and mode != "sparse-only":
             sparse, _ = self.hip_attention_interface(self, query_states, key_states, value_states,
                                                      attention_mask, scaling=scaling,
                                                      sliding_window=window)

@@ -392,11 +392,13 @@ def rope_qk_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch
                    k_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6) -> None:
     """One-token decode step: rope_qk on q (in place) and k, with the rotated k
     and v written to the [B, max_len, Hkv, D] caches at row pos (int64 [1] on
-    the device) instead of a separate cache update. q/k/v [B, 1, H, D]."""
+    the device) instead of a separate cache update. q/k/v [B, 1, H, D]. A pos
+    outside [0, max_len) when the kernel runs leaves both caches unchanged."""
     B, S, Hq, D = q.shape
     Hkv = k.shape[2]
     assert S == 1 and k.shape == (B, 1, Hkv, D) and v.shape == k.shape
     assert k_cache.shape[0] == B and k_cache.shape[2:] == (Hkv, D) and v_cache.shape == k_cache.shape
+    assert k_cache.dtype == v_cache.dtype == q.dtype
     dev = _on_gpu(q, k, v, k_cache, v_cache, pos)
     assert pos.dtype == torch.int64 and pos.numel() == 1
     cos = cos.to(device=dev, dtype=q.dtype)
@@ -412,7 +414,7 @@ def rope_qk_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch
             _ptr(q), _s3(q, 0, 1, 2), Hq, _ptr(k), _s3(k, 0, 1, 2), Hkv, _ptr(v), _s3(v, 0, 1, 2),
             B, D, _ptr(cos), _ptr(sin), cs, _ptr(ws[0]), _ptr(ws[1]), float(eps),
             _ptr(k_cache), _s3(k_cache, 0, 1, 2), _ptr(v_cache), _s3(v_cache, 0, 1, 2),
-            _ptr(pos), _code(q), _stream(dev))
+            int(k_cache.shape[1]), _ptr(pos), _code(q), _stream(dev))
     L.check(rc, "da_rope_qk_append")
 
 

@@ -37,7 +37,7 @@ extern "C" {
 
 #define DA_OK 0
 #define DA_ERR_INVALID_ARG (-1)      /* shape, stride, range or null-pointer error */
-#define DA_ERR_HEAD_DIM (-2)         /* head_dim not supported (32, 64 and 128 are; the RoPE prologue takes 64 and 128) */
+#define DA_ERR_HEAD_DIM (-2)         /* head_dim not supported (32, 64 and 128 are; the RoPE prologue also takes 256) */
 #define DA_ERR_DTYPE (-3)            /* dtype not DA_BF16 / DA_FP16 */
 #define DA_ERR_ALIGNMENT (-4)        /* pointer or stride breaks 16-byte row alignment */
 #define DA_ERR_WORKSPACE (-5)        /* workspace missing or smaller than required */
@@ -288,7 +288,9 @@ int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
  * place. pos is an int64 in device memory (a graph-recorded step reads the
  * current row at replay). Caches are [B, max_len, Hkv, D] with strides
  * kc_str / vc_str = {batch, row, head}; k and v [B, 1, Hkv, D] with k_str /
- * v_str = {batch, seq, head}. The caller keeps *pos below max_len.
+ * v_str = {batch, seq, head}. max_len (>= 1) is the caches' row count: a
+ * *pos outside [0, max_len) when the kernel runs writes neither cache (q is
+ * still rotated), so a runaway position cannot write past the caches.
  */
 int da_rope_qk_append(void* q, const int64_t q_str[3], int Hq,
                       const void* k, const int64_t k_str[3], int Hkv,
@@ -297,7 +299,7 @@ int da_rope_qk_append(void* q, const int64_t q_str[3], int Hq,
                       const void* cos, const void* sin, const int64_t cs_str[2],
                       const void* q_norm_w, const void* k_norm_w, float eps,
                       void* k_cache, const int64_t kc_str[3],
-                      void* v_cache, const int64_t vc_str[3],
+                      void* v_cache, const int64_t vc_str[3], int64_t max_len,
                       const int64_t* pos, int dtype, void* stream);
 
 /* Consecutive-anchor delta cosine (stride.py:43-52 interanchor_cos, the

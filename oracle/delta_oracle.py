@@ -29,6 +29,8 @@ prefill (file:line cite the reference, singhh5050/delta-attention):
                          each norm clamped to eps = 1e-8)
   histc                  drift.py:33: torch.histc's binning (bins over [lo, hi],
                          x == hi in the last bin, out-of-range and NaN dropped)
+  head_row_cos           the per-row cosine over the head dim of the reference's
+                         T1 gate (tests/test_math_identities.py:85)
   masked_attention_grads the attention backward that autograd forms for the
                          FlexAttention / masked SDPA branches of flex_delta.py:167-184
   compose_grads          the composition's backward (flex_delta.py:186-196, the
@@ -455,15 +457,6 @@ def rms_norm(x: np.ndarray, eps: float = 1e-6, weight: Optional[np.ndarray] = No
 
 # ---------------------------------------------------------------------------
 # metrics (validation.py:215-221)
-
-def row_cos(a: np.ndarray, b: np.ndarray) -> np.ndarray:
-    """Per-row cosine over flattened (h, d) of [B,s,H,d] arrays -> [B,s]."""
-    a = a.reshape(a.shape[0], a.shape[1], -1).astype(np.float64)
-    b = b.reshape(b.shape[0], b.shape[1], -1).astype(np.float64)
-    num = (a * b).sum(-1)
-    den = np.sqrt((a * a).sum(-1) * (b * b).sum(-1))
-    return num / np.maximum(den, 1e-300)
-
 
 def head_row_cos(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     """Cosine over the last dim only (tests/test_math_identities.py:85)."""

@@ -57,7 +57,7 @@ def _sparse(lib, **kw):
 def test_sparse_rejects_bad_arguments(lib):
     assert _sparse(lib, dtype=7) == L.DA_ERR_DTYPE
     assert _sparse(lib, D=96) == L.DA_ERR_HEAD_DIM
-    assert _sparse(lib, D=256) == L.DA_ERR_HEAD_DIM
+    assert _sparse(lib, D=512) == L.DA_ERR_HEAD_DIM
     assert _sparse(lib, Hq=6, Hkv=4) == L.DA_ERR_INVALID_ARG
     assert _sparse(lib, q=0) == L.DA_ERR_INVALID_ARG
     assert _sparse(lib, q=24) == L.DA_ERR_ALIGNMENT
@@ -119,7 +119,7 @@ def test_rope_checks(lib):
 
     assert call(dtype=5) == L.DA_ERR_DTYPE
     assert call(D=96) == L.DA_ERR_HEAD_DIM
-    assert call(D=32) == L.DA_ERR_HEAD_DIM       # the prologue takes 64 and 128 only
+    assert call(D=80) == L.DA_ERR_HEAD_DIM       # the prologue takes 32, 64, 128 and 256
     assert call(cos=0) == L.DA_ERR_INVALID_ARG
     assert call(cs=(0, 64)) == L.DA_ERR_INVALID_ARG          # table rows shorter than D
     assert call(cos=24) == L.DA_ERR_ALIGNMENT
@@ -302,6 +302,8 @@ def test_training_entry_checks(lib):
     assert sparse(lse=18) == L.DA_ERR_ALIGNMENT
     assert sparse(q=24) == L.DA_ERR_ALIGNMENT
     assert sparse(D=80) == L.DA_ERR_HEAD_DIM
+    assert sparse(D=256) == L.DA_ERR_HEAD_DIM    # the backward takes 32, 64 and 128
+    assert lib.da_sparse_attn_bwd_workspace_bytes(B, H, Hkv, S, 256, 256, 16, 64) == 0
     assert sparse(dtype=7) == L.DA_ERR_DTYPE
     assert sparse(q_block=0) == L.DA_ERR_INVALID_ARG
     assert sparse(k_row=1 << 23) == L.DA_ERR_INVALID_ARG     # row offsets beyond 32 bits
@@ -344,11 +346,13 @@ def test_rope_append_checks(lib):
     c3 = _s3(40 * 2 * 128, 2 * 128, 128)
     cs = (ctypes.c_int64 * 2)(0, 128)
 
-    def call(pos=16, D=128, dtype=L.DA_BF16, v=16, kc=16, cos=16):
+    def call(pos=16, D=128, dtype=L.DA_BF16, v=16, kc=16, cos=16, max_len=40):
         return lib.da_rope_qk_append(P(16), x3, 8, P(16), x3, 2, P(v) if v else None, x3, 1, D,
                                      P(cos) if cos else None, P(16), cs, None, None, 1e-6,
-                                     P(kc) if kc else None, c3, P(16), c3,
+                                     P(kc) if kc else None, c3, P(16), c3, max_len,
                                      P(pos) if pos else None, dtype, None)
+    assert call(max_len=0) == L.DA_ERR_INVALID_ARG     # the caches' row count
+    assert call(max_len=-5) == L.DA_ERR_INVALID_ARG
     assert call(pos=0) == L.DA_ERR_INVALID_ARG
     assert call(pos=20) == L.DA_ERR_ALIGNMENT          # int64 position
     assert call(v=0) == L.DA_ERR_INVALID_ARG

@@ -35,6 +35,7 @@ def _rand(B, H, Hkv, n, D, seed, dtype=torch.bfloat16):
     (1, 40, 8, 5000, 128, 4096, 64),     # GQA 5
     (1, 32, 8, 131072, 128, 2048, 128),  # 128K cache, sparse
     (1, 32, 8, 131072, 128, 0, 0),       # 128K cache, dense
+    (1, 8, 2, 6000, 256, 1024, 64),      # head_dim 256
 ])
 def test_decode_row_parity(gpu, B, H, Hkv, n, D, window, sink):
     from delta_attention import ops

@@ -172,8 +172,40 @@ def test_qsparse_head_dim_32(gpu, dtype):
     assert_close(np64(out), ref, what="qsa d32 unsorted")
 
 
-def test_head_dim_256_is_refused(gpu):
-    from delta_attention.delta_kernel import attention
-    q = torch.zeros(1, 2, 8, 256, device="cuda", dtype=torch.bfloat16)
-    with pytest.raises(AssertionError, match="no MI355X kernel"):
-        attention(q, q, q, torch.arange(8, device="cuda")[None], 0.1)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_qsparse_head_dim_256(gpu, dtype):
+    """delta_kernel.attention with head_dim 256 (accepted by the reference's
+    wrapper, delta_kernel.py:268; one workgroup per CU): sorted rows over a
+    long key range (several split items per row tile), an unsorted mask, and
+    expanded K/V equal to native GQA bit for bit."""
+    q, k, v = gen_qkv(1, 8, 2, 2500, 256, seed=11, dtype=dtype)
+    rows = torch.tensor([0, 5, 63, 64, 700, 1999, 2400, 2499], device="cuda")
+    out = _qsa(q[:, :, rows], k, v, rows.unsqueeze(0), 256 ** -0.5)
+    ref = O.qsparse_attention(np64(q)[:, :, rows.cpu().numpy()], np64(k), np64(v),
+                              rows.cpu().numpy(), 256 ** -0.5)
+    assert_close(np64(out), ref, what=f"qsa d256 {dtype}")
+    mask = torch.randperm(2500, generator=torch.Generator().manual_seed(4))[:300].unsqueeze(0)
+    out = _qsa(q[:, :, :300], k, v, mask.cuda(), 256 ** -0.5)
+    ref = O.qsparse_attention(np64(q)[:, :, :300], np64(k), np64(v), mask[0].numpy(), 256 ** -0.5)
+    assert_close(np64(out), ref, what="qsa d256 unsorted")
+    ke, ve = (t.repeat_interleave(4, dim=1) for t in (k, v))
+    assert torch.equal(_qsa(q[:, :, :300], ke, ve, mask.cuda(), 256 ** -0.5), out)
+
+
+def test_sparse_attention_head_dim_256(gpu):
+    _sparse_case(1, 8, 2, 1100, 256, 300, 16)
+    _sparse_case(2, 4, 4, 400, 256, 128, 0, dtype=torch.float16)
+
+
+def test_attention_fp32_inputs(gpu):
+    """float32 callers of delta_kernel.attention (the reference's Triton
+    kernel takes them): the rows run in bf16 and come back as float32
+    (llama.py:383-388, 493-494), within the bf16 gate of the float64 result."""
+    g = torch.Generator().manual_seed(12)
+    q, k, v = (torch.randn(1, h, 900, 128, generator=g).cuda() for h in (8, 2, 2))
+    rows = torch.tensor([3, 64, 500, 899], device="cuda")
+    out = _qsa(q[:, :, rows], k, v, rows.unsqueeze(0), 128 ** -0.5)
+    assert out.dtype == torch.float32 and out.shape == (1, 8, 4, 128)
+    ref = O.qsparse_attention(np64(q)[:, :, rows.cpu().numpy()], np64(k), np64(v),
+                              rows.cpu().numpy(), 128 ** -0.5)
+    assert_close(np64(out), ref, what="qsa fp32 inputs")

@@ -34,6 +34,8 @@ def _layer(B, H, Hkv, S, D, gamma, window, sink, mode="delta", seed=0, dtype=tor
     (1, 4, 1, 768, 64, 128, 192, 0),      # gamma 128
     (1, 8, 2, 1300, 32, 64, 256, 16),     # head_dim 32 (fused order)
     (1, 4, 4, 900, 32, 128, 128, 8),      # head_dim 32, gamma 128 with MHA (fused, 128-row tiles)
+    (1, 8, 2, 1500, 256, 64, 384, 16),    # head_dim 256 (one workgroup per CU), fused order
+    (1, 4, 4, 700, 256, 32, 128, 4),      # head_dim 256, MHA: one head per 128-row tile
 ])
 def test_delta_prefill_parity(gpu, B, H, Hkv, S, D, gamma, window, sink):
     got, ref, _ = _layer(B, H, Hkv, S, D, gamma, window, sink)
@@ -146,10 +148,13 @@ def test_module_forward_and_qwen3(gpu):
         assert_close(np64(y)[0], y_ref[0], cos_min=0.99, atol=5e-2, what=f"{cls.__name__} forward")
 
 
-def test_adaptive_stride_path(gpu):
+@pytest.mark.parametrize("mode", ["delta", "recompute"])
+def test_adaptive_stride_path(gpu, mode):
+    """The adaptive policy in the reference's branch order (llama.py:695-711):
+    it replaces the uniform stride for "delta" and for "recompute" alike."""
     from delta_attention.llama import LlamaAttention
     cfg = _cfg(4, 2, 128, stride_policy="adaptive", adapt_chunk=512, delta_lambda=64,
-               adapt_threshold=0.5, gamma_min=16, gamma_max=128)
+               adapt_threshold=0.5, gamma_min=16, gamma_max=128, mode=mode)
     m = LlamaAttention(cfg, layer_idx=0).cuda().to(torch.bfloat16)
     s = 2048
     q, k, v = gen_qkv(1, 4, 2, s, 128, seed=8)
@@ -169,7 +174,21 @@ def test_adaptive_stride_path(gpu):
     dense_sel = O.causal_attention_rows(qn, kn, vn, idx, scale)
     tail = O.causal_attention_rows(qn, kn, vn, np.arange(s_p, s), scale)
     ref = np.concatenate([O.apply_delta_variable(sparse, dense_sel, idx, s_p), tail], 1)
-    assert_close(np64(out), ref, what="adaptive")
+    assert_close(np64(out), ref, what=f"adaptive ({mode})")
+
+
+def test_adaptive_policy_sparse_only_returns_the_sparse_pass(gpu):
+    """mode "sparse-only" returns before the adaptive branch (llama.py:695-696)."""
+    from delta_attention.llama import LlamaAttention
+    cfg = _cfg(4, 2, 128, stride_policy="adaptive", adapt_chunk=512, delta_lambda=64,
+               adapt_threshold=0.5, gamma_min=16, gamma_max=128, mode="sparse-only")
+    m = LlamaAttention(cfg, layer_idx=0).cuda().to(torch.bfloat16)
+    q, k, v = gen_qkv(1, 4, 2, 1024, 128, seed=9)
+    out, _ = m.delta_forward(m, q, k, v, None, scaling=m.scaling)
+    torch.cuda.synchronize()
+    assert getattr(m, "_stride_stats", None) is None   # no adaptive pass ran
+    ref = O.sparse_attention(np64(q), np64(k), np64(v), 256, 16, 128 ** -0.5)
+    assert_close(np64(out), ref, what="adaptive policy, sparse-only")
 
 
 @pytest.mark.parametrize("B,H,Hkv,S,D,gamma,window,sink", [
@@ -181,6 +200,7 @@ def test_adaptive_stride_path(gpu):
     (2, 10, 2, 1100, 128, 64, 256, 16),   # GQA 5 (Qwen3): one head per 128-row tile
     (1, 8, 2, 1500, 128, 128, 256, 16),   # GQA 4, gamma 128: one head per 128-row tile,
                                           # against kernel (1)'s two-head packing
+    (1, 8, 2, 1000, 256, 64, 256, 16),    # head_dim 256
 ])
 def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
     """Kernel (3) fused into kernel (1)'s epilogue (kernel (2) first) gives the

@@ -35,7 +35,7 @@ def _tables(B, S, D, dtype, per_batch):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("D", [128, 64, 32, 256])
 @pytest.mark.parametrize("per_batch", [False, True])
 def test_rope_bit_exact(gpu, dtype, D, per_batch):
     from delta_attention import ops
@@ -51,7 +51,7 @@ def test_rope_bit_exact(gpu, dtype, D, per_batch):
     assert torch.equal(buf[..., (Hq + Hkv) * D:], v_before)     # v untouched
 
 
-@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("D", [128, 64, 32, 256])
 def test_rope_matches_oracle_bf16(gpu, D):
     from delta_attention import ops
     B, S, Hq, Hkv = 1, 200, 4, 1
@@ -75,11 +75,13 @@ def _within_one_rounding(got, ref, what):
     assert exact > 0.97, (what, exact)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_rope_with_qk_norm(gpu, dtype):
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 128),
+                                     (torch.bfloat16, 64), (torch.bfloat16, 32),
+                                     (torch.float16, 256)])
+def test_rope_with_qk_norm(gpu, dtype, D):
     from delta_attention import ops
     from delta_attention.llama import LlamaRMSNorm, apply_rotary_pos_emb
-    B, S, Hq, Hkv, D = 2, 257, 10, 2, 128
+    B, S, Hq, Hkv = 2, 257, 10, 2
     _, q, k = _proj_views(B, S, Hq, Hkv, D, dtype, seed=9)
     qn, kn = LlamaRMSNorm(D, 1e-6).cuda().to(dtype), LlamaRMSNorm(D, 1e-6).cuda().to(dtype)
     with torch.no_grad():
@@ -134,24 +136,30 @@ def test_module_fused_prologue_matches_torch_prologue(gpu):
 
 
 @pytest.mark.parametrize("norm", [False, True])
-def test_rope_qk_append_equals_rope_then_cache_update(gpu, norm):
+@pytest.mark.parametrize("D,dtype,pos", [
+    (128, torch.bfloat16, 17), (128, torch.bfloat16, 0), (128, torch.bfloat16, 39),
+    (64, torch.bfloat16, 39), (64, torch.float16, 0), (128, torch.float16, 39),
+    (32, torch.bfloat16, 5), (256, torch.float16, 39),
+])
+def test_rope_qk_append_equals_rope_then_cache_update(gpu, norm, D, dtype, pos):
     """The one-token decode prologue with the cache append in the same launch:
     q rotated in place and the cache rows at the device-held position hold
     exactly what rope_qk followed by the cache update (index_copy_) writes;
-    other cache rows untouched."""
+    other cache rows untouched. Positions 0 and L_max - 1 (the last cache row)
+    included."""
     from delta_attention import ops
     from delta_attention.llama import rope_cos_sin
-    B, Hq, Hkv, D, L_max, pos = 2, 8, 2, 128, 40, 17
-    print(f"rope append B{B} H{Hq}/{Hkv} D{D} pos {pos} norm {norm}", flush=True)
+    B, Hq, Hkv, L_max = 2, 8, 2, 40
+    print(f"rope append B{B} H{Hq}/{Hkv} D{D} {dtype} pos {pos} norm {norm}", flush=True)
     g = torch.Generator(device="cuda").manual_seed(3)
-    qkv = torch.randn(B, 1, (Hq + 2 * Hkv) * D, device="cuda", generator=g).to(torch.bfloat16)
+    qkv = torch.randn(B, 1, (Hq + 2 * Hkv) * D, device="cuda", generator=g).to(dtype)
     q = qkv[..., :Hq * D].unflatten(-1, (Hq, D))
     k = qkv[..., Hq * D:(Hq + Hkv) * D].unflatten(-1, (Hkv, D))
     v = qkv[..., (Hq + Hkv) * D:].unflatten(-1, (Hkv, D))
-    cos, sin = rope_cos_sin(torch.full((1, 1), pos, device="cuda"), D, 5e5, torch.bfloat16)
-    w = [torch.rand(D, device="cuda", generator=g).to(torch.bfloat16) + 0.5 for _ in range(2)] if norm else [None, None]
-    kc = torch.randn(B, L_max, Hkv, D, device="cuda", generator=g).to(torch.bfloat16)
-    vc = torch.randn(B, L_max, Hkv, D, device="cuda", generator=g).to(torch.bfloat16)
+    cos, sin = rope_cos_sin(torch.full((1, 1), pos, device="cuda"), D, 5e5, dtype)
+    w = [torch.rand(D, device="cuda", generator=g).to(dtype) + 0.5 for _ in range(2)] if norm else [None, None]
+    kc = torch.randn(B, L_max, Hkv, D, device="cuda", generator=g).to(dtype)
+    vc = torch.randn(B, L_max, Hkv, D, device="cuda", generator=g).to(dtype)
     kc2, vc2 = kc.clone(), vc.clone()
     q_ref, k_ref = q.clone(), k.clone()
     ops.rope_qk(q_ref, k_ref, cos, sin, q_norm_w=w[0], k_norm_w=w[1], eps=1e-6)
@@ -164,3 +172,27 @@ def test_rope_qk_append_equals_rope_then_cache_update(gpu, norm):
     assert torch.equal(q, q_ref)
     assert torch.equal(k, k_before)            # k itself is not modified
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+
+
+@pytest.mark.parametrize("pos", [40, -1])
+def test_rope_qk_append_position_outside_the_caches(gpu, pos):
+    """A device-held position outside [0, max_len) is caught by the kernel's
+    own bound: q is rotated as usual, k is kept, and neither cache changes."""
+    from delta_attention import ops
+    from delta_attention.llama import rope_cos_sin
+    B, Hq, Hkv, D, L_max = 1, 8, 2, 128, 40
+    print(f"rope append out-of-range pos {pos}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn(B, 1, Hq, D, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(B, 1, Hkv, D, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(B, 1, Hkv, D, device="cuda", generator=g).to(torch.bfloat16)
+    cos, sin = rope_cos_sin(torch.full((1, 1), 7, device="cuda"), D, 5e5, torch.bfloat16)
+    kc = torch.randn(B, L_max, Hkv, D, device="cuda", generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, L_max, Hkv, D, device="cuda", generator=g).to(torch.bfloat16)
+    kc0, vc0, k0 = kc.clone(), vc.clone(), k.clone()
+    q_ref = q.clone()
+    ops.rope_qk(q_ref, None, cos, sin)
+    ops.rope_qk_append(q, k, v, cos, sin, kc, vc, torch.tensor([pos], device="cuda"))
+    torch.cuda.synchronize()
+    assert torch.equal(q, q_ref) and torch.equal(k, k0)
+    assert torch.equal(kc, kc0) and torch.equal(vc, vc0)

@@ -97,7 +97,29 @@ def test_aggregate_drift():
     assert agg[3]["hist"][30] == 64 and sum(agg[3]["hist"]) == 64
     with pytest.raises(ValueError):
         drift.aggregate_drift([dict(s, hist_bins=10)])
-    assert len(drift.hist_bin_edges()) == drift.HIST_BINS + 1
+    with pytest.raises(ValueError):
+        drift.aggregate_drift([dict(s, hist=hist[:-1])])
+    # several layers, unequal weights, an empty request
+    h2 = [0] * drift.HIST_BINS
+    h2[0], h2[39] = 5, 3
+    agg = drift.aggregate_drift([s, dict(s, layer=7, n=8, mean=-0.25, hist=h2),
+                                 dict(s, n=96, mean=0.1), dict(s, layer=7, n=0, mean=0.9,
+                                                               hist=[0] * drift.HIST_BINS)])
+    assert sorted(agg) == [3, 7]
+    assert agg[3]["mean"] == pytest.approx((32 * 0.5 + 96 * 0.1) / 128) and agg[3]["n"] == 128
+    assert agg[7]["mean"] == pytest.approx(-0.25) and agg[7]["requests"] == 2
+    assert agg[7]["hist"] == h2 and agg[7]["gamma"] == 64
+    assert drift.aggregate_drift([dict(s, n=0)])[3]["mean"] == 0.0
+    assert set(agg[3]) == {"layer", "n", "mean", "requests", "hist", "hist_bins", "hist_range",
+                           "gamma"}
+    # the edges are torch.histc's: a value just inside each edge lands in that bin
+    edges = drift.hist_bin_edges()
+    np.testing.assert_allclose(edges, np.linspace(*drift.HIST_RANGE, drift.HIST_BINS + 1),
+                               rtol=0, atol=1e-15)
+    probe = torch.tensor(edges[:-1], dtype=torch.float64) + 1e-9
+    counts = torch.histc(probe, bins=drift.HIST_BINS, min=drift.HIST_RANGE[0],
+                         max=drift.HIST_RANGE[1])
+    assert counts.tolist() == [1.0] * drift.HIST_BINS
 
 
 def test_product_ops_refuse_cpu_tensors():
@@ -145,11 +167,40 @@ def test_fused_projections_are_views():
     mlp.fuse_projections()
     assert list(at.state_dict()) == keys
     assert all(torch.equal(at.state_dict()[k], vals[k]) for k in keys)
-    torch.testing.assert_close(at._qkv_product(x), ref)
-    assert at._qkv_product(torch.randn(FUSED_MAX_ROWS + 1, 256)) is None
     with torch.no_grad():
+        torch.testing.assert_close(at._qkv_product(x), ref)
+        assert at._qkv_product(torch.randn(FUSED_MAX_ROWS + 1, 256)) is None
         g = mlp.forward(x)
         mlp._gate_up_fused = None
         torch.testing.assert_close(g, mlp.forward(x))
+    assert at._qkv_product(x) is None           # gradients wanted: separate products
     at.k_proj.weight = torch.nn.Parameter(at.k_proj.weight.detach().clone())
-    assert at._qkv_product(x) is None
+    with torch.no_grad():
+        assert at._qkv_product(x) is None
+
+
+def test_fused_projection_params_keep_gradients():
+    """fuse_linears re-points the modules' weights at slices of one buffer
+    that is not an autograd leaf: with gradients enabled (and parameters that
+    require them) fused_params declines, so the separate products run and
+    every parameter gets its gradient; under no_grad the fused product is used."""
+    import torch
+    from torch import nn
+    from delta_attention.llama import fuse_linears, fused_params
+    torch.manual_seed(0)
+    mods = [nn.Linear(16, n, bias=False) for n in (8, 4, 4)]
+    fused = fuse_linears(*mods)
+    assert fused_params(fused, mods, rows=1) == (None, None)
+    with torch.no_grad():
+        w, b = fused_params(fused, mods, rows=1)
+        assert w is fused[0] and b is None
+        assert fused_params(fused, mods, rows=65) == (None, None)   # long inputs: separate GEMMs
+    for m in mods:
+        m.weight.requires_grad_(False)
+    w, _ = fused_params(fused, mods, rows=1)
+    assert w is fused[0]
+    for m in mods:
+        m.weight.requires_grad_(True)
+    x = torch.randn(2, 16)
+    sum(m(x).sum() for m in mods).backward()
+    assert all(m.weight.grad is not None for m in mods)

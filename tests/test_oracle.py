@@ -419,3 +419,27 @@ def test_histc_edges_and_library():
     y = rng.uniform(-1.2, 1.2, 3000).astype(np.float32)
     ref = torch.histc(torch.from_numpy(y), bins=40, min=-1.0, max=1.0).numpy().astype(np.int64)
     np.testing.assert_array_equal(O.histc(y, 40, -1.0, 1.0), ref)
+
+
+def test_head_row_cos_against_library_and_closed_forms():
+    """The smoke check's cosine (over the head dim, T1's gate at
+    tests/test_math_identities.py:85) against torch's cosine_similarity in
+    float64 and the closed forms: parallel rows give 1, opposite rows -1,
+    orthogonal rows 0, and scaling a row leaves it unchanged. A planted
+    mistake (the norms without the square root) fails the library check."""
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((2, 5, 3, 64))
+    b = rng.standard_normal((2, 5, 3, 64))
+    got = O.head_row_cos(a, b)
+    ref = torch.nn.functional.cosine_similarity(torch.from_numpy(a), torch.from_numpy(b),
+                                                dim=-1).numpy()
+    assert got.shape == (2, 5, 3)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-13)
+    np.testing.assert_allclose(O.head_row_cos(a, 3.5 * a), 1.0, atol=1e-14)
+    np.testing.assert_allclose(O.head_row_cos(a, -a), -1.0, atol=1e-14)
+    e0, e1 = np.zeros((1, 64)), np.zeros((1, 64))
+    e0[0, 3], e1[0, 9] = 2.0, -5.0
+    assert O.head_row_cos(e0, e1)[0] == 0.0
+    np.testing.assert_allclose(O.head_row_cos(a, b), O.head_row_cos(0.01 * a, 40 * b), atol=1e-13)
+    no_sqrt = (a * b).sum(-1) / ((a * a).sum(-1) * (b * b).sum(-1))
+    assert np.abs(no_sqrt - ref).max() > 0.1
