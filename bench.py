@@ -128,17 +128,55 @@ def make_inputs(a, device):
     return q, k, v
 
 
+def cpu_threads():
+    """Host threads for the CPU oracle: the cores this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS when it is set (the CPU
+    share of a shared GPU box). -> (threads, affinity count)."""
+    aff = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    n = min(aff, int(cap)) if cap.isdigit() and int(cap) > 0 else aff
+    return n, aff
+
+
+def cpu_c1(O, np, runs=3):
+    """The CPU configuration in full (batch 1, 8/2 heads, head_dim 64, seq
+    4096, fp32, window 512 + 64 sinks, gamma 16), q/k/v ~ N(0,1) from a CPU
+    generator seeded 0 in q, k, v order (validation.py:133-145): the oracle's
+    delta_forward, one warm-up then the median of `runs` timed runs."""
+    import torch
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, h, 4096, 64, generator=g).numpy() for h in (8, 2, 2))
+    scale = 64 ** -0.5
+    O.delta_forward(q, k, v, 16, 512, 64, scale)
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        O.delta_forward(q, k, v, 16, 512, 64, scale)
+        ts.append(time.perf_counter() - t0)
+    flops = (O.flops_sparse(1, 8, 64, 4096, 512, 64)
+             + O.flops_qsparse(1, 8, 64, O.selected_rows(4096, 16)))
+    t = statistics.median(ts)
+    return {"workload": "cpu configuration in full: B1, 8/2 heads, d64, s4096, fp32, "
+                        "window 512 + 64 sinks, gamma 16",
+            "ms": round(t * 1e3, 2), "tflops": round(flops / t / 1e12, 6), "flop": flops,
+            "runs": runs, "warmup": 1, "stat": "median"}
+
+
 def cpu_baseline(a, q, k, v, flops_layer):
     """The CPU oracle (numpy, BLAS threads) on a bounded sample of the same
     workload: the key-sparse pass for a block of rows and the dense pass for
-    the longest anchor rows, both on the heads of one kv group."""
+    the longest anchor rows, both on the heads of one kv group, plus the CPU
+    configuration run in full. BLAS and torch threads are set to cpu_threads()."""
     import numpy as np
+    import torch
     from oracle import delta_oracle as O
+    cores, aff = cpu_threads()
+    torch.set_num_threads(cores)
     try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        from threadpoolctl import threadpool_limits
+        limits = threadpool_limits(limits=cores)
     except Exception:  # pragma: no cover
-        cores = 1
+        limits = None
     G = a.heads // a.kv_heads
     S, D = a.seq, a.head_dim
     scale = D ** -0.5
@@ -169,12 +207,18 @@ def cpu_baseline(a, q, k, v, flops_layer):
         i -= 8
     dt = time.perf_counter() - t0
     tflops = flops / dt / 1e12
+    c1 = cpu_c1(O, np)
+    if limits is not None:
+        limits.unregister()
     return {
         "value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(cores), "kind": "port",
-        "sample": (f"oracle/delta_oracle.py (numpy fp32, BLAS) on heads 0-{G - 1} (kv group 0): "
-                   f"key-sparse pass over {n_rows} rows from row {S // 2} plus the dense pass over "
-                   f"the last {n_dense} anchor rows; {flops / 1e9:.1f} GFLOP in {dt:.1f} s; "
-                   f"full-layer time at this rate {flops_layer / (tflops * 1e12):.0f} s"),
+        "affinity_cores": int(aff),
+        "sample": (f"oracle/delta_oracle.py (numpy fp32, BLAS on {cores} threads) on heads "
+                   f"0-{G - 1} (kv group 0) of this workload: key-sparse pass over {n_rows} rows "
+                   f"from row {S // 2} plus the dense pass over the last {n_dense} anchor rows; "
+                   f"{flops / 1e9:.1f} GFLOP in {dt:.1f} s"),
+        "full_layer_s_extrapolated": round(flops_layer / (tflops * 1e12), 1),
+        "c1_full": c1,
     }
 
 
@@ -459,6 +503,10 @@ class GpuState:
         return out
 
 
+TRAFFIC_SOURCE = ("profiles/hbm_traffic_llama8b_128k.md: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
+                  "of this workload, scaled by a 1 GiB copy; committed, not measured in this run")
+
+
 def load_traffic(name):
     """HBM bytes per launch of `name` from the committed rocprofv3 PMC summary."""
     path = os.path.join(REPO, "profiles", "hbm_traffic.json")
@@ -671,7 +719,9 @@ def main():
     achieved = kernels[dom]["tflops"]
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": kernels[dom]["traffic"]}
+                "traffic": kernels[dom]["traffic"],
+                "traffic_source": (TRAFFIC_SOURCE if kernels[dom]["traffic"] is not None
+                                   else None)}
     # the published peak is quoted at the 2400 MHz maximum engine clock; the
     # fraction of the peak at the clock the GPU actually held is given beside it
     st = gpu_state.summary()
@@ -688,7 +738,8 @@ def main():
         "metric": METRIC, "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": ("synthetic (seeded N(0,1) q/k/v" + ("" if a.no_q_scale else ", q*d^-0.5")
+        "data": ("synthetic (N(0,1) q/k/v from torch's device generator seeded "
+                 f"{a.seed}, drawn q, k, v" + ("" if a.no_q_scale else ", q*d^-0.5")
                  + (", per-head q/k RMSNorm" if a.qk_norm else "")
                  + f", RoPE theta {a.rope_theta:g}, bf16)"),
         "config": {"workload": a.workload or (
