@@ -122,6 +122,11 @@ struct AttnArgs {
   // MODE_SPARSE: optional row log-sum-exp [B, Hq, n_rows] (log2 domain of the
   // scaled scores, +inf for a row without visible keys), for the backward
   float* lse;
+  // divisions by the launch's fixed divisors: n_hs, n_mtiles, n_splits, Hkv,
+  // Gs (heads per row tile), q_block, gamma
+  FastDiv fd_hs, fd_mt, fd_sp, fd_hkv, fd_gt, fd_qb, fd_gamma;
+  int tile_rows;    // BM / Gs: query rows per row tile
+  int n_grp;        // MODE_FUSED: stride groups per row tile (tile_rows / gamma)
 };
 
 // Bytes of LDS that hold a fused tile's dense anchor rows, prefetched with the
@@ -217,37 +222,39 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   int mt, split = 0, bh, hs = 0;
   if (KSPARSE) {
     // head split innermost: the tiles of one row block share K/V in L2
-    hs = w % a.n_hs;
-    const int t = w / a.n_hs;
-    mt = t % a.n_mtiles;
-    bh = t / a.n_mtiles;
+    const int t = (int)fdiv(w, a.fd_hs);
+    hs = (int)fmodq(w, t, a.fd_hs);
+    bh = (int)fdiv(t, a.fd_mt);
+    mt = (int)fmodq(t, bh, a.fd_mt);
   } else {
-    mt = w % a.n_mtiles;
-    const int t = w / a.n_mtiles;
-    split = t % a.n_splits;
-    bh = t / a.n_splits;
+    const int t = (int)fdiv(w, a.fd_mt);
+    mt = (int)fmodq(w, t, a.fd_mt);
+    bh = (int)fdiv(t, a.fd_sp);
+    split = (int)fmodq(t, bh, a.fd_sp);
   }
-  const int hk = bh % a.Hkv;
-  const int b = bh / a.Hkv;
+  const int b = (int)fdiv(bh, a.fd_hkv);
+  const int hk = (int)fmodq(bh, b, a.fd_hkv);
   const int G = a.G;
   const int GT = KSPARSE ? a.Gs : G;   // heads packed in this row tile
   const int n_kv = (KSPARSE || !a.n_kv_dev) ? a.n_kv : min(max(*a.n_kv_dev, 1), a.n_kv);
   // Fused epilogue: a tile wholly in the dense tail writes nothing. The other
   // tiles keep the row grouping of the plain launch (the wave-wide rescale
   // decisions, hence the rounded results, are the same).
-  if (MODE == MODE_FUSED && mt * (BM / GT) >= a.s_p) return;
+  if (MODE == MODE_FUSED && mt * a.tile_rows >= a.s_p) return;
 
   // ---- this lane's (query row, head): flattened pair mt * BM + 32 * wave + ln
   //      of the tile's GT heads hk * G + hs * GT + (0 .. GT-1) ----
   const int mflat = mt * BM + wave * 32 + ln;
   const bool valid = mflat < a.n_rows * GT;
-  const int irow = valid ? mflat / GT : 0;
-  const int hrow = hk * G + hs * GT + (valid ? mflat % GT : 0);
+  const int mq = (int)fdiv(mflat, a.fd_gt);
+  const int irow = valid ? mq : 0;
+  const int hin = valid ? (int)fmodq(mflat, mq, a.fd_gt) : 0;   // head within the tile
+  const int hrow = hk * G + hs * GT + hin;
   int qrow, lo, hi;
   if (KSPARSE) {
     qrow = irow;
     hi = valid ? irow : -1;
-    lo = (irow / a.q_block) * a.q_block + a.q_block - a.window;
+    lo = (int)fdiv(irow, a.fd_qb) * a.q_block + a.q_block - a.window;
   } else {
     // row_last == NULL: every row sees all keys (a decode row at the end of
     // the cache); window > 0: the row sees sinks + its last `window` keys
@@ -276,12 +283,12 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   if (KSPARSE) {
     // the tile holds rows r0 .. r1 (BM / GT of them, the last tile fewer);
     // hi = row and lo grow with the row
-    const int r0 = mt * (BM / GT);
-    const int r1 = min(r0 + BM / GT, a.n_rows) - 1;
+    const int r0 = mt * a.tile_rows;
+    const int r1 = min(r0 + a.tile_rows, a.n_rows) - 1;
     hi_min = r0;
     hi_max = r1;
-    lo_min = (r0 / a.q_block) * a.q_block + a.q_block - a.window;
-    lo_max = (r1 / a.q_block) * a.q_block + a.q_block - a.window;
+    lo_min = (int)fdiv(r0, a.fd_qb) * a.q_block + a.q_block - a.window;
+    lo_max = (int)fdiv(r1, a.fd_qb) * a.q_block + a.q_block - a.window;
   } else {
     int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
     int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   tile_list(hi_max, lo_min, sink, n_first, second_t0, n_second);
   int nt = n_first + n_second, t_off = 0;
   if (!KSPARSE) {
-    const int chunk = a.n_kv_dev ? max(1, (nt + a.n_splits - 1) / a.n_splits) : a.chunk;
+    const int chunk = a.n_kv_dev ? max(1, (int)fdiv(nt + a.n_splits - 1, a.fd_sp)) : a.chunk;
     t_off = split * chunk;
     if (t_off >= nt) return;   // past the list: the merge skips this split
     nt = min(chunk, nt - t_off);
@@ -545,12 +552,12 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   // tile's anchors point beyond the buffer and read as zero.
   bool pre = false;
   if constexpr (MODE == MODE_FUSED) {
-    const int n_grp = (BM / GT) / a.gamma;
+    const int n_grp = a.n_grp;
     pre = n_grp * GT * D * (int)esz <= DPRE_BYTES;
     if (pre) {
-      const int g0 = mt * (BM / GT) / a.gamma;
+      const int g0 = mt * n_grp;
       const int slot = tid / DCH, ch = tid % DCH;
-      const int gl = slot / GT, hl = slot % GT;
+      const int gl = (int)fdiv(slot, a.fd_gt), hl = (int)fmodq(slot, gl, a.fd_gt);
       const int64_t span = ((int64_t)(a.n_anchor - 1) * a.dsel_a + (int64_t)(a.Hq - 1) * a.dsel_h + D) * esz;
       const char* dbase = (const char*)a.dsel + (int64_t)b * a.dsel_b * esz;
       const __amdgpu_buffer_rsrc_t rd =
@@ -622,9 +629,9 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   // tile's rows, or, with `limit`, at rows >= limit)
   auto out_row = [&](int r, int limit) -> char* {
     const int mf = mt * BM + wave * 32 + r;
-    const int ir = mf / GT;
+    const int ir = (int)fdiv(mf, a.fd_gt);
     if (mf >= a.n_rows * GT || ir >= limit) return nullptr;
-    const int hr = hk * G + hs * GT + mf % GT;
+    const int hr = hk * G + hs * GT + (int)fmodq(mf, ir, a.fd_gt);
     return (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hr * a.os_h + (int64_t)ir * a.os_s) * esz;
   };
   if (MODE == MODE_FUSED) {
@@ -642,9 +649,10 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
         sp[dt][jq][0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
         sp[dt][jq][1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
       }
-    const int row0 = mt * (BM / GT);                 // first row of the tile
     const bool live = valid && irow < a.s_p;
-    const int gl = (irow - row0) / a.gamma;          // group within the tile
+    const int ga = (int)fdiv(irow, a.fd_gamma);      // this row's stride group
+    const int gl = ga - mt * a.n_grp;                // its group within the tile (gamma
+                                                     // divides the tile's rows)
     // delta rows in LDS. With the dense rows prefetched (dpre, [group][head][D]),
     // each anchor lane writes its delta elements to the padded slots of dlt,
     // so one barrier suffices. Otherwise they go to the K/V stage memory
@@ -653,14 +661,14 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     DA_LDS u32x2* dn_pre = nullptr;
     if (pre) {
       static_assert(DLT_BYTES >= DPRE_BYTES + (DPRE_BYTES / (2 * 32)) * DPAD, "padded slots fit");
-      dn_pre = (DA_LDS u32x2*)&dpre[0] + ((gl * GT + mflat % GT) * D) / 4 + lg;
-      dl = (DA_LDS u32x2*)&dlt[(gl * GT + mflat % GT) * (D * (int)esz + DPAD)] + lg;
+      dn_pre = (DA_LDS u32x2*)&dpre[0] + ((gl * GT + hin) * D) / 4 + lg;
+      dl = (DA_LDS u32x2*)&dlt[(gl * GT + hin) * (D * (int)esz + DPAD)] + lg;
       if (nt == 0) {     // no key tile ran: make every wave's dpre DMA visible
         wait_vmcnt<0>();
         __syncthreads();
       }
     } else {
-      dl = (DA_LDS u32x2*)&smem[0][0][0] + ((gl * GT + mflat % GT) * 2 + lg) * (NDT * 4);
+      dl = (DA_LDS u32x2*)&smem[0][0][0] + ((gl * GT + hin) * 2 + lg) * (NDT * 4);
       __syncthreads();   // every wave is done with the K/V stages
     }
     // element (dt, jq) of this lane: dims 32 dt + 8 jq + 4 lg .. +3. One code
@@ -672,8 +680,8 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
       auto dslot = [&](int dt, int jq) -> DA_LDS u32x2* {
         return PRE ? dl + 8 * dt + 2 * jq : dl + dt * 4 + jq;
       };
-      if (live && irow % a.gamma == 0) {
-        const int64_t g = irow / a.gamma;
+      if (live && irow == ga * a.gamma) {
+        const int64_t g = ga;
         u32x2 dn[NDT][4];
         if constexpr (PRE) {
 #pragma unroll
@@ -1048,6 +1056,8 @@ static int sparse_args(AttnArgs& a, const void* q, const void* k, const void* v,
   a.Gs = tile_heads(a.G); a.n_hs = a.G / a.Gs;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.window = window; a.sink = sink; a.q_block = q_block;
+  a.fd_hkv = make_fastdiv(Hkv); a.fd_qb = make_fastdiv(q_block);
+  a.fd_sp = make_fastdiv(1); a.fd_gamma = make_fastdiv(1);
   return DA_OK;
 }
 
@@ -1057,6 +1067,9 @@ static int sparse_items(AttnArgs& a) {
   const int64_t items = (int64_t)a.B * a.Hkv * a.n_hs * a.n_mtiles;
   if (items > 0x7fffff00LL) return DA_ERR_INVALID_ARG;
   a.n_items = (int)items;
+  a.tile_rows = BM / a.Gs;
+  a.fd_hs = make_fastdiv(a.n_hs); a.fd_mt = make_fastdiv(a.n_mtiles);
+  a.fd_gt = make_fastdiv(a.Gs);
   return DA_OK;
 }
 
@@ -1125,11 +1138,13 @@ extern "C" int da_sparse_attn_delta_fwd(const void* q, const void* k, const void
   a.dout = delta_out;
   if (delta_out) { a.dout_b = dl_str[0]; a.dout_h = dl_str[1]; a.dout_a = dl_str[2]; }
   a.gamma = gamma; a.s_p = s_p; a.n_anchor = s_p / gamma;
+  a.fd_gamma = make_fastdiv(gamma);
   // every stride group needs its anchor in the row tile: a gamma that does not
   // divide the two-head tile height takes one head per 128-row tile (the
   // per-row softmax makes the packing invisible in the results)
   if ((BM / a.Gs) % gamma != 0) { a.Gs = 1; a.n_hs = a.G; }
   if ((rc = sparse_items(a)) != DA_OK) return rc;
+  a.n_grp = a.tile_rows / gamma;
   (void)hipGetLastError();
   dispatch_attn<MODE_FUSED>(a, D, dtype, (hipStream_t)stream);
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
@@ -1159,6 +1174,10 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   a.n_rows = n; a.n_q = Sq; a.n_kv = Skv;
   a.n_mtiles = p.n_mtiles;
   a.n_items = p.n_items;
+  a.tile_rows = BM / a.Gs;
+  a.fd_hs = make_fastdiv(1); a.fd_mt = make_fastdiv(p.n_mtiles);
+  a.fd_sp = make_fastdiv(p.n_splits); a.fd_hkv = make_fastdiv(Hkv);
+  a.fd_gt = make_fastdiv(a.Gs); a.fd_qb = make_fastdiv(1); a.fd_gamma = make_fastdiv(1);
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.q_rows = q_rows; a.row_last = row_last; a.rl_b = rl_bstride;
   a.chunk = p.chunk; a.n_splits = p.n_splits; a.n_kv_dev = n_kv_dev;

@@ -106,6 +106,36 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, DA_LDS void* lds
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
 }
 
+// Division by a divisor fixed for a launch (d >= 1) of dividends in
+// [0, 2^31), by multiply and shift: q = (mulhi(n, m) + n) >> s with
+// s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 (Granlund and
+// Montgomery's round-up method; mulhi(n, m) <= n keeps the sum below 2^32).
+// The kernels' runtime divisors (heads per tile, row tiles, KV heads, query
+// block, stride) would otherwise each cost a ~30-instruction software divide.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+__host__ __device__ inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+  return FastDiv{d, (uint32_t)m, s};
+}
+
+__host__ __device__ inline uint32_t fdiv(uint32_t n, const FastDiv& f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return (__umulhi(n, f.m) + n) >> f.s;
+#else
+  return (uint32_t)((((uint64_t)n * f.m) >> 32) + n) >> f.s;
+#endif
+}
+
+// n mod d, given q = n / d
+__host__ __device__ inline uint32_t fmodq(uint32_t n, uint32_t q, const FastDiv& f) {
+  return n - q * f.d;
+}
+
 // Transposed 4 x b16 LDS read: within each 16-lane group, lane i gets element
 // (i % 4) of the 8-byte blocks addressed by lanes 4r + i/4, r = 0..3.
 __device__ __forceinline__ u32x2 read_tr16(const DA_LDS void* p) {
