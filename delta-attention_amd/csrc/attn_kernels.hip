@@ -131,12 +131,16 @@ struct AttnArgs {
 
 // Bytes of LDS that hold a fused tile's dense anchor rows, prefetched with the
 // first K/V tiles (tiles with more anchor rows read them in the epilogue).
+// Row slot s is DMA'd by wave s % 4 into its block of dpre, at row s / 4 of
+// it; the four blocks are DPAD bytes more than 1 KB apart, so the anchor
+// lanes of consecutive slots (the heads of a group) read different banks.
 constexpr int DPRE_BYTES = 4096;
 // The deltas those rows give, one 16-byte-padded slot per (group, head): the
 // lanes of a wave read the slots of two heads at once, which the padding puts
 // on different LDS banks.
 constexpr int DPAD = 16;
 constexpr int DLT_BYTES = DPRE_BYTES + 64 * DPAD;
+constexpr int DPRE_BLOCK = DPRE_BYTES / 4 + DPAD;   // one wave's block of dpre
 
 // sigma: swaps bits 2 and 3 of a key index within a 32-key half tile. Using
 // K row sigma(r) as A-operand row r puts keys 8*g .. 8*g+7 (g = lane / 32) in
@@ -201,7 +205,7 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   // [stage][K, V][tile bytes]
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE][2][TL::BYTES];
   __shared__ int red[4][NWAVE];
-  __shared__ __attribute__((aligned(16))) char dpre[MODE == MODE_FUSED ? DPRE_BYTES : 16];
+  __shared__ __attribute__((aligned(16))) char dpre[MODE == MODE_FUSED ? 4 * DPRE_BLOCK : 16];
   __shared__ __attribute__((aligned(16))) char dlt[MODE == MODE_FUSED ? DLT_BYTES : 16];
 
   const int tid = threadIdx.x;
@@ -556,7 +560,8 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     pre = n_grp * GT * D * (int)esz <= DPRE_BYTES;
     if (pre) {
       const int g0 = mt * n_grp;
-      const int slot = tid / DCH, ch = tid % DCH;
+      static_assert(NWAVE == 4, "dpre holds one block per wave");
+      const int slot = (lane / DCH) * NWAVE + wave, ch = lane % DCH;
       const int gl = (int)fdiv(slot, a.fd_gt), hl = (int)fmodq(slot, gl, a.fd_gt);
       const int64_t span = ((int64_t)(a.n_anchor - 1) * a.dsel_a + (int64_t)(a.Hq - 1) * a.dsel_h + D) * esz;
       const char* dbase = (const char*)a.dsel + (int64_t)b * a.dsel_b * esz;
@@ -565,7 +570,7 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
       const bool ok = slot < n_grp * GT && g0 + gl < a.n_anchor;
       const int64_t off = ((int64_t)(g0 + gl) * a.dsel_a + (int64_t)(hk * G + hs * GT + hl) * a.dsel_h) * esz + ch * 16;
       if (tid < DPRE_BYTES / 16)
-        dma16(rd, (DA_LDS void*)(&dpre[wave * 1024]), ok && off < 0xffff0000LL ? (uint32_t)off : 0xffffffffu);
+        dma16(rd, (DA_LDS void*)(&dpre[wave * DPRE_BLOCK]), ok && off < 0xffff0000LL ? (uint32_t)off : 0xffffffffu);
     }
   }
 
@@ -598,42 +603,6 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
 
   // ---- epilogue ----
   const float l_tot = sum32(l_i);
-  // Output rows leave through LDS: each lane parks its 4-element pieces (dims
-  // 32 dt + 8 jq + 4 lg .. +3 of wave row ln) in the wave's 32-row block of K/V
-  // stage 1, with the 16-byte chunks XOR-swizzled by the row so that neither
-  // the writes nor the reads conflict, then stores whole 16-byte chunks of
-  // consecutive rows: every store instruction writes complete rows, which
-  // measured faster than each one writing 16-byte pieces of 32 rows. The
-  // caller has a barrier behind it (stage 1 is no longer read by any wave);
-  // row_dst(r) gives row r's destination, or nullptr for a row not written.
-  auto stage_rows = [&](const u32x2 (&val)[NDT][4], auto row_dst) {
-    static_assert(NWAVE * 32 * RB <= 2 * TL::BYTES, "staging fits K/V stage 1");
-    DA_LDS char* sbuf = (DA_LDS char*)&smem[1][0][0] + wave * 32 * RB;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq)
-        *(DA_LDS u32x2*)(sbuf + ln * RB + (((4 * dt + jq) ^ (ln & (DCH - 1))) * 16) + 8 * lg) =
-            val[dt][jq];
-    constexpr int RPI = 1024 / RB;     // rows per store instruction
-    const int c = lane % DCH;
-#pragma unroll
-    for (int k = 0; k < 32 / RPI; ++k) {
-      const int r = k * RPI + lane / DCH;
-      const u32x4 x = *(const DA_LDS u32x4*)(sbuf + r * RB + ((c ^ (r & (DCH - 1))) * 16));
-      char* dst = row_dst(r);
-      if (dst) *(u32x4*)(dst + c * 16) = x;
-    }
-  };
-  // destination of wave row r in the [B, S, Hq, D] output (nullptr past the
-  // tile's rows, or, with `limit`, at rows >= limit)
-  auto out_row = [&](int r, int limit) -> char* {
-    const int mf = mt * BM + wave * 32 + r;
-    const int ir = (int)fdiv(mf, a.fd_gt);
-    if (mf >= a.n_rows * GT || ir >= limit) return nullptr;
-    const int hr = hk * G + hs * GT + (int)fmodq(mf, ir, a.fd_gt);
-    return (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hr * a.os_h + (int64_t)ir * a.os_s) * esz;
-  };
   if (MODE == MODE_FUSED) {
     // out[r] = rnd(rnd(sparse[r]) + delta[r / gamma]) for rows r < s_p, with
     // delta[g] = rnd(dense[g] - rnd(sparse[g * gamma])) formed by the anchor
@@ -661,7 +630,10 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     DA_LDS u32x2* dn_pre = nullptr;
     if (pre) {
       static_assert(DLT_BYTES >= DPRE_BYTES + (DPRE_BYTES / (2 * 32)) * DPAD, "padded slots fit");
-      dn_pre = (DA_LDS u32x2*)&dpre[0] + ((gl * GT + hin) * D) / 4 + lg;
+      {
+        const int ps = gl * GT + hin;      // this row's dpre slot
+        dn_pre = (DA_LDS u32x2*)&dpre[(ps % NWAVE) * DPRE_BLOCK + (ps / NWAVE) * RB] + lg;
+      }
       dl = (DA_LDS u32x2*)&dlt[(gl * GT + hin) * (D * (int)esz + DPAD)] + lg;
       if (nt == 0) {     // no key tile ran: make every wave's dpre DMA visible
         wait_vmcnt<0>();
@@ -721,52 +693,65 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
         }
       }
       __syncthreads();
-      // every lane forms its row's output (rows >= s_p are not stored)
-      u32x2 dv[NDT][4], o[NDT][4];
+      if (live) {
+        char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
+                                 (int64_t)qrow * a.os_s) * esz;
+        u32x2 dv[NDT][4];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int jq = 0; jq < 4; ++jq) dv[dt][jq] = *dslot(dt, jq);
+          for (int jq = 0; jq < 4; ++jq) dv[dt][jq] = *dslot(dt, jq);
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int jq = 0; jq < 4; ++jq)
+          for (int jq = 0; jq < 4; ++jq) {
+            u32x2 o;
 #pragma unroll
-          for (int e = 0; e < 2; ++e)
-            o[dt][jq][e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[dt][jq][e]),
-                                    E::hi(sp[dt][jq][e]) + E::hi(dv[dt][jq][e]));
-      stage_rows(o, [&](int r) { return out_row(r, a.s_p); });
+            for (int e = 0; e < 2; ++e)
+              o[e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[dt][jq][e]),
+                              E::hi(sp[dt][jq][e]) + E::hi(dv[dt][jq][e]));
+            *(u32x2*)(op + (32 * dt + 8 * jq + 4 * lg) * esz) = o;
+          }
+      }
     };
     if (pre) fused_out(std::true_type());
     else fused_out(std::false_type());
     return;
   }
   if (MODE == MODE_SPARSE) {
+    if (!valid) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (valid && a.lse && lg == 0)
+    if (a.lse && lg == 0)
       a.lse[((int64_t)b * a.Hq + hrow) * a.n_rows + irow] =
           l_tot > 0.f ? m_i + __builtin_log2f(l_tot) : INFINITY;
-    u32x2 o[NDT][4];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq) {
-        o[dt][jq][0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
-        o[dt][jq][1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
-      }
-    __syncthreads();   // every wave is done with the K/V stages
-    stage_rows(o, [&](int r) { return out_row(r, a.n_rows); });
-  } else {
-    if (!valid) return;   // the merge reads the rows of the selection only
-    const int r = wave * 32 + ln;
-    float* po = a.part_o + ((int64_t)w * a.ws_rows + r) * D;
+    char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
+                             (int64_t)qrow * a.os_s) * esz;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
         const int d = 32 * dt + 8 * jq + 4 * lg;
-        *(f32x4*)(po + d) = (f32x4){acc[dt][4 * jq + 0], acc[dt][4 * jq + 1],
-                                     acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]};
+        u32x2 pkd;
+        pkd[0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
+        pkd[1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
+        *(u32x2*)(op + d * esz) = pkd;
+      }
+  } else {
+    if (!valid) return;   // the merge reads the rows of the selection only
+    const int r = wave * 32 + ln;
+    float* po = a.part_o + ((int64_t)w * a.ws_rows + r) * D;
+    // the partials go around L2 (non-temporal): written once and read back by
+    // the merge launch, they would otherwise evict the key/value chunk that
+    // the concurrent items of this XCD share (split-kernel fetch 1.78 -> 1.59
+    // GB per launch at 128K, same time)
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const int d = 32 * dt + 8 * jq + 4 * lg;
+        __builtin_nontemporal_store((f32x4){acc[dt][4 * jq + 0], acc[dt][4 * jq + 1],
+                                            acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]},
+                                    (f32x4*)(po + d));
       }
     if (lg == 0) {
       a.part_ml[(int64_t)w * 2 * a.ws_rows + r] = m_i;
