@@ -37,7 +37,7 @@ extern "C" {
 
 #define DA_OK 0
 #define DA_ERR_INVALID_ARG (-1)      /* shape, stride, range or null-pointer error */
-#define DA_ERR_HEAD_DIM (-2)         /* head_dim not supported (32, 64 and 128 are; the RoPE prologue also takes 256) */
+#define DA_ERR_HEAD_DIM (-2)         /* head_dim not supported (forward, decode and RoPE: 32, 64, 128, 256; backward: up to 128) */
 #define DA_ERR_DTYPE (-3)            /* dtype not DA_BF16 / DA_FP16 */
 #define DA_ERR_ALIGNMENT (-4)        /* pointer or stride breaks 16-byte row alignment */
 #define DA_ERR_WORKSPACE (-5)        /* workspace missing or smaller than required */
@@ -396,7 +396,7 @@ int da_qsparse_attn_bwd(const void* q, const void* k, const void* v, const void*
 
 /*
  * Backward of the composition (flex_delta.py:186-196, and the _ScaleGrad /
-X [B, S, H, D] ->
+ * detach arms, flex_delta.py:79-92): upstream gradient grad [B, S, H, D] ->
  *   dsparse [B, S, H, D]: grad[r] for r < s_p, rnd(grad[r] - ddelta[r / gamma])
  *                         at anchor rows, 0 for r >= s_p;
  *   ddense [B, n_anchor + S - s_p, H, D]: ddelta[i] for the anchors, then
