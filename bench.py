@@ -81,6 +81,12 @@ def parse():
     p.add_argument("--train", action="store_true",
                    help="time delta_forward_train's forward and backward (the training "
                         "path) at --seq/--gamma/--window/--sink instead of the prefill")
+    p.add_argument("--adaptive", action="store_true",
+                   help="time the adaptive-stride layer (stride_policy \"adaptive\": per "
+                        "--adapt-chunk rows a dense pass at the current stride, the inter-anchor "
+                        "delta cosine, one host sync per chunk) beside the fixed-stride layer")
+    p.add_argument("--adapt-chunk", type=int, default=4096)
+    p.add_argument("--adapt-threshold", type=float, default=0.95)
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -261,6 +267,65 @@ def gamma_sweep(a, q, k, v, gammas):
             "cos_to_full_mean": round(cos.mean().item(), 6), "cos_to_full_min": round(cos.min().item(), 6),
             "sparse_only_cos_mean": round(cs.mean().item(), 6), "sparse_only_cos_min": round(cs.min().item(), 6),
             "seq_len": S, "window": a.window, "sink": a.sink}), flush=True)
+
+
+def adaptive_layer(a, q, k, v):
+    """The adaptive-stride layer: LlamaAttention.delta_forward with
+    stride_policy "adaptive" (the reference's llama.py:695-711, 759-824): the
+    key-sparse pass, then per adapt_chunk rows a dense pass over the chunk's
+    anchors at the current stride, the inter-anchor delta cosine (one host
+    sync per chunk: the next chunk's stride depends on it), the
+    variable-stride broadcast and the dense tail. Wall clock per layer, with
+    the fixed-stride layer at the starting and at the smallest stride beside
+    it (on these random inputs the delta cosine stays low, so the stride
+    falls to gamma_min within a few chunks)."""
+    import types
+    import torch
+    from delta_attention import ops
+    from delta_attention.llama import LlamaAttention
+    B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
+    scale = D ** -0.5
+    cfg = types.SimpleNamespace(
+        hidden_size=H * D, num_attention_heads=H, num_key_value_heads=Hkv, head_dim=D,
+        attention_bias=False, attention_dropout=0.0, rms_norm_eps=1e-6,
+        _attn_implementation="window", mode="delta", delta_lambda=a.gamma,
+        sliding_window=a.window, sink_tokens=a.sink, stride_policy="adaptive", log_drift=False,
+        adapt_chunk=a.adapt_chunk, adapt_threshold=a.adapt_threshold, gamma_min=16,
+        gamma_max=256, stride_trigger="absolute", adapt_k=2.0)
+    m = LlamaAttention(cfg, layer_idx=0).to(q.device).to(torch.bfloat16)
+
+    def timed(fn):
+        for _ in range(a.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / a.steps * 1e3
+
+    with torch.inference_mode():
+        ms = timed(lambda: m.delta_forward(m, q, k, v, None, scaling=scale))
+        st = m._stride_stats
+        fixed = {g: round(timed(lambda: ops.delta_prefill(q, k, v, gamma=g, window=a.window,
+                                                          sink=a.sink, sm_scale=scale)), 4)
+                 for g in sorted({a.gamma, 16})}
+        sparse_ms = timed(lambda: ops.sparse_attention(q, k, v, window=a.window, sink=a.sink,
+                                                       sm_scale=scale))
+    gammas = [c["gamma"] for c in st["chunks"]]
+    n = len(gammas)
+    print(json.dumps({
+        "metric": "adaptive-stride layer prefill (wall clock, host syncs included)",
+        "value": round(ms, 4), "unit": "ms", "higher_is_better": False,
+        "steps": a.steps, "warmup": a.warmup, "chunks": n, "adapt_chunk": a.adapt_chunk,
+        "adapt_threshold": a.adapt_threshold, "n_anchors": st["n_anchors"],
+        "gamma_first_chunks": gammas[:6], "gamma_last": gammas[-1] if gammas else None,
+        "effective_sparsity": round(st["effective_sparsity"], 6),
+        "sparse_pass_ms": round(sparse_ms, 4),
+        "per_chunk_ms": round((ms - sparse_ms) / max(n, 1), 4),
+        "fixed_stride_layer_ms": fixed,
+        "config": {"batch": B, "seq_len": S, "heads": H, "kv_heads": Hkv, "head_dim": D,
+                   "window": a.window, "sink": a.sink, "gamma_start": a.gamma}}), flush=True)
 
 
 def prologue(a, dev):
@@ -595,6 +660,9 @@ def main():
         return
     if a.train:
         train_step(a, q, k, v)
+        return
+    if a.adaptive:
+        adaptive_layer(a, q, k, v)
         return
 
     cut_n, s_p, n_anchor = ops.anchor_layout(S, a.gamma)

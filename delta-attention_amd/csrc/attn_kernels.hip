@@ -439,7 +439,10 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     }
   };
   // scaled row max of a score tile: four independent chains, then one
-  // permlane32 swap (lanes l and l + 32 hold the two key groups of a row)
+  // permlane32 swap (lanes l and l + 32 hold the two key groups of a row).
+  // IEEE `maximum` (v_maximum3_f32) instead of fmaxf: fmaxf must quiet
+  // signalling NaNs first, one extra v_max per chain start on the MFMA
+  // results; scores hold no NaN, where the two agree.
   auto rowmax = [&](const f32x16 (&x)[NH]) -> float {
     float p[4];
 #pragma unroll
@@ -447,11 +450,14 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
       const int hf = c >> 1, j0 = 8 * (c & 1);
       float m = x[hf][j0];
 #pragma unroll
-      for (int j = 1; j < 8; ++j) m = __builtin_fmaxf(m, x[hf][j0 + j]);
+      for (int j = 1; j < 8; ++j) m = __builtin_elementwise_maximum(m, x[hf][j0 + j]);
       p[c] = m;
     }
-    const float mx = __builtin_fmaxf(__builtin_fmaxf(p[0], p[1]), __builtin_fmaxf(p[2], p[3]));
-    return max32(mx) * c2;          // scaling by c2 > 0 keeps the max
+    const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(p[0], p[1]),
+                                                   __builtin_elementwise_maximum(p[2], p[3]));
+    float s0, s1;
+    swap32(mx, s0, s1);
+    return __builtin_elementwise_maximum(s0, s1) * c2;   // scaling by c2 > 0 keeps the max
   };
   // lazy online-softmax update with the scaled tile max: a row's running max
   // moves (and its O, l are rescaled) only when its tile max exceeds it by
@@ -960,8 +966,15 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
 // their prologue and partials, and at 32K keys (638 rows x 32 heads) 56 packs
 // the ~1K useful items into two rounds of resident workgroups (0.258 ms vs
 // 0.269-0.272 at 40; neutral at 128K keys, where the 8K target binds).
+// A short row list (fewer than 64 (batch, kv head, row tile) triples: the
+// adaptive stride's chunks, a dense tail alone) cannot fill the GPU with
+// 56-tile items, and one item's latency would bound the launch: ~1024 items of
+// at least 16 tiles instead.
 static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
-  return plan_qsparse(B, Hq, Hkv, n, (Skv + BN - 1) / BN, D, DA_ROWS_ITEMS, 56);
+  const int64_t vis = (Skv + BN - 1) / BN;
+  const int64_t tiles = (int64_t)B * Hkv * (((int64_t)n * (Hq / Hkv) + BM - 1) / BM);
+  if (tiles < 64) return plan_qsparse(B, Hq, Hkv, n, vis, D, 1024, 16);
+  return plan_qsparse(B, Hq, Hkv, n, vis, D, DA_ROWS_ITEMS, 56);
 }
 
 // One decode row per batch at the end of the cache: its list is the sink

@@ -21,6 +21,7 @@ from typing import Optional, Tuple
 import torch
 from torch import nn
 
+from . import _lib as L
 from . import ops
 from .delta_kernel import attention as qsa_kernel
 from .timing import region
@@ -271,24 +272,35 @@ class LlamaAttention(nn.Module):
         """Chunked adaptive anchor placement (llama.py:759-824): anchors at the
         current stride inside each adapt_chunk rows, stride re-planned from the
         chunk's mean consecutive-delta cosine, variable-stride broadcast
-        (kernel 3 with an anchor list), dense cut_n tail."""
-        from .stride import (apply_delta_variable, effective_sparsity, interanchor_cos,
-                             next_gamma, next_gamma_relative, plan_chunks)
+        (kernel 3 with an anchor list), dense cut_n tail.
+
+        The result equals the reference's cat(apply_delta_variable(...),
+        tail_dense), assembled in place in the sparse pass's output: the anchor
+        deltas rnd(dense - sparse[:, idx]) are formed first (the rounding of
+        stride.py:38), the broadcast then adds them row by row, and the tail
+        rows are written by the query-sparse kernel's scatter epilogue. The
+        chunks' dense rows read q through a row list, not a gathered copy."""
+        from .stride import effective_sparsity, interanchor_cos, next_gamma, next_gamma_relative, plan_chunks
 
         cfg = self.config
         device = query_states.device
         q, k, v = query_states, key_states, value_states
+        out = sparse_attn_output
         if q.dtype == torch.float32:
             q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
-            sparse_attn_output = sparse_attn_output.to(torch.bfloat16)
+        if out.dtype != q.dtype:
+            out = out.to(q.dtype)
+        scale = float(scaling)
         gamma_c = int(cfg.delta_lambda)
         trigger = getattr(cfg, "stride_trigger", "absolute")
         cos_history, idx_parts, dense_parts, chunk_log = [], [], [], []
         for start, end in plan_chunks(s_p, int(cfg.adapt_chunk)):
             c_idx = torch.arange(start, end, step=gamma_c, device=device)
-            dense_c = qsa_kernel(q[:, :, c_idx], k, v, c_idx.unsqueeze(0), scaling).transpose(1, 2)
+            # the chunk's rows see keys < end: the split plan sizes its items for that
+            dense_c = ops.qsparse_attention(q, k[:, :, :end], v[:, :, :end], c_idx, scale,
+                                            q_rows=c_idx).transpose(1, 2)
             # deltas rnd(dense - sparse) at the chunk's anchors, formed in the kernel
-            cos_mean, cos_min = interanchor_cos(dense_c, sparse=sparse_attn_output, rows=c_idx)
+            cos_mean, cos_min = interanchor_cos(dense_c, sparse=out, rows=c_idx)
             idx_parts.append(c_idx)
             dense_parts.append(dense_c)
             chunk_log.append({"start": int(start), "gamma": int(gamma_c), "cos_mean": cos_mean,
@@ -302,17 +314,16 @@ class LlamaAttention(nn.Module):
                 gamma_c = next_gamma(cos_mean, gamma_c, threshold=float(cfg.adapt_threshold),
                                      gamma_min=int(cfg.gamma_min), gamma_max=int(cfg.gamma_max))
         idx = torch.cat(idx_parts)
-        dense_sel = torch.cat(dense_parts, dim=1).contiguous()
-        corrected = apply_delta_variable(sparse_attn_output[:, :s_p], dense_sel, idx, s_p)
+        delta = torch.cat(dense_parts, dim=1) - out[:, idx]        # bf16: one rounding
+        ops.delta_add(out, s_p=s_p, out=out, delta=delta, anchors=idx)
         tail_idx = torch.arange(s_p, s, device=device)
-        tail_dense = qsa_kernel(q[:, :, tail_idx], k, v, tail_idx.unsqueeze(0), scaling).transpose(1, 2)
+        ops.qsparse_attention(q, k, v, tail_idx, scale, q_rows=tail_idx, epi=L.DA_EPI_SCATTER, out=out)
         self._stride_stats = {
             "kind": "stride", "layer": int(self.layer_idx), "seq_len": int(s),
             "effective_sparsity": effective_sparsity(torch.cat((idx, tail_idx)), s,
                                                      int(cfg.sliding_window), self._sink()),
             "n_anchors": int(idx.numel()), "chunks": chunk_log,
         }
-        out = torch.cat((corrected, tail_dense), dim=1)
         return out.to(query_states.dtype)
 
     # -- decode (llama.py:498-657) ---------------------------------------------------

@@ -15,6 +15,8 @@ from __future__ import annotations
 
 from typing import List, Tuple
 
+import numpy as np
+
 ADAPT_MARGIN = 0.02  # hysteresis above adapt_threshold before gamma grows (stride.py:23)
 
 
@@ -39,11 +41,12 @@ def interanchor_cos(deltas, *, sparse=None, rows=None) -> Tuple[float, float]:
 
     if deltas.size(1) < 2:
         return 1.0, 1.0
-    import torch
 
     cos = ops.anchor_delta_cos(deltas, sparse=sparse, rows=rows)
-    mean, mn = torch.stack((cos.mean(), cos.min())).tolist()   # one device sync
-    return float(mean), float(mn)
+    # one device-to-host copy of the [b, n-1, h] cosines (a few KB) instead
+    # of reduction launches; the mean is taken in float64 on the host
+    c = cos.cpu().numpy()
+    return float(c.mean(dtype=np.float64)), float(c.min())
 
 
 def next_gamma(cos_mean: float, gamma_c: int, *, threshold: float,
