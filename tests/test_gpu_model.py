@@ -54,11 +54,15 @@ def test_swiglu(gpu):
     _ulp_close(c, ref, frac_exact=0.99, what="swiglu in place")
 
 
-def test_small_model_matches_reference_layer_ops(gpu):
+@pytest.mark.parametrize("D", [128, 32, 256])
+def test_small_model_matches_reference_layer_ops(gpu, D):
+    """A 2-layer model (head_dim 128, and 32 / 256: the fused RoPE prologue and
+    the attention kernels at those head dims) against the reference decoder
+    layer's torch ops with the same weights."""
     from delta_attention.llama import apply_rotary_pos_emb
     from delta_attention.model import LlamaConfig, random_llama
     cfg = LlamaConfig(vocab_size=512, hidden_size=2048, intermediate_size=4096, num_hidden_layers=2,
-                      num_attention_heads=16, num_key_value_heads=4, head_dim=128,
+                      num_attention_heads=16, num_key_value_heads=4, head_dim=D,
                       delta_lambda=64, sliding_window=256, sink_tokens=16)
     m = random_llama(cfg, "cuda", torch.bfloat16, seed=5)
     S = 1024
@@ -74,7 +78,7 @@ def test_small_model_matches_reference_layer_ops(gpu):
             at = layer.self_attn
             residual = h
             x = layer.input_layernorm(h)
-            q, k, v = at._qkv(x, (1, S, -1, 128))
+            q, k, v = at._qkv(x, (1, S, -1, D))
             q, k = apply_rotary_pos_emb(q, k, cos, sin)
             a, _ = at.delta_forward(at, q, k, v, None, scaling=at.scaling)
             h = residual + at.o_proj(a.reshape(1, S, -1))
