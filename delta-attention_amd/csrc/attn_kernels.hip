@@ -608,6 +608,27 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   }
 
   // ---- epilogue ----
+  // Row stores of 16 bytes: lanes l and l + 32 hold dims 8 jq + 0..3 and
+  // + 4..7 of the same row; one permlane32 swap per register pair gives lane
+  // l dims 8 (2p) + 0..7 and lane l + 32 dims 8 (2p + 1) + 0..7, so each
+  // store instruction writes 32 rows x 32 bytes instead of 32 rows x 16.
+  auto store_rows16 = [&](char* op, u32x2 (&o)[NDT][4]) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int p2 = 0; p2 < 2; ++p2) {
+        u32x2& x0 = o[dt][2 * p2];
+        u32x2& x1 = o[dt][2 * p2 + 1];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          auto r = __builtin_amdgcn_permlane32_swap(x0[e], x1[e], false, false);
+          x0[e] = r[0];
+          x1[e] = r[1];
+        }
+        const u32x4 v = {x0[0], x0[1], x1[0], x1[1]};
+        *(u32x4*)(op + (32 * dt + 16 * p2 + 8 * lg) * esz) = v;
+      }
+  };
   const float l_tot = sum32(l_i);
   if (MODE == MODE_FUSED) {
     // out[r] = rnd(rnd(sparse[r]) + delta[r / gamma]) for rows r < s_p, with
@@ -707,17 +728,16 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
           for (int jq = 0; jq < 4; ++jq) dv[dt][jq] = *dslot(dt, jq);
+        u32x2 o[NDT][4];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-          for (int jq = 0; jq < 4; ++jq) {
-            u32x2 o;
+          for (int jq = 0; jq < 4; ++jq)
 #pragma unroll
             for (int e = 0; e < 2; ++e)
-              o[e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[dt][jq][e]),
-                              E::hi(sp[dt][jq][e]) + E::hi(dv[dt][jq][e]));
-            *(u32x2*)(op + (32 * dt + 8 * jq + 4 * lg) * esz) = o;
-          }
+              o[dt][jq][e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[dt][jq][e]),
+                                      E::hi(sp[dt][jq][e]) + E::hi(dv[dt][jq][e]));
+        store_rows16(op, o);
       }
     };
     if (pre) fused_out(std::true_type());
@@ -732,16 +752,15 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
           l_tot > 0.f ? m_i + __builtin_log2f(l_tot) : INFINITY;
     char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
                              (int64_t)qrow * a.os_s) * esz;
+    u32x2 o[NDT][4];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
-        const int d = 32 * dt + 8 * jq + 4 * lg;
-        u32x2 pkd;
-        pkd[0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
-        pkd[1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
-        *(u32x2*)(op + d * esz) = pkd;
+        o[dt][jq][0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
+        o[dt][jq][1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
       }
+    store_rows16(op, o);
   } else {
     if (!valid) return;   // the merge reads the rows of the selection only
     const int r = wave * 32 + ln;
