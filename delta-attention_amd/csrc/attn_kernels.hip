@@ -109,7 +109,7 @@ struct AttnArgs {
   // [1, n_kv]) and chunk = ceil(list / n_splits): the launch stays valid as a
   // cache grows (decode rows under graph replay)
   const int* n_kv_dev;
-  float* part_o;    // [item][ws_rows][D]
+  uint32_t* part_o; // [item][ws_rows][D / 2]: bf16 pairs of each row's O / l
   float* part_ml;   // [item][2][ws_rows]  (running max, row sum)
   int ws_rows;      // workspace rows per item: min(BM, n_rows * G) (a tile's valid rows)
   // MODE_FUSED: dense anchor rows [B, n_anchor, Hq, D] (strides batch, head,
@@ -764,19 +764,31 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   } else {
     if (!valid) return;   // the merge reads the rows of the selection only
     const int r = wave * 32 + ln;
-    float* po = a.part_o + ((int64_t)w * a.ws_rows + r) * D;
-    // the partials go around L2 (non-temporal): written once and read back by
-    // the merge launch, they would otherwise evict the key/value chunk that
-    // the concurrent items of this XCD share (split-kernel fetch 1.78 -> 1.59
-    // GB per launch at 128K, same time)
+    // normalised split rows O / l in bf16, a 16-byte row piece per lane after
+    // one permlane32 swap (the merge reads them back once). At half the fp32
+    // volume, plain stores through L2 measured 0.5-1 % faster than
+    // non-temporal ones; with fp32 partials the non-temporal form had kept
+    // the shared key/value chunk in L2 (split-kernel fetch 1.78 -> 1.59 GB).
+    uint32_t* po = a.part_o + ((int64_t)w * a.ws_rows + r) * (D / 2);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    using B16 = Elt<__bf16>;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int jq = 0; jq < 4; ++jq) {
-        const int d = 32 * dt + 8 * jq + 4 * lg;
-        __builtin_nontemporal_store((f32x4){acc[dt][4 * jq + 0], acc[dt][4 * jq + 1],
-                                            acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]},
-                                    (f32x4*)(po + d));
+      for (int p2 = 0; p2 < 2; ++p2) {
+        u32x2 x0, x1;
+        const int j0 = 2 * p2, j1 = 2 * p2 + 1;
+        x0[0] = B16::pack2(acc[dt][4 * j0 + 0] * inv, acc[dt][4 * j0 + 1] * inv);
+        x0[1] = B16::pack2(acc[dt][4 * j0 + 2] * inv, acc[dt][4 * j0 + 3] * inv);
+        x1[0] = B16::pack2(acc[dt][4 * j1 + 0] * inv, acc[dt][4 * j1 + 1] * inv);
+        x1[1] = B16::pack2(acc[dt][4 * j1 + 2] * inv, acc[dt][4 * j1 + 3] * inv);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          auto sw = __builtin_amdgcn_permlane32_swap(x0[e], x1[e], false, false);
+          x0[e] = sw[0];
+          x1[e] = sw[1];
+        }
+        *(u32x4*)(po + (32 * dt + 16 * p2 + 8 * lg) / 2) = (u32x4){x0[0], x0[1], x1[0], x1[1]};
       }
     if (lg == 0) {
       a.part_ml[(int64_t)w * 2 * a.ws_rows + r] = m_i;
@@ -800,7 +812,7 @@ struct MergeArgs {
   int window, sink;
   int lanes;        // P: threads sharing one (row, 8-column) task, splits s = p mod P
   int wgs;          // workgroups per row tile
-  const float* part_o;
+  const uint32_t* part_o;   // bf16 pairs of O / l per split row
   const float* part_ml;
   int ws_rows;      // as in AttnArgs
   int epi, n_anchor, n_q;
@@ -883,16 +895,18 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    using B16 = Elt<__bf16>;
     for (int s = p; s < nsv; s += P) {
       const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
-      const float sc = fast_exp2(a.part_ml[w * 2 * a.ws_rows + r] - M);
-      L += sc * a.part_ml[w * 2 * a.ws_rows + a.ws_rows + r];
-      const f32x4* po = (const f32x4*)(a.part_o + (w * a.ws_rows + r) * D + 8 * c);
-      const f32x4 x0 = po[0], x1 = po[1];
+      // split weight exp2(m_s - M) l_s on the stored O_s / l_s
+      const float sc = fast_exp2(a.part_ml[w * 2 * a.ws_rows + r] - M) *
+                       a.part_ml[w * 2 * a.ws_rows + a.ws_rows + r];
+      L += sc;
+      const u32x4 x = *(const u32x4*)(a.part_o + (w * a.ws_rows + r) * (D / 2) + 4 * c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        acc[e] += sc * x0[e];
-        acc[4 + e] += sc * x1[e];
+        acc[2 * e] += sc * B16::lo(x[e]);
+        acc[2 * e + 1] += sc * B16::hi(x[e]);
       }
     }
     for (int off = 1; off < P; off <<= 1) {
@@ -976,7 +990,7 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
   const bool fits = items <= 0x7fffff00LL && base * 128 <= 0x7fffff00LL;
   p.n_items = fits ? (int)items : 0;
   p.ws_rows = (int)min((int64_t)BM, (int64_t)n * G);
-  p.ws_bytes = fits ? (size_t)p.n_items * p.ws_rows * (D + 2) * sizeof(float) : 0;
+  p.ws_bytes = fits ? (size_t)p.n_items * p.ws_rows * (D * sizeof(uint16_t) + 2 * sizeof(float)) : 0;
   return p;
 }
 
@@ -1199,8 +1213,8 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   a.q_rows = q_rows; a.row_last = row_last; a.rl_b = rl_bstride;
   a.chunk = p.chunk; a.n_splits = p.n_splits; a.n_kv_dev = n_kv_dev;
   a.window = window; a.sink = sink;
-  a.part_o = (float*)workspace;
-  a.part_ml = (float*)workspace + (size_t)p.n_items * p.ws_rows * D;
+  a.part_o = (uint32_t*)workspace;
+  a.part_ml = (float*)((char*)workspace + (size_t)p.n_items * p.ws_rows * D * sizeof(uint16_t));
   a.ws_rows = p.ws_rows;
 
   MergeArgs m = {};
