@@ -271,16 +271,20 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   const int sink = (KSPARSE || a.window > 0) ? a.sink : 0;
   constexpr size_t esz = sizeof(T);
 
-  // ---- Q^T fragments (registers for the whole kernel), loaded first so
-  //      that their latency overlaps the set-up below ----
+  // ---- Q^T fragments (registers for the whole kernel). Key-sparse modes
+  //      load them first, so that their latency overlaps the set-up below;
+  //      the query-sparse mode loads them once the item is known not to be
+  //      past the end of its tile's list (about half of the split items at
+  //      long causal row lists), still ahead of the first K/V wait ----
   u32x4 qf[NDS];
-  {
+  auto load_q = [&]() {
     const char* qp = (const char*)a.q +
                      ((int64_t)b * a.qs_b + (int64_t)hrow * a.qs_h + (int64_t)qrow * a.qs_s) * esz;
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds)
       qf[ds] = valid ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
-  }
+  };
+  if constexpr (KSPARSE) load_q();
 
   // ---- tile-wide bounds over the valid rows ----
   int hi_min, hi_max, lo_min, lo_max;
@@ -330,6 +334,7 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     t_off = split * chunk;
     if (t_off >= nt) return;   // past the list: the merge skips this split
     nt = min(chunk, nt - t_off);
+    load_q();
   }
 
   const char* kbase = (const char*)a.k + ((int64_t)b * a.ks_b + (int64_t)hk * a.ks_h) * esz;
