@@ -31,7 +31,10 @@
 //     its V^T A-fragments come from transposed reads (ds_read_b64_tr_b16).
 //   * Softmax: one FMA + exp2 per score, row sum by v_dot2 over the packed P.
 //     Lazy rescale: the running max only moves when a row's tile max exceeds
-//     it by more than 2^8, so most tiles skip the O rescale.
+//     it by more than 40 (log2 domain). The first pass over the tiles takes
+//     no per-tile row max once every row has its first max; a row sum above
+//     2^39 (a max that would have moved) sends the workgroup through a second,
+//     exact pass, whose bits equal the first pass's for every other row.
 //   * Per key tile, 32 MFMAs in one scheduling region keep the matrix pipe
 //     fed: the exponentials of tile t run under the score MFMAs of tile t+1,
 //     then the PV MFMAs of tile t follow with their V reads running ahead.
@@ -76,7 +79,12 @@ constexpr int BN = 64;               // keys per tile
 constexpr int NH = BN / 32;          // 32-key halves per tile
 constexpr int MTHR = 256;            // threads of the split-merge kernel
 constexpr int NSTAGE = 2;            // LDS stages for K and for V
-constexpr float RESCALE_THRESH = 8.0f;   // log2 domain
+// Lazy-rescale bound (log2 domain): a row's running max moves only when a
+// tile's max exceeds it by more than this, so P <= 2^40 and l <= 2^40 * keys.
+// The same bound on a row's sum tells the tile loop that ran without row
+// maxima that no row needed a move (P <= l).
+constexpr float RESCALE_THRESH = 40.0f;
+constexpr float RESCALE_LSUM = 1099511627776.0f;   // 2^RESCALE_THRESH
 constexpr float NEG_BIG = -1.0e30f;      // finite "minus infinity" for the running max
 
 // MODE_FUSED is MODE_SPARSE with the delta broadcast-add in its epilogue.
@@ -403,11 +411,10 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   }
 
   f32x16 acc[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
-  float m_i = NEG_BIG, l_i = 0.f;
+  float m_i, l_i;
+  // First pass: a wave takes row maxima only while one of its rows has no
+  // reference max yet and can still see keys.
+  bool track = true;
   const float c2 = a.scale_log2;
   const DA_LDS char* lds0 = (const DA_LDS char*)&smem[0][0][0];
 
@@ -466,10 +473,10 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   };
   // lazy online-softmax update with the scaled tile max: a row's running max
   // moves (and its O, l are rescaled) only when its tile max exceeds it by
-  // more than 2^RESCALE_THRESH. The decision is per row (the other rows of the
-  // wave multiply by exactly 1), so a row's result does not depend on which
-  // rows share its wave: every head packing and row grouping gives the same
-  // bits.
+  // more than RESCALE_THRESH (log2 domain). The decision is per row (the other
+  // rows of the wave multiply by exactly 1), so a row's result does not depend
+  // on which rows share its wave: every head packing and row grouping gives
+  // the same bits.
   auto update = [&](float mx) {
     const bool up = mx > m_i + RESCALE_THRESH;
     if (__any(up)) {
@@ -482,6 +489,12 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
         for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
     }
   };
+  // Whether a row of this wave has no reference max yet (nothing visible in
+  // the tiles so far) but can still see a key from tile t on: the list runs
+  // through increasing keys, and a row sees no key above `hi`.
+  auto pending = [&](int t) -> bool {
+    return __any(valid && m_i == NEG_BIG && hi >= tile_n0(t));
+  };
 
   // Step t. On entry: S(t) (masked) is in `cur` and the running max covers it;
   // K(t+1) and V(t) are resident in LDS stages (t+1) & 1 and t & 1.
@@ -493,10 +506,11 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   //   Both phases are one basic block, so that the exponentials stay under
   //   the score MFMAs instead of sinking to their use in phase B.
   //   Then S(t+1) is masked (boundary tiles only), its max taken (overlapping
-  //   the PV MFMAs still in the pipe), the running max moved if needed; wait
-  //   for the DMA, barrier.
-  auto step = [&](int t, auto last_tag, f32x16 (&cur)[NH], f32x16 (&nxt)[NH]) {
+  //   the PV MFMAs still in the pipe) and the running max moved if needed,
+  //   when `track` is set; wait for the DMA, barrier.
+  auto step = [&](int t, auto last_tag, auto exact_tag, f32x16 (&cur)[NH], f32x16 (&nxt)[NH]) __attribute__((always_inline)) {
     constexpr bool LAST = decltype(last_tag)::value;   // t == nt - 1
+    constexpr bool EXACT = decltype(exact_tag)::value;
     // Key-sparse modes: the wave runs its MFMA block (exponentials, score
     // MFMAs, PV MFMAs) at raised priority and drops it for the mask, row max,
     // DMA wait and barrier, so that the other wave on the SIMD fills those
@@ -555,7 +569,10 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
 #endif
     if (!LAST) {
       mask(t + 1, nxt);
-      update(rowmax(nxt));
+      if (EXACT || track) {
+        update(rowmax(nxt));
+        if (!EXACT) track = pending(t + 2);
+      }
       // K(t+2) and V(t+1) must have landed (nothing younger is in flight)
       wait_vmcnt<0>();
       __syncthreads();
@@ -585,31 +602,62 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     }
   }
 
+  // Two passes at most. Every row's reference max is its first visible tile's
+  // max; it moves only by more than RESCALE_THRESH. The first pass takes row
+  // maxima only while a row lacks its reference (in the key-sparse modes with
+  // sinks, the first tile sets every row's), which keeps the max reduction
+  // off the per-tile path between the PV products and the barrier. A row
+  // whose max would have moved has a tile probability above
+  // 2^(RESCALE_THRESH - 1), hence a larger partial sum; if any row of the
+  // workgroup shows one (or a non-finite sum), all its tiles run again with
+  // every row max taken. Rows whose max never moves go through identical
+  // operations in both passes, so each row's bits are those of the exact
+  // pass whichever rows share its workgroup.
   f32x16 sa[NH], sb[NH];
-  if (nt > 0) {
-    // prologue: K(0), V(0), K(1); S(0) and its running max
-    issue_k(0, 0);
-    issue_v(0, 0);
-    if (nt > 1) issue_k(1, 1);
-    wait_vmcnt<0>();
-    __syncthreads();
-    qk(0, sa);
-    mask(0, sa);
-    update(rowmax(sa));
-    __syncthreads();   // every wave is done with K stage 0 before it is refilled
-  }
   using NotLast = std::integral_constant<bool, false>;
   using Last = std::integral_constant<bool, true>;
-  int t = 0;
-  for (; t + 2 < nt; t += 2) {
-    step(t, NotLast(), sa, sb);
-    step(t + 1, NotLast(), sb, sa);
-  }
-  if (t + 1 < nt) {          // two tiles left
-    step(t, NotLast(), sa, sb);
-    step(t + 1, Last(), sb, sa);
-  } else if (t < nt) {       // one tile left
-    step(t, Last(), sa, sb);
+  auto run = [&](auto exact_tag) __attribute__((always_inline)) {
+    constexpr bool EXACT = decltype(exact_tag)::value;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+    m_i = NEG_BIG;
+    l_i = 0.f;
+    if (nt > 0) {
+      // prologue: K(0), V(0), K(1); S(0) and its running max
+      issue_k(0, 0);
+      issue_v(0, 0);
+      if (nt > 1) issue_k(1, 1);
+      wait_vmcnt<0>();
+      __syncthreads();
+      qk(0, sa);
+      mask(0, sa);
+      update(rowmax(sa));
+      if (!EXACT) track = pending(1);
+      __syncthreads();   // every wave is done with K stage 0 before it is refilled
+    }
+    int t = 0;
+    for (; t + 2 < nt; t += 2) {
+      step(t, NotLast(), exact_tag, sa, sb);
+      step(t + 1, NotLast(), exact_tag, sb, sa);
+    }
+    if (t + 1 < nt) {          // two tiles left
+      step(t, NotLast(), exact_tag, sa, sb);
+      step(t + 1, Last(), exact_tag, sb, sa);
+    } else if (t < nt) {       // one tile left
+      step(t, Last(), exact_tag, sa, sb);
+    }
+  };
+  if constexpr (D > 128) {
+    // one wave per SIMD: the exact pass only (the first pass's second loop
+    // copy would not fit beside the head_dim-256 state without spills)
+    run(std::true_type());
+  } else {
+    run(std::false_type());
+    // the barrier inside also orders the first pass's last LDS reads before
+    // the second pass refills the stages
+    if (__syncthreads_or(valid && !(l_i <= 0.5f * RESCALE_LSUM))) run(std::true_type());
   }
 
   // ---- epilogue ----

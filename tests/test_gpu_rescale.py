@@ -2,10 +2,13 @@
 lot: key norms that grow along the sequence (the max rises tile after tile),
 rare outlier keys whose scores jump far above everything before them, and
 wide-range inputs. The running max of a row only moves when a tile's max
-exceeds it by more than 2^8 (log2 domain), per row; these inputs cross that
-threshold many times in every kernel: kernel (1), kernel (2) (split, merged),
-the fused layer and the decode rows, each against the oracle's exact softmax
-(delta_kernel.py:71-80 is the online-softmax reference)."""
+exceeds it by more than 40 (log2 domain), per row, and the kernels' first pass
+takes no per-tile row max at all: a workgroup with a row whose max would have
+moved runs its tiles again with every max taken. These inputs send workgroups
+through that second pass in every kernel: kernel (1), kernel (2) (split,
+merged), the fused layer and the decode rows, each against the oracle's exact
+softmax (delta_kernel.py:71-80 is the online-softmax reference), and rows keep
+the same bits whichever rows share their workgroup."""
 
 import numpy as np
 import pytest
@@ -91,3 +94,27 @@ def test_rescale_decode(gpu, kind):
         torch.cuda.synchronize()
         ref = O.decode_row(np64(q), np64(k), np64(v), window, sink, scale)
         assert_close(np64(got), ref, what=f"decode {kind} w{window}")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_rescale_bits_independent_of_packing(gpu, kind):
+    """GQA 4 packs two heads per key-sparse tile and four per query-sparse
+    tile; the same heads expanded to GQA 1 pack one. A row that needs its max
+    moved sends its whole workgroup through the exact pass, so the other rows
+    of that workgroup change pass with the packing: their bits must not."""
+    from delta_attention import ops
+    from delta_attention.delta_kernel import attention
+    from delta_attention.llama import repeat_kv
+    q, k, v = _inputs(kind, 1, 8, 2, 1500, 128, seed=45)
+    ke, ve = repeat_kv(k, 4), repeat_kv(v, 4)
+    scale = 128 ** -0.5
+    a = ops.sparse_attention(q, k, v, window=512, sink=16, sm_scale=scale)
+    b = ops.sparse_attention(q, ke, ve, window=512, sink=16, sm_scale=scale)
+    assert torch.equal(a, b)
+    rows = np.arange(0, 1500, 37)
+    rt = torch.from_numpy(rows)[None].cuda()
+    c = attention(q[:, :, rows], k, v, rt, scale)
+    d = attention(q[:, :, rows], ke, ve, rt, scale)
+    assert torch.equal(c, d)
+    ref = O.qsparse_attention(np64(q)[:, :, rows], np64(k), np64(v), rows, scale)
+    assert_close(np64(c), ref, what=f"query-sparse packing {kind}")
