@@ -36,6 +36,7 @@ struct CosArgs {
   int bins;
   float lo, hi;
   int B, n, H, D;
+  const int* n_dev;        // set: the delta count is min(*n_dev, n), read on the device
 };
 
 template <typename T>
@@ -63,12 +64,13 @@ template <typename T>
 __global__ __launch_bounds__(256) void anchor_cos_kernel(CosArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t pairs = (int64_t)a.B * (a.n - 1) * a.H;
+  const int n = a.n_dev ? min(max(*a.n_dev, 0), a.n) : a.n;
+  const int64_t pairs = n >= 2 ? (int64_t)a.B * (n - 1) * a.H : 0;
   if (p >= pairs) return;
   const int h = (int)(p % a.H);
   const int64_t t = p / a.H;
-  const int i = (int)(t % (a.n - 1));
-  const int b = (int)(t / (a.n - 1));
+  const int i = (int)(t % (n - 1));
+  const int b = (int)(t / (n - 1));
   float w12 = 0.f, w1 = 0.f, w2 = 0.f;
   for (int e = 2 * lane; e < a.D; e += 128) {
     float u0, u1, v0, v1;
@@ -92,6 +94,96 @@ __global__ __launch_bounds__(256) void anchor_cos_kernel(CosArgs a) {
     int bin = (int)((c - a.lo) * (float)a.bins / (a.hi - a.lo));
     if (bin >= a.bins) bin = a.bins - 1;
     atomicAdd(&a.hist[bin], 1);
+  }
+}
+
+// One chunk's decision of the adaptive stride (llama.py:784-805 with
+// stride.py:55-86), on the device so that the host enqueues every chunk
+// without reading anything back. One workgroup: the mean (fp64, fixed order)
+// and min of the chunk's b x (n-1) x h delta cosines (fewer than two anchors:
+// 1.0 and 1.0, as interanchor_cos returns), logged per chunk; the next stride
+// by the absolute rule (halve below `threshold`, double above threshold +
+// margin) or the relative one (halve below mu - k sd, double above mu + k sd
+// of the earlier chunks' means, population sd, at least two of them), clamped
+// to [gamma_min, gamma_max]; then the next chunk's anchor rows start + j *
+// gamma for j < ceil((end - start) / gamma), -1 for the rest of the max_n
+// slots (rows that the query-sparse kernel treats as empty).
+struct AdaptArgs {
+  const float* cos;        // [B, n - 1, H] of this chunk
+  int B, H;
+  int* state;              // {gamma, n} of this chunk; overwritten with the next chunk's
+  int chunk;               // this chunk's index into the logs
+  int next_start, next_end, max_n;
+  int64_t* rows_next;      // [max_n] or nullptr
+  int trigger;             // 0 absolute, 1 relative
+  double threshold, margin, k;
+  int gamma_min, gamma_max;
+  double* log_mean;
+  float* log_min;
+  int* log_gamma;
+  int* log_n;
+};
+
+__global__ __launch_bounds__(256) void adapt_next_kernel(AdaptArgs a) {
+  __shared__ double s_sum[256];
+  __shared__ float s_min[256];
+  __shared__ int s_next[2];
+  const int tid = threadIdx.x;
+  const int gamma = a.state[0];
+  const int n = a.state[1];
+  const int64_t pairs = n >= 2 ? (int64_t)a.B * (n - 1) * a.H : 0;
+  double sum = 0.0;
+  float mn = INFINITY;
+  for (int64_t p = tid; p < pairs; p += 256) {
+    const float c = a.cos[p];
+    sum += (double)c;
+    mn = fminf(mn, c);
+  }
+  s_sum[tid] = sum;
+  s_min[tid] = mn;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (tid < off) {
+      s_sum[tid] += s_sum[tid + off];
+      s_min[tid] = fminf(s_min[tid], s_min[tid + off]);
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const double mean = pairs > 0 ? s_sum[0] / (double)pairs : 1.0;
+    const float cmin = pairs > 0 ? s_min[0] : 1.0f;
+    a.log_mean[a.chunk] = mean;
+    a.log_min[a.chunk] = cmin;
+    a.log_gamma[a.chunk] = gamma;
+    a.log_n[a.chunk] = n;
+    int g = gamma;
+    if (a.trigger == 0) {
+      if (mean < a.threshold) g = max(gamma / 2, a.gamma_min);
+      else if (mean > a.threshold + a.margin) g = min(gamma * 2, a.gamma_max);
+    } else if (a.chunk >= 2) {
+      double mu = 0.0;
+      for (int i = 0; i < a.chunk; ++i) mu += a.log_mean[i];
+      mu /= (double)a.chunk;
+      double var = 0.0;
+      for (int i = 0; i < a.chunk; ++i) {
+        const double d = a.log_mean[i] - mu;
+        var += d * d;
+      }
+      const double sd = sqrt(var / (double)a.chunk);
+      if (mean < mu - a.k * sd) g = max(gamma / 2, a.gamma_min);
+      else if (mean > mu + a.k * sd) g = min(gamma * 2, a.gamma_max);
+    }
+    const int nn = a.next_end > a.next_start ? (a.next_end - a.next_start + g - 1) / g : 0;
+    s_next[0] = g;
+    s_next[1] = min(nn, a.max_n);
+    a.state[0] = g;
+    a.state[1] = min(nn, a.max_n);
+  }
+  __syncthreads();
+  if (a.rows_next) {
+    const int g = s_next[0], nn = s_next[1];
+    for (int j = tid; j < a.max_n; j += 256)
+      a.rows_next[j] = j < nn ? (int64_t)a.next_start + (int64_t)j * g : (int64_t)-1;
   }
 }
 
@@ -132,5 +224,49 @@ extern "C" int da_anchor_delta_cos(const void* a, const int64_t a_str[3],
     hipLaunchKernelGGL((anchor_cos_kernel<__bf16>), dim3((unsigned)grid), dim3(256), 0, s, c);
   else
     hipLaunchKernelGGL((anchor_cos_kernel<_Float16>), dim3((unsigned)grid), dim3(256), 0, s, c);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}
+
+extern "C" int da_adapt_chunk_step(const void* dense, const int64_t d_str[3],
+                                   const void* sparse, const int64_t s_str[3], int64_t n_rows,
+                                   const int64_t* rows, int B, int H, int D, int max_n,
+                                   int* state, float* cos_work, int chunk,
+                                   int next_start, int next_end, int64_t* rows_next,
+                                   int trigger, double threshold, double margin, double k,
+                                   int gamma_min, int gamma_max,
+                                   double* log_mean, float* log_min, int* log_gamma, int* log_n,
+                                   int dtype, void* stream) {
+  int rc;
+  if ((rc = check_common(B, H, H, D, dtype)) != DA_OK) return rc;
+  if (!dense || !d_str || !sparse || !s_str || n_rows < 1 || !rows || !state || !cos_work)
+    return DA_ERR_INVALID_ARG;
+  if (!log_mean || !log_min || !log_gamma || !log_n || chunk < 0) return DA_ERR_INVALID_ARG;
+  if (max_n < 1 || (trigger != 0 && trigger != 1) || gamma_min < 1 || gamma_max < gamma_min)
+    return DA_ERR_INVALID_ARG;
+  if (next_end > next_start && (next_start < 0 || !rows_next)) return DA_ERR_INVALID_ARG;
+  if (((uintptr_t)dense & 3u) || d_str[0] % 2 || d_str[1] % 2 || d_str[2] % 2) return DA_ERR_ALIGNMENT;
+  if (((uintptr_t)sparse & 3u) || s_str[0] % 2 || s_str[1] % 2 || s_str[2] % 2) return DA_ERR_ALIGNMENT;
+  const int64_t grid = ((int64_t)B * (max_n > 1 ? max_n - 1 : 1) * H + 3) / 4;
+  if (grid > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
+  CosArgs c = {};
+  c.a = dense; c.a_b = d_str[0]; c.a_n = d_str[1]; c.a_h = d_str[2];
+  c.s = sparse; c.s_b = s_str[0]; c.s_r = s_str[1]; c.s_h = s_str[2];
+  c.rows = rows; c.n_rows = n_rows;
+  c.cos = cos_work; c.B = B; c.n = max_n; c.H = H; c.D = D;
+  c.n_dev = state + 1;
+  AdaptArgs a = {};
+  a.cos = cos_work; a.B = B; a.H = H; a.state = state; a.chunk = chunk;
+  a.next_start = next_start; a.next_end = next_end; a.max_n = max_n;
+  a.rows_next = next_end > next_start ? rows_next : nullptr;
+  a.trigger = trigger; a.threshold = threshold; a.margin = margin; a.k = k;
+  a.gamma_min = gamma_min; a.gamma_max = gamma_max;
+  a.log_mean = log_mean; a.log_min = log_min; a.log_gamma = log_gamma; a.log_n = log_n;
+  hipStream_t st = (hipStream_t)stream;
+  (void)hipGetLastError();
+  if (dtype == DA_BF16)
+    hipLaunchKernelGGL((anchor_cos_kernel<__bf16>), dim3((unsigned)grid), dim3(256), 0, st, c);
+  else
+    hipLaunchKernelGGL((anchor_cos_kernel<_Float16>), dim3((unsigned)grid), dim3(256), 0, st, c);
+  hipLaunchKernelGGL(adapt_next_kernel, dim3(1), dim3(256), 0, st, a);
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }

@@ -117,6 +117,10 @@ struct AttnArgs {
   // [1, n_kv]) and chunk = ceil(list / n_splits): the launch stays valid as a
   // cache grows (decode rows under graph replay)
   const int* n_kv_dev;
+  // query-sparse mode: when set, only the first *n_rows_dev rows (clamped to
+  // [0, n_rows]) are computed; the items of their row tiles come first in the
+  // grid (plain block order) and the rest exit at once
+  const int* n_rows_dev;
   uint32_t* part_o; // [item][ws_rows][D / 2]: bf16 pairs of each row's O / l
   float* part_ml;   // [item][2][ws_rows]  (running max, row sum)
   int ws_rows;      // workspace rows per item: min(BM, n_rows * G) (a tile's valid rows)
@@ -227,12 +231,29 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   const int lg = lane >> 5;
 
   // ---- work item (XCD-aware: each XCD walks a contiguous range) ----
-  const int per_xcd = gridDim.x >> 3;
-  const int w = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (w >= a.n_items) return;
   constexpr bool KSPARSE = MODE != MODE_QSPARSE;
+  const bool live = !KSPARSE && a.n_rows_dev;
+  int w;
   int mt, split = 0, bh, hs = 0;
-  if (KSPARSE) {
+  if (live) {
+    // items of the live row tiles only: (bh, split, mt < mt_live), in block order
+    const int n_live = min(max(*a.n_rows_dev, 0), a.n_rows);
+    const int mt_live = (int)(((int64_t)n_live * a.G + BM - 1) / BM);
+    w = blockIdx.x;
+    if (mt_live == 0 || w >= a.B * a.Hkv * a.n_splits * mt_live) return;
+    const int t = w / mt_live;
+    mt = w - t * mt_live;
+    bh = (int)fdiv(t, a.fd_sp);
+    split = (int)fmodq(t, bh, a.fd_sp);
+    // partials keep the full grid's item index, which the merge recomputes
+    w = (bh * a.n_splits + split) * a.n_mtiles + mt;
+  } else {
+    const int per_xcd = gridDim.x >> 3;
+    w = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  }
+  if (w >= a.n_items) return;
+  if (live) {
+  } else if (KSPARSE) {
     // head split innermost: the tiles of one row block share K/V in L2
     const int t = (int)fdiv(w, a.fd_hs);
     hs = (int)fmodq(w, t, a.fd_hs);
@@ -861,7 +882,9 @@ struct MergeArgs {
   const int64_t* row_last;
   int64_t rl_b;
   int n_rows, G, Hkv, n_kv, n_mtiles, n_splits, chunk;
+  int B;
   const int* n_kv_dev;   // as in AttnArgs
+  const int* n_rows_dev; // as in AttnArgs: only the live row tiles are merged
   int window, sink;
   int lanes;        // P: threads sharing one (row, 8-column) task, splits s = p mod P
   int wgs;          // workgroups per row tile
@@ -886,8 +909,15 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   using E = Elt<T>;
   constexpr int CPR = D / 8;   // 8-column chunks per row
   __shared__ int s_hmax[4], s_lmin[4];
-  const int tile = blockIdx.x / a.wgs;
+  int tile = blockIdx.x / a.wgs;
   const int sub = blockIdx.x % a.wgs;
+  if (a.n_rows_dev) {
+    // live row tiles of every (b, kv head) first, as the split items
+    const int n_live = min(max(*a.n_rows_dev, 0), a.n_rows);
+    const int mt_live = (n_live * a.G + BM - 1) / BM;
+    if (mt_live == 0 || tile >= a.B * a.Hkv * mt_live) return;
+    tile = (tile / mt_live) * a.n_mtiles + tile % mt_live;
+  }
   const int mt = tile % a.n_mtiles;
   const int bh = tile / a.n_mtiles;
   const int hk = bh % a.Hkv;
@@ -1061,6 +1091,23 @@ static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
   const int64_t tiles = (int64_t)B * Hkv * (((int64_t)n * (Hq / Hkv) + BM - 1) / BM);
   if (tiles < 64) return plan_qsparse(B, Hq, Hkv, n, vis, D, 1024, 16);
   return plan_qsparse(B, Hq, Hkv, n, vis, D, DA_ROWS_ITEMS, 56);
+}
+
+// Split plan for n rows of which about n_live hold keys (the others are -1
+// rows with empty tile lists: the adaptive stride's padded row lists): the
+// items per row tile follow the plan of n_live rows, the grid covers all n.
+static QsparsePlan plan_rows_live(int B, int Hq, int Hkv, int n, int n_live, int Skv, int D) {
+  if (n_live >= n || n_live < 1) return plan_rows(B, Hq, Hkv, n, Skv, D);
+  QsparsePlan p = plan_rows(B, Hq, Hkv, n_live, Skv, D);
+  const int G = Hq / Hkv;
+  p.n_mtiles = (int)(((int64_t)n * G + BM - 1) / BM);
+  const int64_t base = (int64_t)B * Hkv * p.n_mtiles;
+  const int64_t items = base * p.n_splits;
+  const bool fits = p.n_items > 0 && items <= 0x7fffff00LL && base * 128 <= 0x7fffff00LL;
+  p.n_items = fits ? (int)items : 0;
+  p.ws_rows = (int)min((int64_t)BM, (int64_t)n * G);
+  p.ws_bytes = fits ? (size_t)p.n_items * p.ws_rows * (D * sizeof(uint16_t) + 2 * sizeof(float)) : 0;
+  return p;
 }
 
 // One decode row per batch at the end of the cache: its list is the sink
@@ -1244,7 +1291,8 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
                        int window, int sink, float sm_scale, void* workspace,
                        size_t workspace_bytes, int dtype, void* stream,
                        const int* n_kv_dev = nullptr, const void* add = nullptr,
-                       const int64_t* add_str = nullptr, float* lse = nullptr) {
+                       const int64_t* add_str = nullptr, float* lse = nullptr,
+                       const int* n_rows_dev = nullptr) {
   if (p.n_items <= 0) return DA_ERR_INVALID_ARG;
   if (!workspace || workspace_bytes < p.ws_bytes) return DA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DA_ERR_ALIGNMENT;
@@ -1265,6 +1313,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.q_rows = q_rows; a.row_last = row_last; a.rl_b = rl_bstride;
   a.chunk = p.chunk; a.n_splits = p.n_splits; a.n_kv_dev = n_kv_dev;
+  a.n_rows_dev = n_rows_dev;
   a.window = window; a.sink = sink;
   a.part_o = (uint32_t*)workspace;
   a.part_ml = (float*)((char*)workspace + (size_t)p.n_items * p.ws_rows * D * sizeof(uint16_t));
@@ -1274,6 +1323,7 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   m.q_rows = q_rows; m.row_last = row_last; m.rl_b = rl_bstride;
   m.n_rows = n; m.n_q = Sq; m.G = a.G; m.Hkv = Hkv; m.n_kv = Skv; m.n_mtiles = p.n_mtiles;
   m.n_splits = p.n_splits; m.chunk = p.chunk; m.n_kv_dev = n_kv_dev;
+  m.B = B; m.n_rows_dev = n_rows_dev;
   m.window = window; m.sink = sink;
   // P threads per (row, column chunk) task: about 4 splits each, up to 16;
   // workgroups per row tile cover its valid rows only
@@ -1324,10 +1374,11 @@ static int qsparse_fwd(const void* q, const void* k, const void* v,
                        void* o, const int64_t o_str[3],
                        int epi, int n_anchor, void* delta, const int64_t d_str[3],
                        float sm_scale, void* workspace, size_t workspace_bytes,
-                       int dtype, void* stream, float* lse) {
+                       int dtype, void* stream, float* lse, int n_live,
+                       const int* n_rows_dev = nullptr) {
   int rc;
   if ((rc = check_common(B, Hq, Hkv, D, dtype)) != DA_OK) return rc;
-  if (n < 0 || Sq < 0 || Skv < 0 || rl_bstride < 0) return DA_ERR_INVALID_ARG;
+  if (n < 0 || Sq < 0 || Skv < 0 || rl_bstride < 0 || n_live < 1) return DA_ERR_INVALID_ARG;
   if (epi != DA_EPI_OUTPUT && epi != DA_EPI_DELTA && epi != DA_EPI_SCATTER && epi != DA_EPI_DENSE)
     return DA_ERR_INVALID_ARG;
   if (!q_str || !k_str || !v_str || !o_str) return DA_ERR_INVALID_ARG;
@@ -1343,11 +1394,11 @@ static int qsparse_fwd(const void* q, const void* k, const void* v,
       !strides8(q_str) || !strides8(k_str) || !strides8(v_str) || !strides8(o_str))
     return DA_ERR_ALIGNMENT;
   if (!kv_rows_ok(k_str, v_str)) return DA_ERR_INVALID_ARG;
-  const QsparsePlan p = plan_rows(B, Hq, Hkv, n, Skv, D);
+  const QsparsePlan p = plan_rows_live(B, Hq, Hkv, n, n_live, Skv, D);
   return run_qsparse(p, q, k, v, q_rows, row_last, rl_bstride, n, B, Hq, Hkv, Sq, Skv, D,
                      q_str, k_str, v_str, o, o_str, epi, n_anchor, delta, d_str, 0, 0,
                      sm_scale, workspace, workspace_bytes, dtype, stream, nullptr, nullptr,
-                     nullptr, lse);
+                     nullptr, lse, n_rows_dev);
 }
 
 extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
@@ -1360,7 +1411,29 @@ extern "C" int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
                                    int dtype, void* stream) {
   return qsparse_fwd(q, k, v, q_rows, row_last, rl_bstride, n, B, Hq, Hkv, Sq, Skv, D, q_str,
                      k_str, v_str, o, o_str, epi, n_anchor, delta, d_str, sm_scale, workspace,
-                     workspace_bytes, dtype, stream, nullptr);
+                     workspace_bytes, dtype, stream, nullptr, 0x7fffffff);
+}
+
+extern "C" size_t da_qsparse_workspace_bytes_live(int B, int Hq, int Hkv, int n, int n_live, int Skv,
+                                                  int D) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || n < 1 || n_live < 1 || Skv < 1 ||
+      !head_dim_ok(D))
+    return 0;
+  return plan_rows_live(B, Hq, Hkv, n, n_live, Skv, D).ws_bytes;
+}
+
+extern "C" int da_qsparse_attn_fwd_live(const void* q, const void* k, const void* v,
+                                        const int64_t* q_rows, const int64_t* row_last,
+                                        int64_t rl_bstride, int n, int n_live,
+                                        const int* n_dev, int B, int Hq,
+                                        int Hkv, int Sq, int Skv, int D, const int64_t q_str[3],
+                                        const int64_t k_str[3], const int64_t v_str[3],
+                                        void* o, const int64_t o_str[3], float sm_scale,
+                                        void* workspace, size_t workspace_bytes, int dtype,
+                                        void* stream) {
+  return qsparse_fwd(q, k, v, q_rows, row_last, rl_bstride, n, B, Hq, Hkv, Sq, Skv, D, q_str,
+                     k_str, v_str, o, o_str, DA_EPI_OUTPUT, 0, nullptr, nullptr, sm_scale,
+                     workspace, workspace_bytes, dtype, stream, nullptr, n_live, n_dev);
 }
 
 extern "C" int da_qsparse_attn_fwd_lse(const void* q, const void* k, const void* v,
@@ -1375,7 +1448,7 @@ extern "C" int da_qsparse_attn_fwd_lse(const void* q, const void* k, const void*
   if (((uintptr_t)lse & 3u) != 0) return DA_ERR_ALIGNMENT;
   return qsparse_fwd(q, k, v, q_rows, row_last, rl_bstride, n, B, Hq, Hkv, Sq, Skv, D, q_str,
                      k_str, v_str, o, o_str, DA_EPI_OUTPUT, 0, nullptr, nullptr, sm_scale,
-                     workspace, workspace_bytes, dtype, stream, lse);
+                     workspace, workspace_bytes, dtype, stream, lse, 0x7fffffff);
 }
 
 extern "C" size_t da_decode_workspace_bytes(int B, int Hq, int Hkv, int n_keys, int D, int window,

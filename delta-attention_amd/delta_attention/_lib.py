@@ -55,6 +55,9 @@ EXPORTS = (
     "da_build_target",
     "da_decode_scratch_bytes",
     "da_decode_attn_fwd_dev_noalloc",
+    "da_adapt_chunk_step",
+    "da_qsparse_workspace_bytes_live",
+    "da_qsparse_attn_fwd_live",
 )
 
 _ERR_TEXT = {
@@ -179,6 +182,17 @@ def _load() -> ctypes.CDLL:
     L.da_decode_attn_fwd_dev_noalloc.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i,
                                                  _p3, _p3, _p3, _p3, _i, _i, _f, _vp, _p3,
                                                  _i, _vp]
+    L.da_qsparse_workspace_bytes_live.restype = _sz
+    L.da_qsparse_workspace_bytes_live.argtypes = [_i, _i, _i, _i, _i, _i, _i]
+    L.da_qsparse_attn_fwd_live.restype = _i
+    L.da_qsparse_attn_fwd_live.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _vp,
+                                           _i, _i, _i, _i, _i, _i,
+                                           _p3, _p3, _p3, _vp, _p3, _f, _vp, _sz, _i, _vp]
+    L.da_adapt_chunk_step.restype = _i
+    L.da_adapt_chunk_step.argtypes = [_vp, _p3, _vp, _p3, _i64, _vp, _i, _i, _i, _i,
+                                      _vp, _vp, _i, _i, _i, _vp,
+                                      _i, ctypes.c_double, ctypes.c_double, ctypes.c_double, _i, _i,
+                                      _vp, _vp, _vp, _vp, _i, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
     return L

@@ -274,13 +274,19 @@ class LlamaAttention(nn.Module):
         chunk's mean consecutive-delta cosine, variable-stride broadcast
         (kernel 3 with an anchor list), dense cut_n tail.
 
-        The result equals the reference's cat(apply_delta_variable(...),
-        tail_dense), assembled in place in the sparse pass's output: the anchor
-        deltas rnd(dense - sparse[:, idx]) are formed first (the rounding of
-        stride.py:38), the broadcast then adds them row by row, and the tail
-        rows are written by the query-sparse kernel's scatter epilogue. The
-        chunks' dense rows read q through a row list, not a gathered copy."""
-        from .stride import effective_sparsity, interanchor_cos, next_gamma, next_gamma_relative, plan_chunks
+        The chunk loop runs without reading anything back: each chunk's dense
+        anchor rows (kernel (2) over a row list of max_n slots, -1 past the
+        chunk's anchors), then da_adapt_chunk_step, which takes the chunk's
+        delta cosines rnd(dense - sparse[idx]), logs their mean / min, picks the
+        next stride (stride.py:55-86) and writes the next chunk's row list, all
+        on the device. One read of the per-chunk log after the loop gives the
+        anchor list. The result equals the reference's
+        cat(apply_delta_variable(...), tail_dense), assembled in place in the
+        sparse pass's output: the anchor deltas rnd(dense - sparse[:, idx]) are
+        formed first (the rounding of stride.py:38), the broadcast then adds
+        them row by row, and the tail rows are written by the query-sparse
+        kernel's scatter epilogue."""
+        from .stride import ADAPT_MARGIN, effective_sparsity, plan_chunks
 
         cfg = self.config
         device = query_states.device
@@ -290,32 +296,61 @@ class LlamaAttention(nn.Module):
             q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
         if out.dtype != q.dtype:
             out = out.to(q.dtype)
+        out = out.contiguous()
         scale = float(scaling)
-        gamma_c = int(cfg.delta_lambda)
+        b, h, _, d = q.shape
+        gamma0 = int(cfg.delta_lambda)
+        g_min, g_max = int(cfg.gamma_min), int(cfg.gamma_max)
         trigger = getattr(cfg, "stride_trigger", "absolute")
-        cos_history, idx_parts, dense_parts, chunk_log = [], [], [], []
-        for start, end in plan_chunks(s_p, int(cfg.adapt_chunk)):
-            c_idx = torch.arange(start, end, step=gamma_c, device=device)
-            # the chunk's rows see keys < end: the split plan sizes its items for that
-            dense_c = ops.qsparse_attention(q, k[:, :, :end], v[:, :, :end], c_idx, scale,
-                                            q_rows=c_idx).transpose(1, 2)
-            # deltas rnd(dense - sparse) at the chunk's anchors, formed in the kernel
-            cos_mean, cos_min = interanchor_cos(dense_c, sparse=out, rows=c_idx)
-            idx_parts.append(c_idx)
-            dense_parts.append(dense_c)
-            chunk_log.append({"start": int(start), "gamma": int(gamma_c), "cos_mean": cos_mean,
-                              "cos_min": cos_min, "n_anchors": int(c_idx.numel())})
-            if trigger == "relative":
-                gamma_c = next_gamma_relative(cos_mean, cos_history, gamma_c,
-                                              k=float(getattr(cfg, "adapt_k", 2.0)),
-                                              gamma_min=int(cfg.gamma_min), gamma_max=int(cfg.gamma_max))
-                cos_history.append(cos_mean)
-            else:
-                gamma_c = next_gamma(cos_mean, gamma_c, threshold=float(cfg.adapt_threshold),
-                                     gamma_min=int(cfg.gamma_min), gamma_max=int(cfg.gamma_max))
-        idx = torch.cat(idx_parts)
-        delta = torch.cat(dense_parts, dim=1) - out[:, idx]        # bf16: one rounding
-        ops.delta_add(out, s_p=s_p, out=out, delta=delta, anchors=idx)
+        chunks = plan_chunks(s_p, int(cfg.adapt_chunk))
+        nc = len(chunks)
+        idx = torch.empty(0, dtype=torch.int64, device=device)
+        chunk_log = []
+        if nc > 0:
+            # anchor slots per chunk: the finest stride a chunk can get
+            g_low = max(1, min(gamma0, g_min))
+            max_n = max(-(-(end - start) // g_low) for start, end in chunks)
+            # split plans sized for a chunk at the starting stride
+            n_live = min(max_n, max(1, -(-int(cfg.adapt_chunk) // max(gamma0, 1))))
+            rows_all = torch.full((nc, max_n), -1, dtype=torch.int64)
+            first = torch.arange(chunks[0][0], chunks[0][1], gamma0, dtype=torch.int64)
+            rows_all[0, :first.numel()] = first
+            rows_all = rows_all.to(device)
+            state = torch.tensor([gamma0, first.numel()], dtype=torch.int32).to(device)
+            dense_all = torch.empty((b, h, nc * max_n, d), dtype=q.dtype, device=device)
+            cos_work = torch.empty(b * max(max_n - 1, 1) * h, dtype=torch.float32, device=device)
+            log_mean = torch.empty(nc, dtype=torch.float64, device=device)
+            log_min = torch.empty(nc, dtype=torch.float32, device=device)
+            log_gamma = torch.empty(nc, dtype=torch.int32, device=device)
+            log_n = torch.empty(nc, dtype=torch.int32, device=device)
+            for c, (start, end) in enumerate(chunks):
+                dense_c = dense_all[:, :, c * max_n:(c + 1) * max_n]
+                # the chunk's rows see keys < end: the split plan sizes its items for that
+                ops.qsparse_attention(q, k[:, :, :end], v[:, :, :end], rows_all[c], scale,
+                                      q_rows=rows_all[c], out=dense_c, n_live=n_live,
+                                      n_dev=state[1:2])
+                nxt = chunks[c + 1] if c + 1 < nc else (0, 0)
+                ops.adapt_chunk_step(
+                    dense_c.transpose(1, 2), out, rows_all[c], state, cos_work, chunk=c,
+                    next_start=nxt[0], next_end=nxt[1],
+                    rows_next=rows_all[c + 1] if c + 1 < nc else None, trigger=trigger,
+                    threshold=float(cfg.adapt_threshold), margin=ADAPT_MARGIN,
+                    k=float(getattr(cfg, "adapt_k", 2.0)), gamma_min=g_min, gamma_max=g_max,
+                    log_mean=log_mean, log_min=log_min, log_gamma=log_gamma, log_n=log_n)
+            # the one read-back of the layer: per-chunk stride, anchors and cosines
+            lg, ln = log_gamma.tolist(), log_n.tolist()
+            lm, lmin = log_mean.tolist(), log_min.tolist()
+            idx_parts, slots = [], []
+            for c, (start, end) in enumerate(chunks):
+                n_c = int(ln[c])
+                idx_parts.append(torch.arange(start, end, lg[c], dtype=torch.int64))
+                slots.append(torch.arange(c * max_n, c * max_n + n_c, dtype=torch.int64))
+                chunk_log.append({"start": int(start), "gamma": int(lg[c]), "cos_mean": float(lm[c]),
+                                  "cos_min": float(lmin[c]), "n_anchors": n_c})
+            idx = torch.cat(idx_parts).to(device)
+            dense_sel = dense_all.index_select(2, torch.cat(slots).to(device)).transpose(1, 2)
+            delta = dense_sel - out[:, idx]        # bf16: one rounding
+            ops.delta_add(out, s_p=s_p, out=out, delta=delta, anchors=idx)
         tail_idx = torch.arange(s_p, s, device=device)
         ops.qsparse_attention(q, k, v, tail_idx, scale, q_rows=tail_idx, epi=L.DA_EPI_SCATTER, out=out)
         self._stride_stats = {

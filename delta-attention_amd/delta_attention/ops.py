@@ -155,9 +155,16 @@ def qsparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                       q_rows: Optional[torch.Tensor] = None,
                       epi: int = L.DA_EPI_OUTPUT, out: Optional[torch.Tensor] = None,
                       n_anchor: int = 0, delta: Optional[torch.Tensor] = None,
-                      workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      workspace: Optional[torch.Tensor] = None,
+                      n_live: Optional[int] = None,
+                      n_dev: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Query-sparse, key-dense attention: selected row i attends keys
     0..row_last[i] (inclusive), split over the key axis on the GPU.
+
+    n_live (DA_EPI_OUTPUT only): about this many rows hold keys, the others
+    being -1 rows; the split plan is sized for them (da_qsparse_attn_fwd_live).
+    n_dev: with n_live, a device int32 holding the live row count; rows in
+    row tiles wholly past it are neither computed nor written.
 
     q [B,H,Sq,D]; k/v [B,Hkv,Skv,D] (GQA native, any strides);
     q_rows: optional [n] int64 rows of q to use (default: rows 0..n-1, n = len(row_last)).
@@ -191,6 +198,25 @@ def qsparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if epi in (L.DA_EPI_DELTA, L.DA_EPI_DENSE) and n_anchor > 0:
         assert delta is not None and delta.shape == (B, n_anchor, H, D) and delta.dtype == q.dtype
         d_str = L.strides3(delta.stride(0), delta.stride(2), delta.stride(1))
+    if n_live is not None and n > 0:
+        assert epi == L.DA_EPI_OUTPUT and n_live >= 1
+        if n_dev is not None:
+            assert n_dev.dtype == torch.int32 and n_dev.device == dev
+        if workspace is None:
+            nb = L.lib().da_qsparse_workspace_bytes_live(B, H, Hkv, n, int(n_live), Skv, D)
+            assert nb > 0, "selected-rows launch too large"
+            workspace = torch.empty(nb, dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            rc = L.lib().da_qsparse_attn_fwd_live(
+                _ptr(q), _ptr(k), _ptr(v), _ptr(q_rows), _ptr(rl), int(rl_b),
+                n, int(n_live), _ptr(n_dev), B, H, Hkv, Sq, Skv, D,
+                L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+                L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+                L.strides3(v.stride(0), v.stride(1), v.stride(2)),
+                _ptr(out), o_str, float(sm_scale), _ptr(workspace), workspace.numel(), _code(q),
+                _stream(dev))
+        L.check(rc, "da_qsparse_attn_fwd_live")
+        return out
     if workspace is None:
         workspace = qsparse_workspace(B, H, Hkv, n, Skv, D, dev)
     with torch.cuda.device(dev):
@@ -613,6 +639,42 @@ def anchor_delta_cos(a: torch.Tensor, *, sparse: Optional[torch.Tensor] = None,
             float(hist_range[0]), float(hist_range[1]), code, _stream(dev))
     L.check(rc, "da_anchor_delta_cos")
     return (cos, hist) if hist_bins > 0 else cos
+
+
+def adapt_chunk_step(dense: torch.Tensor, sparse: torch.Tensor, rows: torch.Tensor,
+                     state: torch.Tensor, cos_work: torch.Tensor, *, chunk: int,
+                     next_start: int, next_end: int, rows_next: Optional[torch.Tensor],
+                     trigger: str, threshold: float, margin: float, k: float,
+                     gamma_min: int, gamma_max: int, log_mean: torch.Tensor,
+                     log_min: torch.Tensor, log_gamma: torch.Tensor, log_n: torch.Tensor) -> None:
+    """One chunk's stride decision of the adaptive path on the device
+    (da_adapt_chunk_step): the chunk's delta cosines rnd(dense - sparse[rows])
+    over its first state[1] anchors, their mean / min into the logs, the next
+    stride into state[0] and the next chunk's anchor rows into rows_next.
+
+    dense [B, max_n, H, D] (any strides with rows contiguous), sparse
+    [B, S, H, D]; rows / rows_next int64 [max_n] (-1 past the anchors);
+    state int32 [2]; cos_work fp32 >= B * (max_n - 1) * H; logs [n_chunks]
+    (fp64 mean, fp32 min, int32 stride, int32 anchors)."""
+    B, max_n, H, D = dense.shape
+    dev = _on_gpu(dense, sparse, rows, state, cos_work, log_mean, log_min, log_gamma, log_n)
+    assert sparse.shape[0] == B and sparse.shape[2:] == (H, D) and sparse.dtype == dense.dtype
+    assert rows.dtype == torch.int64 and rows.is_contiguous() and rows.numel() == max_n
+    assert state.dtype == torch.int32 and state.numel() >= 2
+    assert cos_work.dtype == torch.float32 and cos_work.numel() >= B * max(max_n - 1, 1) * H
+    assert log_mean.dtype == torch.float64 and log_min.dtype == torch.float32
+    assert log_gamma.dtype == torch.int32 and log_n.dtype == torch.int32
+    assert trigger in ("absolute", "relative"), trigger
+    if rows_next is not None:
+        assert rows_next.dtype == torch.int64 and rows_next.is_contiguous() and rows_next.numel() == max_n
+    with torch.cuda.device(dev):
+        rc = L.lib().da_adapt_chunk_step(
+            _ptr(dense), L.I64x3(*dense.stride()[:3]), _ptr(sparse), L.I64x3(*sparse.stride()[:3]),
+            int(sparse.shape[1]), _ptr(rows), B, H, D, max_n, _ptr(state), _ptr(cos_work), int(chunk),
+            int(next_start), int(next_end), _ptr(rows_next), 0 if trigger == "absolute" else 1,
+            float(threshold), float(margin), float(k), int(gamma_min), int(gamma_max),
+            _ptr(log_mean), _ptr(log_min), _ptr(log_gamma), _ptr(log_n), _code(dense), _stream(dev))
+    L.check(rc, "da_adapt_chunk_step")
 
 
 def anchor_layout(s: int, gamma: int) -> Tuple[int, int, int]:

@@ -145,6 +145,26 @@ int da_qsparse_attn_fwd(const void* q, const void* k, const void* v,
                         float sm_scale, void* workspace, size_t workspace_bytes,
                         int dtype, void* stream);
 
+/* da_qsparse_attn_fwd (DA_EPI_OUTPUT) for a row list of n slots of which
+ * about n_live hold keys: the split items per row tile follow the plan of
+ * n_live rows and the grid covers all n, so a padded list keeps the
+ * parallelism of its live rows. n_dev: NULL, or a device int, read on the
+ * device, saying that only the first *n_dev rows (clamped to [0, n]) are
+ * live; their row tiles' items come first in the grid, the others exit at
+ * once, and output rows in row tiles wholly past *n_dev are not written.
+ * For the adaptive stride's chunk lists, whose length is decided on the
+ * device (n = the chunk's anchor slots at the finest stride). No counterpart
+ * in the reference, whose chunk lists have host-known lengths.
+ * workspace must hold da_qsparse_workspace_bytes_live(...) bytes. */
+size_t da_qsparse_workspace_bytes_live(int B, int Hq, int Hkv, int n, int n_live, int Skv, int D);
+int da_qsparse_attn_fwd_live(const void* q, const void* k, const void* v,
+                             const int64_t* q_rows, const int64_t* row_last, int64_t rl_bstride,
+                             int n, int n_live, const int* n_dev,
+                             int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                             const int64_t q_str[3], const int64_t k_str[3], const int64_t v_str[3],
+                             void* o, const int64_t o_str[3], float sm_scale,
+                             void* workspace, size_t workspace_bytes, int dtype, void* stream);
+
 /*
  * Decode row: the query at the end of a KV cache of n_keys keys (position
  * n_keys - 1) attends keys [0, sink) and its last `window` keys
@@ -321,6 +341,41 @@ int da_anchor_delta_cos(const void* a, const int64_t a_str[3],
                         const int64_t* rows, int64_t n_rows,
                         int B, int n, int H, int D,
                         float* cos_out, int* hist, int bins, float lo, float hi,
+                        int dtype, void* stream);
+
+/* One chunk of the adaptive stride (llama.py:779-805: interanchor_cos of the
+ * chunk's deltas, then stride.py:55-62 next_gamma or stride.py:65-86
+ * next_gamma_relative) decided on the device, so that the host enqueues every
+ * chunk of delta_adaptive_forward without reading a value back; the reference
+ * reads each chunk's mean cosine on the host. Two launches on `stream`:
+ *   1. the cosines of da_anchor_delta_cos over the chunk's first n deltas,
+ *      rnd(dense_i - sparse[b, rows[i], h]), into cos_work (>= B*(max_n-1)*H
+ *      floats), with n = state[1] read on the device;
+ *   2. one workgroup: their mean (fp64) and min (n < 2: 1.0 and 1.0) into
+ *      log_mean[chunk] / log_min[chunk], this chunk's stride and n into
+ *      log_gamma[chunk] / log_n[chunk]; the next stride by the absolute rule
+ *      (trigger 0: halve below threshold, double above threshold + margin) or
+ *      the relative one (trigger 1: against mu -/+ k * sd of log_mean[0 ..
+ *      chunk-1], population sd, once two chunks are logged), clamped to
+ *      [gamma_min, gamma_max]; state = {next stride, next n}; and, when
+ *      next_end > next_start, rows_next[j] = next_start + j * stride for
+ *      j < next n, -1 for the remaining max_n slots (da_qsparse_attn_fwd
+ *      gives a -1 row an all-zero output).
+ *   dense   [B, max_n, H, D] (strides batch, anchor, head): the chunk's dense
+ *           anchor rows; sparse [B, n_rows, H, D] (strides batch, row, head).
+ *   rows    device int64 [max_n]: the chunk's anchor rows (-1 past n).
+ *   state   device int32 [2]: {stride, n} of this chunk (the caller writes the
+ *           first chunk's).
+ * Element strides must be even. No counterpart entry point in the reference
+ * (it runs these steps as host code). */
+int da_adapt_chunk_step(const void* dense, const int64_t d_str[3],
+                        const void* sparse, const int64_t s_str[3], int64_t n_rows,
+                        const int64_t* rows, int B, int H, int D, int max_n,
+                        int* state, float* cos_work, int chunk,
+                        int next_start, int next_end, int64_t* rows_next,
+                        int trigger, double threshold, double margin, double k,
+                        int gamma_min, int gamma_max,
+                        double* log_mean, float* log_min, int* log_gamma, int* log_n,
                         int dtype, void* stream);
 
 /*

@@ -266,6 +266,46 @@ def test_anchor_delta_cos_checks(lib):
     assert call(a_str=_s3(64 * 8 * 128, 8 * 128, 127)) == L.DA_ERR_ALIGNMENT
 
 
+def test_adapt_chunk_step_checks(lib):
+    """Refusals of the adaptive stride's device-side chunk step (every check
+    precedes the launches; nothing runs on a GPU here)."""
+    P = ctypes.c_void_p
+    d3 = _s3(64 * 8 * 128, 8 * 128, 128)
+
+    def call(dense=16, sparse=16, rows=16, state=16, cos=16, logs=16, max_n=64, D=128,
+             dtype=L.DA_BF16, trigger=0, gmin=16, gmax=128, chunk=0, nxt=(0, 0), rows_next=None,
+             n_rows=4096, d_str=d3):
+        return lib.da_adapt_chunk_step(
+            P(dense) if dense else None, d_str, P(sparse) if sparse else None, d3, n_rows,
+            P(rows) if rows else None, 1, 8, D, max_n, P(state) if state else None,
+            P(cos) if cos else None, chunk, nxt[0], nxt[1], P(rows_next) if rows_next else None,
+            trigger, 0.95, 0.02, 2.0, gmin, gmax,
+            P(logs) if logs else None, P(logs) if logs else None, P(logs) if logs else None,
+            P(logs) if logs else None, dtype, None)
+    assert call(dtype=7) == L.DA_ERR_DTYPE
+    assert call(D=80) == L.DA_ERR_HEAD_DIM
+    for kw in ({"dense": 0}, {"sparse": 0}, {"rows": 0}, {"state": 0}, {"cos": 0}, {"logs": 0},
+               {"max_n": 0}, {"trigger": 2}, {"gmin": 0}, {"gmin": 64, "gmax": 32}, {"chunk": -1},
+               {"n_rows": 0}, {"nxt": (4096, 8192)}, {"nxt": (-1, 8), "rows_next": 16}):
+        assert call(**kw) == L.DA_ERR_INVALID_ARG, kw
+    assert call(dense=18) == L.DA_ERR_ALIGNMENT
+    assert call(d_str=_s3(64 * 8 * 128, 8 * 128, 127)) == L.DA_ERR_ALIGNMENT
+
+
+def test_qsparse_live_plan_sizes(lib):
+    """The live-rows plan: the grid (and the workspace's item count) covers
+    all n slots, the splits per row tile follow n_live rows; n_live >= n is the
+    plain plan, n_live < 1 is refused."""
+    plain = lib.da_qsparse_workspace_bytes(1, 32, 8, 256, 131072, 128)
+    assert lib.da_qsparse_workspace_bytes_live(1, 32, 8, 256, 256, 131072, 128) == plain
+    assert lib.da_qsparse_workspace_bytes_live(1, 32, 8, 256, 1000, 131072, 128) == plain
+    assert lib.da_qsparse_workspace_bytes_live(1, 32, 8, 256, 0, 131072, 128) == 0
+    # 64 live rows of 256: the short-list plan's splits over all 8 row tiles per kv head
+    live = lib.da_qsparse_workspace_bytes_live(1, 32, 8, 256, 64, 131072, 128)
+    small = lib.da_qsparse_workspace_bytes(1, 32, 8, 64, 131072, 128)
+    assert live == 4 * small
+
+
 def test_split_plans_refuse_grid_overflow(lib):
     # a selected-rows launch whose work items would not fit a 32-bit grid
     assert lib.da_qsparse_workspace_bytes(1, 32, 8, 2_000_000_000, 131072, 128) == 0

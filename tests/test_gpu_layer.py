@@ -177,6 +177,59 @@ def test_adaptive_stride_path(gpu, mode):
     assert_close(np64(out), ref, what=f"adaptive ({mode})")
 
 
+@pytest.mark.parametrize("trigger,threshold,k", [("absolute", None, 2.0), ("relative", 0.95, 0.3)])
+def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold, k):
+    """The adaptive chunk loop decides each next stride on the device
+    (da_adapt_chunk_step). Checked against the host rules of stride.py:
+    every logged stride follows from the previous chunk's logged mean by
+    next_gamma / next_gamma_relative, and each logged mean and min equal the
+    chunk deltas' cosines recomputed here from the layer's own sparse pass
+    and dense anchor rows (anchor_delta_cos, fp64 mean). The absolute
+    threshold is set between the chunk means of a first run, so that the
+    stride does move."""
+    from delta_attention import ops
+    from delta_attention.llama import LlamaAttention
+    from delta_attention.stride import next_gamma, next_gamma_relative
+    s, chunk, window, sink = 4096, 256, 256, 16
+    q, k_, v = gen_qkv(1, 8, 2, s, 128, seed=12)
+
+    def run(thr):
+        cfg = _cfg(8, 2, 128, stride_policy="adaptive", adapt_chunk=chunk, delta_lambda=32,
+                   adapt_threshold=thr, gamma_min=8, gamma_max=128, stride_trigger=trigger,
+                   adapt_k=k, sliding_window=window, sink_tokens=sink)
+        m = LlamaAttention(cfg, layer_idx=0).cuda().to(torch.bfloat16)
+        m.delta_forward(m, q, k_, v, None, scaling=m.scaling)
+        torch.cuda.synchronize()
+        return m._stride_stats["chunks"]
+
+    if threshold is None:
+        means = sorted(c["cos_mean"] for c in run(0.5))
+        threshold = means[len(means) // 2]
+    chunks = run(threshold)
+    gammas = [c["gamma"] for c in chunks]
+    assert len(set(gammas)) > 1, gammas
+    for c in range(len(chunks) - 1):
+        g, cm = chunks[c]["gamma"], chunks[c]["cos_mean"]
+        if trigger == "absolute":
+            want = next_gamma(cm, g, threshold=threshold, gamma_min=8, gamma_max=128)
+        else:
+            want = next_gamma_relative(cm, [x["cos_mean"] for x in chunks[:c]], g, k=k,
+                                       gamma_min=8, gamma_max=128)
+        assert chunks[c + 1]["gamma"] == want, (c, chunks[c], chunks[c + 1])
+    sparse = ops.sparse_attention(q, k_, v, window=window, sink=sink, sm_scale=128 ** -0.5)
+    for c in chunks:
+        rows = torch.arange(c["start"], c["start"] + chunk, c["gamma"], device="cuda")
+        rows = rows[rows < s - (s % 32 + 128)]
+        assert rows.numel() == c["n_anchors"]
+        dense = ops.qsparse_attention(q, k_, v, rows, 128 ** -0.5, q_rows=rows).transpose(1, 2)
+        if rows.numel() < 2:
+            assert c["cos_mean"] == 1.0 and c["cos_min"] == 1.0
+            continue
+        cos = ops.anchor_delta_cos(dense, sparse=sparse, rows=rows).cpu().double().numpy()
+        assert abs(cos.mean() - c["cos_mean"]) <= 1e-12, (cos.mean(), c)
+        assert float(cos.min()) == c["cos_min"]
+
+
 def test_adaptive_policy_sparse_only_returns_the_sparse_pass(gpu):
     """mode "sparse-only" returns before the adaptive branch (llama.py:695-696)."""
     from delta_attention.llama import LlamaAttention
