@@ -108,6 +108,7 @@ struct AttnArgs {
   int n_items;      // work items before padding the grid to a multiple of 8
   float scale_log2; // sm_scale * log2(e)
   int window, sink, q_block;
+  int row0;         // key-sparse mode: query row of local row 0 (rows row0 .. row0 + n_rows - 1)
   const int64_t* q_rows;
   const int64_t* row_last;
   int64_t rl_b;
@@ -280,7 +281,7 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   const int mflat = mt * BM + wave * 32 + ln;
   const bool valid = mflat < a.n_rows * GT;
   const int mq = (int)fdiv(mflat, a.fd_gt);
-  const int irow = valid ? mq : 0;
+  const int irow = (KSPARSE ? a.row0 : 0) + (valid ? mq : 0);
   const int hin = valid ? (int)fmodq(mflat, mq, a.fd_gt) : 0;   // head within the tile
   const int hrow = hk * G + hs * GT + hin;
   int qrow, lo, hi;
@@ -320,8 +321,8 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   if (KSPARSE) {
     // the tile holds rows r0 .. r1 (BM / GT of them, the last tile fewer);
     // hi = row and lo grow with the row
-    const int r0 = mt * a.tile_rows;
-    const int r1 = min(r0 + a.tile_rows, a.n_rows) - 1;
+    const int r0 = a.row0 + mt * a.tile_rows;
+    const int r1 = min(r0 + a.tile_rows, a.row0 + a.n_rows) - 1;
     hi_min = r0;
     hi_max = r1;
     lo_min = (int)fdiv(r0, a.fd_qb) * a.q_block + a.q_block - a.window;
@@ -1214,6 +1215,26 @@ extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, v
   int rc = sparse_args(a, q, k, v, out, B, Hq, Hkv, S, D, q_str, k_str, v_str, o_str,
                        window, sink, q_block, sm_scale, dtype);
   if (rc != DA_OK || S == 0) return rc;
+  if ((rc = sparse_items(a)) != DA_OK) return rc;
+  (void)hipGetLastError();
+  dispatch_attn<MODE_SPARSE>(a, D, dtype, (hipStream_t)stream);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
+}
+
+extern "C" int da_sparse_attn_fwd_rows(const void* q, const void* k, const void* v, void* out,
+                                       int B, int Hq, int Hkv, int S, int D,
+                                       const int64_t q_str[3], const int64_t k_str[3],
+                                       const int64_t v_str[3], const int64_t o_str[3],
+                                       int window, int sink, int q_block, float sm_scale,
+                                       int row0, int n_rows, int dtype, void* stream) {
+  AttnArgs a;
+  int rc = sparse_args(a, q, k, v, out, B, Hq, Hkv, S, D, q_str, k_str, v_str, o_str,
+                       window, sink, q_block, sm_scale, dtype);
+  if (rc != DA_OK) return rc;
+  if (row0 < 0 || n_rows < 0 || (int64_t)row0 + n_rows > S) return DA_ERR_INVALID_ARG;
+  if (S == 0 || n_rows == 0) return DA_OK;
+  a.row0 = row0;
+  a.n_rows = n_rows;
   if ((rc = sparse_items(a)) != DA_OK) return rc;
   (void)hipGetLastError();
   dispatch_attn<MODE_SPARSE>(a, D, dtype, (hipStream_t)stream);

@@ -58,6 +58,7 @@ EXPORTS = (
     "da_adapt_chunk_step",
     "da_qsparse_workspace_bytes_live",
     "da_qsparse_attn_fwd_live",
+    "da_sparse_attn_fwd_rows",
 )
 
 _ERR_TEXT = {
@@ -188,6 +189,9 @@ def _load() -> ctypes.CDLL:
     L.da_qsparse_attn_fwd_live.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _vp,
                                            _i, _i, _i, _i, _i, _i,
                                            _p3, _p3, _p3, _vp, _p3, _f, _vp, _sz, _i, _vp]
+    L.da_sparse_attn_fwd_rows.restype = _i
+    L.da_sparse_attn_fwd_rows.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                          _p3, _p3, _p3, _p3, _i, _i, _i, _f, _i, _i, _i, _vp]
     L.da_adapt_chunk_step.restype = _i
     L.da_adapt_chunk_step.argtypes = [_vp, _p3, _vp, _p3, _i64, _vp, _i, _i, _i, _i,
                                       _vp, _vp, _i, _i, _i, _vp,

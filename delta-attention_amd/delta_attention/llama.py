@@ -244,12 +244,10 @@ class LlamaAttention(nn.Module):
         # the sparse pass, then the adaptive policy replaces the uniform stride
         # for every other mode ("recompute" included)
         if getattr(cfg, "stride_policy", "fixed") == "adaptive" and mode != "sparse-only":
-            sparse, _ = self.hip_attention_interface(self, query_states, key_states, value_states,
-                                                     attention_mask, scaling=scaling,
-                                                     sliding_window=window)
+            # the key-sparse pass runs inside, in row chunks beside the chunk loop
             cut_n = s % lambd + max(128, lambd)
             s_p = s - cut_n
-            return self.delta_adaptive_forward(query_states, key_states, value_states, sparse,
+            return self.delta_adaptive_forward(query_states, key_states, value_states, None,
                                                s, s_p, cut_n, scaling), None
 
         original_dtype = query_states.dtype
@@ -280,7 +278,11 @@ class LlamaAttention(nn.Module):
         delta cosines rnd(dense - sparse[idx]), logs their mean / min, picks the
         next stride (stride.py:55-86) and writes the next chunk's row list, all
         on the device. One read of the per-chunk log after the loop gives the
-        anchor list. The result equals the reference's
+        anchor list. With sparse_attn_output None the key-sparse pass runs here,
+        one launch per chunk on a second stream, and each chunk's decision waits
+        only for its own rows of it, so the latency-bound chunk loop runs beside
+        the bandwidth- and MFMA-heavy sparse launches (rows >= s_p, which the
+        dense tail replaces, are not computed). The result equals the reference's
         cat(apply_delta_variable(...), tail_dense), assembled in place in the
         sparse pass's output: the anchor deltas rnd(dense - sparse[:, idx]) are
         formed first (the rounding of stride.py:38), the broadcast then adds
@@ -291,14 +293,18 @@ class LlamaAttention(nn.Module):
         cfg = self.config
         device = query_states.device
         q, k, v = query_states, key_states, value_states
-        out = sparse_attn_output
         if q.dtype == torch.float32:
             q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
-        if out.dtype != q.dtype:
-            out = out.to(q.dtype)
-        out = out.contiguous()
-        scale = float(scaling)
         b, h, _, d = q.shape
+        overlap = sparse_attn_output is None
+        if overlap:
+            out = torch.empty((b, s, h, d), dtype=q.dtype, device=device)
+        else:
+            out = sparse_attn_output
+            if out.dtype != q.dtype:
+                out = out.to(q.dtype)
+            out = out.contiguous()
+        scale = float(scaling)
         gamma0 = int(cfg.delta_lambda)
         g_min, g_max = int(cfg.gamma_min), int(cfg.gamma_max)
         trigger = getattr(cfg, "stride_trigger", "absolute")
@@ -306,6 +312,17 @@ class LlamaAttention(nn.Module):
         nc = len(chunks)
         idx = torch.empty(0, dtype=torch.int64, device=device)
         chunk_log = []
+        main = torch.cuda.current_stream(device)
+        ready = [None] * nc
+        if overlap and nc > 0:
+            side = self._side_stream(device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                for c, (start, end) in enumerate(chunks):
+                    ops.sparse_attention(q, k, v, window=int(cfg.sliding_window), sink=self._sink(),
+                                         sm_scale=scale, out=out, rows=(start, end - start))
+                    ready[c] = torch.cuda.Event()
+                    ready[c].record(side)
         if nc > 0:
             # anchor slots per chunk: the finest stride a chunk can get
             g_low = max(1, min(gamma0, g_min))
@@ -330,6 +347,8 @@ class LlamaAttention(nn.Module):
                                       q_rows=rows_all[c], out=dense_c, n_live=n_live,
                                       n_dev=state[1:2])
                 nxt = chunks[c + 1] if c + 1 < nc else (0, 0)
+                if ready[c] is not None:
+                    main.wait_event(ready[c])     # this chunk's rows of the key-sparse pass
                 ops.adapt_chunk_step(
                     dense_c.transpose(1, 2), out, rows_all[c], state, cos_work, chunk=c,
                     next_start=nxt[0], next_end=nxt[1],
@@ -360,6 +379,15 @@ class LlamaAttention(nn.Module):
             "n_anchors": int(idx.numel()), "chunks": chunk_log,
         }
         return out.to(query_states.dtype)
+
+    def _side_stream(self, device):
+        """A second stream (default priority) for the adaptive path's row-chunked
+        key-sparse pass, one per device."""
+        streams = self.__dict__.setdefault("_adapt_streams", {})
+        st = streams.get(device)
+        if st is None:
+            st = streams[device] = torch.cuda.Stream(device=device)
+        return st
 
     # -- decode (llama.py:498-657) ---------------------------------------------------
     def sdpa_rectangle_forward(self, module, query_states, key_states, value_states,

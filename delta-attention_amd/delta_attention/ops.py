@@ -55,13 +55,16 @@ def _on_gpu(*ts: torch.Tensor) -> torch.device:
 
 def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int,
                      sink: int, sm_scale: float, q_block: int = Q_BLOCK,
-                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     out: Optional[torch.Tensor] = None,
+                     rows: Optional[Tuple[int, int]] = None) -> torch.Tensor:
     """Causal sink + block-anchored sliding-window attention.
 
     q [B,H,S,D], k/v [B,Hkv,S,D] (any strides, GQA native) -> out [B,S,H,D].
     A key k is visible to row r iff k <= r and (k < sink or
     k + window > floor(r/q_block)*q_block + q_block - 1)
     (delta_attention/train/flex_delta.py:59-61).
+    rows = (row0, n): only rows row0 .. row0 + n - 1 are computed (the other
+    rows of `out` are left as they are; da_sparse_attn_fwd_rows).
     """
     assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4
     B, H, S, D = q.shape
@@ -75,14 +78,20 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, windo
         out = torch.empty((B, S, H, D), device=dev, dtype=q.dtype)
     assert out.shape == (B, S, H, D) and out.dtype == q.dtype
     assert out.stride(-1) == 1 and out.data_ptr() % 16 == 0
+    strides = (L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+               L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+               L.strides3(v.stride(0), v.stride(1), v.stride(2)),
+               L.strides3(out.stride(0), out.stride(2), out.stride(1)))
     with torch.cuda.device(dev):
-        rc = L.lib().da_sparse_attn_fwd(
-            _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, S, D,
-            L.strides3(q.stride(0), q.stride(1), q.stride(2)),
-            L.strides3(k.stride(0), k.stride(1), k.stride(2)),
-            L.strides3(v.stride(0), v.stride(1), v.stride(2)),
-            L.strides3(out.stride(0), out.stride(2), out.stride(1)),
-            int(window), int(sink), int(q_block), float(sm_scale), _code(q), _stream(dev))
+        if rows is not None:
+            rc = L.lib().da_sparse_attn_fwd_rows(
+                _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, S, D, *strides,
+                int(window), int(sink), int(q_block), float(sm_scale), int(rows[0]), int(rows[1]),
+                _code(q), _stream(dev))
+        else:
+            rc = L.lib().da_sparse_attn_fwd(
+                _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, S, D, *strides,
+                int(window), int(sink), int(q_block), float(sm_scale), _code(q), _stream(dev))
     L.check(rc, "da_sparse_attn_fwd")
     return out
 

@@ -75,6 +75,19 @@ int da_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out,
                        int window, int sink, int q_block, float sm_scale,
                        int dtype, void* stream);
 
+/* da_sparse_attn_fwd for query rows row0 .. row0 + n_rows - 1 only (the
+ * visibility of each row as in the full launch; out rows outside the range
+ * untouched), so that a row range can run beside other work: the adaptive
+ * stride's chunk decisions need only their chunk's rows of the key-sparse
+ * output (llama.py:784-788). No counterpart in the reference, which runs the
+ * key-sparse pass over all rows first. row0 + n_rows must not exceed S. */
+int da_sparse_attn_fwd_rows(const void* q, const void* k, const void* v, void* out,
+                            int B, int Hq, int Hkv, int S, int D,
+                            const int64_t q_str[3], const int64_t k_str[3],
+                            const int64_t v_str[3], const int64_t o_str[3],
+                            int window, int sink, int q_block, float sm_scale,
+                            int row0, int n_rows, int dtype, void* stream);
+
 /*
  * Kernel (1) with kernel (3) fused into its epilogue: the uniform-stride
  * broadcast of delta_attention/llama.py:733-755 applied while the key-sparse

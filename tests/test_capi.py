@@ -67,6 +67,24 @@ def test_sparse_rejects_bad_arguments(lib):
     assert _sparse(lib, S=0) == L.DA_OK          # nothing to do, nothing launched
 
 
+def test_sparse_rows_rejects_bad_ranges(lib):
+    def call(row0, n, **kw):
+        a = dict(q=16, D=128, dtype=L.DA_BF16)
+        a.update(kw)
+        return lib.da_sparse_attn_fwd_rows(
+            ctypes.c_void_p(a["q"]), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+            1, 8, 2, 128, a["D"], _s3(8 * 128 * 128, 128 * 128, 128), _s3(2 * 128 * 128, 128 * 128, 128),
+            _s3(2 * 128 * 128, 128 * 128, 128), _s3(128 * 8 * 128, 128, 8 * 128),
+            64, 4, 64, 0.1, row0, n, a["dtype"], None)
+    assert call(-1, 10) == L.DA_ERR_INVALID_ARG
+    assert call(0, -1) == L.DA_ERR_INVALID_ARG
+    assert call(100, 29) == L.DA_ERR_INVALID_ARG      # past S = 128
+    assert call(64, 0) == L.DA_OK                     # nothing to do, nothing launched
+    assert call(0, 10, dtype=9) == L.DA_ERR_DTYPE
+    assert call(0, 10, D=96) == L.DA_ERR_HEAD_DIM
+    assert call(0, 10, q=0) == L.DA_ERR_INVALID_ARG
+
+
 def test_qsparse_workspace_and_checks(lib):
     ws = lib.da_qsparse_workspace_bytes
     assert ws(1, 32, 8, 2174, 131072, 128) > 0

@@ -49,6 +49,29 @@ def test_sparse_attention_fp16_and_q_block(gpu):
     _sparse_case(1, 4, 1, 256, 64, 64, 8, qb=1)
 
 
+@pytest.mark.parametrize("H,Hkv,D,window,sink,cuts", [
+    (8, 2, 128, 256, 16, (0, 300, 301, 1024, 1500)),   # GQA 4: two heads per 64-row tile
+    (5, 1, 64, 100, 0, (0, 64, 500, 1500)),            # GQA 5: one head per 128-row tile
+])
+def test_sparse_attention_row_ranges(gpu, H, Hkv, D, window, sink, cuts):
+    """Row ranges of the key-sparse pass (da_sparse_attn_fwd_rows), launched
+    one after another into one output, give the full launch's bits; rows
+    outside a launched range are left untouched."""
+    from delta_attention import ops
+    q, k, v = gen_qkv(1, H, Hkv, 1500, D, seed=31)
+    scale = D ** -0.5
+    full = ops.sparse_attention(q, k, v, window=window, sink=sink, sm_scale=scale)
+    out = torch.full_like(full, 7.0)
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        ops.sparse_attention(q, k, v, window=window, sink=sink, sm_scale=scale, out=out, rows=(a, b - a))
+    torch.cuda.synchronize()
+    assert torch.equal(out, full)
+    part = torch.full_like(full, 7.0)
+    ops.sparse_attention(q, k, v, window=window, sink=sink, sm_scale=scale, out=part, rows=(301, 700))
+    assert torch.equal(part[:, 301:1001], full[:, 301:1001])
+    assert bool((part[:, :301] == 7.0).all()) and bool((part[:, 1001:] == 7.0).all())
+
+
 def test_sparse_attention_model_layout(gpu):
     # q/k/v as transposed views of [B,S,H,D] storage (no copies on the way in)
     _sparse_case(1, 8, 2, 1024, 128, 256, 64, model_layout=True, seed=3)
