@@ -119,8 +119,8 @@ struct AttnArgs {
   // cache grows (decode rows under graph replay)
   const int* n_kv_dev;
   // query-sparse mode: when set, only the first *n_rows_dev rows (clamped to
-  // [0, n_rows]) are computed; the items of their row tiles come first in the
-  // grid (plain block order) and the rest exit at once
+  // [0, n_rows]) are computed; the items of their row tiles are spread over
+  // the XCDs in contiguous ranges and the other blocks exit at once
   const int* n_rows_dev;
   uint32_t* part_o; // [item][ws_rows][D / 2]: bf16 pairs of each row's O / l
   float* part_ml;   // [item][2][ws_rows]  (running max, row sum)
@@ -237,11 +237,16 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   int w;
   int mt, split = 0, bh, hs = 0;
   if (live) {
-    // items of the live row tiles only: (bh, split, mt < mt_live), in block order
+    // items of the live row tiles only: (bh, split, mt < mt_live), each XCD
+    // a contiguous range of them (the row tiles of one split share its
+    // key/value chunk in that XCD's L2); blocks past the range exit
     const int n_live = min(max(*a.n_rows_dev, 0), a.n_rows);
     const int mt_live = (int)(((int64_t)n_live * a.G + BM - 1) / BM);
-    w = blockIdx.x;
-    if (mt_live == 0 || w >= a.B * a.Hkv * a.n_splits * mt_live) return;
+    const int total = a.B * a.Hkv * a.n_splits * mt_live;
+    const int per = (total + 7) >> 3;
+    if (mt_live == 0 || (int)(blockIdx.x >> 3) >= per) return;
+    w = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (w >= total) return;
     const int t = w / mt_live;
     mt = w - t * mt_live;
     bh = (int)fdiv(t, a.fd_sp);

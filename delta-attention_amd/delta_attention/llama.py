@@ -313,42 +313,47 @@ class LlamaAttention(nn.Module):
         idx = torch.empty(0, dtype=torch.int64, device=device)
         chunk_log = []
         main = torch.cuda.current_stream(device)
-        ready = [None] * nc
-        if overlap and nc > 0:
-            side = self._side_stream(device)
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                for c, (start, end) in enumerate(chunks):
-                    ops.sparse_attention(q, k, v, window=int(cfg.sliding_window), sink=self._sink(),
-                                         sm_scale=scale, out=out, rows=(start, end - start))
-                    ready[c] = torch.cuda.Event()
-                    ready[c].record(side)
         if nc > 0:
             # anchor slots per chunk: the finest stride a chunk can get
             g_low = max(1, min(gamma0, g_min))
             max_n = max(-(-(end - start) // g_low) for start, end in chunks)
             # split plans sized for a chunk at the starting stride
             n_live = min(max_n, max(1, -(-int(cfg.adapt_chunk) // max(gamma0, 1))))
-            rows_all = torch.full((nc, max_n), -1, dtype=torch.int64)
-            first = torch.arange(chunks[0][0], chunks[0][1], gamma0, dtype=torch.int64)
+            # chunk state built on the device (no host-to-device copy to wait
+            # behind the second stream's launches)
+            first = torch.arange(chunks[0][0], chunks[0][1], gamma0, dtype=torch.int64, device=device)
+            rows_all = torch.full((nc, max_n), -1, dtype=torch.int64, device=device)
             rows_all[0, :first.numel()] = first
-            rows_all = rows_all.to(device)
-            state = torch.tensor([gamma0, first.numel()], dtype=torch.int32).to(device)
+            state = torch.full((2,), gamma0, dtype=torch.int32, device=device)
+            state[1] = first.numel()
             dense_all = torch.empty((b, h, nc * max_n, d), dtype=q.dtype, device=device)
             cos_work = torch.empty(b * max(max_n - 1, 1) * h, dtype=torch.float32, device=device)
             log_mean = torch.empty(nc, dtype=torch.float64, device=device)
             log_min = torch.empty(nc, dtype=torch.float32, device=device)
             log_gamma = torch.empty(nc, dtype=torch.int32, device=device)
             log_n = torch.empty(nc, dtype=torch.int32, device=device)
+            side = None
+            if overlap:
+                side = self._side_stream(device)
+                side.wait_stream(main)
             for c, (start, end) in enumerate(chunks):
+                ready = None
+                if side is not None:
+                    # this chunk's rows of the key-sparse pass, on the second stream
+                    with torch.cuda.stream(side):
+                        ops.sparse_attention(q, k, v, window=int(cfg.sliding_window),
+                                             sink=self._sink(), sm_scale=scale, out=out,
+                                             rows=(start, end - start))
+                        ready = torch.cuda.Event()
+                        ready.record(side)
                 dense_c = dense_all[:, :, c * max_n:(c + 1) * max_n]
                 # the chunk's rows see keys < end: the split plan sizes its items for that
                 ops.qsparse_attention(q, k[:, :, :end], v[:, :, :end], rows_all[c], scale,
                                       q_rows=rows_all[c], out=dense_c, n_live=n_live,
                                       n_dev=state[1:2])
                 nxt = chunks[c + 1] if c + 1 < nc else (0, 0)
-                if ready[c] is not None:
-                    main.wait_event(ready[c])     # this chunk's rows of the key-sparse pass
+                if ready is not None:
+                    main.wait_event(ready)
                 ops.adapt_chunk_step(
                     dense_c.transpose(1, 2), out, rows_all[c], state, cos_work, chunk=c,
                     next_start=nxt[0], next_end=nxt[1],
