@@ -271,12 +271,13 @@ def gamma_sweep(a, q, k, v, gammas):
 
 def adaptive_layer(a, q, k, v):
     """The adaptive-stride layer: LlamaAttention.delta_forward with
-    stride_policy "adaptive" (the reference's llama.py:695-711, 759-824): the
-    key-sparse pass in row chunks on a second stream, and per adapt_chunk
-    rows a dense pass over the chunk's anchors at the current stride and the
-    inter-anchor delta cosine with the next stride decided on the device
-    (no host sync inside the loop; one read of the chunk log after it), the
-    variable-stride broadcast and the dense tail. Wall clock per layer, with
+    stride_policy "adaptive" (the reference's llama.py:695-711, 759-824), one
+    library call that enqueues the key-sparse pass in row chunks on a second
+    stream and, per adapt_chunk rows, a dense pass over the chunk's anchors at
+    the current stride, the inter-anchor delta cosines with the next stride
+    decided on the device and the chunk's broadcast-add, then the dense tail.
+    Nothing is read back inside the layer (the per-chunk log is read after
+    the timed steps, for the stride statistics). Wall clock per layer, with
     the fixed-stride layer at the starting and at the smallest stride beside
     it."""
     import types
@@ -315,7 +316,7 @@ def adaptive_layer(a, q, k, v):
     gammas = [c["gamma"] for c in st["chunks"]]
     n = len(gammas)
     print(json.dumps({
-        "metric": "adaptive-stride layer prefill (wall clock, its one host read-back included)",
+        "metric": "adaptive-stride layer prefill (wall clock)",
         "value": round(ms, 4), "unit": "ms", "higher_is_better": False,
         "steps": a.steps, "warmup": a.warmup, "chunks": n, "adapt_chunk": a.adapt_chunk,
         "adapt_threshold": a.adapt_threshold, "n_anchors": st["n_anchors"],

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "delta_attention", "libdelta_attn.so")
 SOURCES = ["attn_kernels.hip", "attn_bwd.hip", "delta_add.hip", "rope.hip", "norm.hip",
-           "anchor_cos.hip"]
+           "anchor_cos.hip", "adapt_loop.hip"]
 ARCH = "gfx950"
 
 # Packed fp32 VALU ops are disabled: they are not used by hand and must not be

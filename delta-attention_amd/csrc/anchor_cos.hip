@@ -21,30 +21,23 @@
 // latency-bound; it replaces a subtract, a cosine and reductions of torch ops.
 #include "device_common.h"
 #include "capi_common.h"
+#include "adapt_args.h"
 
 namespace da {
 
-struct CosArgs {
-  const void* a;           // dense anchor rows or deltas [B, n, H, D]
-  int64_t a_b, a_n, a_h;
-  const void* s;           // key-sparse output [B, rows, H, D] or nullptr
-  int64_t s_b, s_r, s_h;
-  const int64_t* rows;     // anchor row of each delta in `s` (nullptr: row i)
-  int64_t n_rows;          // rows of `s` (indices are clamped into it)
-  float* cos;              // [B, n - 1, H]
-  int* hist;               // [bins] or nullptr
-  int bins;
-  float lo, hi;
-  int B, n, H, D;
-  const int* n_dev;        // set: the delta count is min(*n_dev, n), read on the device
-};
 
 template <typename T>
 __device__ __forceinline__ void delta_pair(const CosArgs& a, int b, int i, int h, int e,
                                            float& x0, float& x1) {
   using E = Elt<T>;
   constexpr size_t esz = sizeof(T);
-  const char* ap = (const char*)a.a + ((int64_t)b * a.a_b + (int64_t)i * a.a_n + (int64_t)h * a.a_h + e) * esz;
+  const char* ap;
+  if (a.sel && a.sel[0] < 0) {
+    ap = (const char*)a.a_alt + ((int64_t)b * a.alt_b + (int64_t)i * a.alt_n + (int64_t)h * a.alt_h + e) * esz;
+  } else {
+    const int64_t slot = a.sel ? a.sel[0] + (int64_t)i * a.sel[1] : i;
+    ap = (const char*)a.a + ((int64_t)b * a.a_b + slot * a.a_n + (int64_t)h * a.a_h + e) * esz;
+  }
   const uint32_t v = *(const uint32_t*)ap;
   if (a.s) {
     int64_t r = a.rows ? a.rows[i] : i;
@@ -108,21 +101,6 @@ __global__ __launch_bounds__(256) void anchor_cos_kernel(CosArgs a) {
 // to [gamma_min, gamma_max]; then the next chunk's anchor rows start + j *
 // gamma for j < ceil((end - start) / gamma), -1 for the rest of the max_n
 // slots (rows that the query-sparse kernel treats as empty).
-struct AdaptArgs {
-  const float* cos;        // [B, n - 1, H] of this chunk
-  int B, H;
-  int* state;              // {gamma, n} of this chunk; overwritten with the next chunk's
-  int chunk;               // this chunk's index into the logs
-  int next_start, next_end, max_n;
-  int64_t* rows_next;      // [max_n] or nullptr
-  int trigger;             // 0 absolute, 1 relative
-  double threshold, margin, k;
-  int gamma_min, gamma_max;
-  double* log_mean;
-  float* log_min;
-  int* log_gamma;
-  int* log_n;
-};
 
 __global__ __launch_bounds__(256) void adapt_next_kernel(AdaptArgs a) {
   __shared__ double s_sum[256];
@@ -150,6 +128,10 @@ __global__ __launch_bounds__(256) void adapt_next_kernel(AdaptArgs a) {
     __syncthreads();
   }
   if (tid == 0) {
+    if (a.sel_log) {
+      a.sel_log[2 * a.chunk] = a.state[3];
+      a.sel_log[2 * a.chunk + 1] = a.state[4];
+    }
     const double mean = pairs > 0 ? s_sum[0] / (double)pairs : 1.0;
     const float cmin = pairs > 0 ? s_min[0] : 1.0f;
     a.log_mean[a.chunk] = mean;
@@ -178,6 +160,12 @@ __global__ __launch_bounds__(256) void adapt_next_kernel(AdaptArgs a) {
     s_next[1] = min(nn, a.max_n);
     a.state[0] = g;
     a.state[1] = min(nn, a.max_n);
+    if (a.spec_gamma > 0) {
+      const bool ahead = g % a.spec_gamma == 0 && a.next_start % a.spec_gamma == 0;
+      a.state[2] = ahead ? 0 : min(nn, a.max_n);
+      a.state[3] = ahead ? a.next_start / a.spec_gamma : -1;
+      a.state[4] = ahead ? g / a.spec_gamma : 1;
+    }
   }
   __syncthreads();
   if (a.rows_next) {
@@ -185,6 +173,19 @@ __global__ __launch_bounds__(256) void adapt_next_kernel(AdaptArgs a) {
     for (int j = tid; j < a.max_n; j += 256)
       a.rows_next[j] = j < nn ? (int64_t)a.next_start + (int64_t)j * g : (int64_t)-1;
   }
+}
+
+// The two launches of one chunk step (the library's own chunk loop).
+int adapt_step_launch(const CosArgs& c, const AdaptArgs& a, int dtype, hipStream_t st) {
+  const int64_t grid = ((int64_t)c.B * (c.n > 1 ? c.n - 1 : 1) * c.H + 3) / 4;
+  if (grid > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
+  (void)hipGetLastError();
+  if (dtype == DA_BF16)
+    hipLaunchKernelGGL((anchor_cos_kernel<__bf16>), dim3((unsigned)grid), dim3(256), 0, st, c);
+  else
+    hipLaunchKernelGGL((anchor_cos_kernel<_Float16>), dim3((unsigned)grid), dim3(256), 0, st, c);
+  hipLaunchKernelGGL(adapt_next_kernel, dim3(1), dim3(256), 0, st, a);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }
 
 }  // namespace da

@@ -24,6 +24,13 @@ struct DeltaArgs {
   int64_t ds_b, ds_h, ds_a;
   const int64_t* anchors;
   int n_anchor, gamma, s_p, H, D;
+  const int* n_dev;        // set: one chunk's anchor list, min(*n_dev, n_anchor) anchors
+  int row_end;             // with n_dev: the chunk's end row
+  // set: {slot0, step} on the device. slot0 >= 0: anchor g's dense row is
+  // slot slot0 + g * step of `dense`; slot0 < 0: row g of dense_alt
+  const int* sel;
+  const void* dense_alt;
+  int64_t alt_b, alt_h, alt_a;
 };
 
 constexpr int DA_ROWS_UNROLL = 16;
@@ -35,7 +42,16 @@ __global__ __launch_bounds__(256) void delta_add_kernel(DeltaArgs a) {
   using E = Elt<T>;
   const int b = blockIdx.y;
   int r0, r1, aidx;
-  if (a.anchors) {
+  if (a.n_dev) {
+    // one chunk of the adaptive stride: group g covers rows anchors[g] ..
+    // anchors[g + 1] - 1, the last one up to the chunk's end; the anchor
+    // count is read on the device
+    const int n = min(*a.n_dev, a.n_anchor);
+    aidx = blockIdx.x;
+    if (aidx >= n) return;
+    r0 = (int)a.anchors[aidx];
+    r1 = aidx + 1 < n ? (int)a.anchors[aidx + 1] : a.row_end;
+  } else if (a.anchors) {
     // block 0 covers rows before anchors[0]; they take the last anchor's
     // delta (searchsorted(..., right=True) - 1 == -1 picks the last entry).
     const int g = (int)blockIdx.x - 1;
@@ -70,8 +86,14 @@ __global__ __launch_bounds__(256) void delta_add_kernel(DeltaArgs a) {
     if constexpr (FROM_DENSE) {
       // anchors outside [0, s_p) are clamped so the read stays inside the rows
       const int arow = (int)min(max(a.anchors[aidx], (int64_t)0), (int64_t)(a.s_p - 1));
-      const u32x4 dn = *(const u32x4*)((const char*)a.dense +
-          ((int64_t)b * a.ds_b + (int64_t)h * a.ds_h + (int64_t)aidx * a.ds_a + off8) * esz);
+      const char* dp;
+      if (a.sel && a.sel[0] < 0) {
+        dp = (const char*)a.dense_alt + ((int64_t)b * a.alt_b + (int64_t)h * a.alt_h + (int64_t)aidx * a.alt_a) * esz;
+      } else {
+        const int64_t slot = a.sel ? a.sel[0] + (int64_t)aidx * a.sel[1] : aidx;
+        dp = (const char*)a.dense + ((int64_t)b * a.ds_b + (int64_t)h * a.ds_h + slot * a.ds_a) * esz;
+      }
+      const u32x4 dn = *(const u32x4*)(dp + off8 * esz);
       const u32x4 sa = *(const u32x4*)(sp_base + ((int64_t)h * a.sp_h + (int64_t)arow * a.sp_s + off8) * esz);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -122,6 +144,38 @@ static void launch_delta(const DeltaArgs& a, dim3 grid, bool from_dense, hipStre
     hipLaunchKernelGGL((delta_add_kernel<T, true>), grid, dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL((delta_add_kernel<T, false>), grid, dim3(256), 0, s, a);
+}
+
+// One chunk of the adaptive stride in place (the library's own chunk loop):
+// rows anchors[g] .. of `out` [B, S, H, D] (strides batch, head, row) become
+// rnd(out[r] + rnd(dense[g] - out[anchors[g]])) for g < min(*n_dev, max_n),
+// rows below min(row_end, s_p). Each workgroup reads its group's anchor row
+// before it writes the group, and no group reads another's rows, so the
+// update is safe in place. dense / alt: [B, H, rows, D] (strides batch, head,
+// anchor), chosen per anchor through sel as DeltaArgs describes (sel null:
+// row g of dense).
+int delta_add_chunk(void* out, const int64_t o_str[3], const void* dense,
+                    const int64_t ds_str[3], const int* sel, const void* alt,
+                    const int64_t alt_str[3], const int64_t* anchors, const int* n_dev,
+                    int max_n, int row_end, int s_p, int B, int H, int D, int dtype,
+                    hipStream_t s) {
+  if (max_n < 1 || row_end < 0 || row_end > s_p || B < 1 || B > 65535) return DA_ERR_INVALID_ARG;
+  if (!out || !o_str || !dense || !ds_str || !anchors || !n_dev) return DA_ERR_INVALID_ARG;
+  if (!aligned16(out) || !aligned16(dense) || !strides8(o_str) || !strides8(ds_str))
+    return DA_ERR_ALIGNMENT;
+  if (sel && (!alt || !alt_str || !aligned16(alt) || !strides8(alt_str))) return DA_ERR_INVALID_ARG;
+  DeltaArgs a = {};
+  a.sparse = out; a.sp_b = o_str[0]; a.sp_h = o_str[1]; a.sp_s = o_str[2];
+  a.out = out; a.o_b = o_str[0]; a.o_h = o_str[1]; a.o_s = o_str[2];
+  a.dense = dense; a.ds_b = ds_str[0]; a.ds_h = ds_str[1]; a.ds_a = ds_str[2];
+  a.anchors = anchors; a.n_anchor = max_n; a.s_p = s_p; a.H = H; a.D = D;
+  a.n_dev = n_dev; a.row_end = row_end;
+  a.sel = sel;
+  if (sel) { a.dense_alt = alt; a.alt_b = alt_str[0]; a.alt_h = alt_str[1]; a.alt_a = alt_str[2]; }
+  (void)hipGetLastError();
+  if (dtype == DA_BF16) launch_delta<__bf16>(a, dim3(max_n, B), true, s);
+  else launch_delta<_Float16>(a, dim3(max_n, B), true, s);
+  return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }
 
 }  // namespace da

@@ -59,6 +59,8 @@ EXPORTS = (
     "da_qsparse_workspace_bytes_live",
     "da_qsparse_attn_fwd_live",
     "da_sparse_attn_fwd_rows",
+    "da_adapt_layer_workspace_bytes",
+    "da_adapt_layer_fwd",
 )
 
 _ERR_TEXT = {
@@ -197,6 +199,14 @@ def _load() -> ctypes.CDLL:
                                       _vp, _vp, _i, _i, _i, _vp,
                                       _i, ctypes.c_double, ctypes.c_double, ctypes.c_double, _i, _i,
                                       _vp, _vp, _vp, _vp, _i, _vp]
+    _d = ctypes.c_double
+    L.da_adapt_layer_workspace_bytes.restype = _sz
+    L.da_adapt_layer_workspace_bytes.argtypes = [_i, _i, _i, _i, _i, _i, _i, _i, _i]
+    L.da_adapt_layer_fwd.restype = _i
+    L.da_adapt_layer_fwd.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                     _p3, _p3, _p3, _p3, _i, _i, _i, _f,
+                                     _i, _i, _i, _i, _i, _i, _d, _d, _d,
+                                     _vp, _vp, _vp, _vp, _i, _vp, _sz, _i, _vp, _vp]
     L.da_build_target.restype = ctypes.c_char_p
     L.da_build_target.argtypes = []
     return L

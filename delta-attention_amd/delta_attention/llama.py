@@ -16,6 +16,7 @@ pipeline knobs of `config.PIPELINE_FIELDS`.
 
 from __future__ import annotations
 
+import functools
 from typing import Optional, Tuple
 
 import torch
@@ -152,6 +153,29 @@ def repeat_kv(hidden_states: torch.Tensor, n_rep: int) -> torch.Tensor:
     return hidden_states[:, :, None].expand(b, hkv, n_rep, s, d).reshape(b, hkv * n_rep, s, d)
 
 
+def _adaptive_stride_stats(logs, layer, s, s_p, adapt_chunk, window, sink):
+    """The stride statistics of one adaptive pass (llama.py:806-824) from its
+    per-chunk device logs: per chunk its first row, stride, mean / min delta
+    cosine and anchor count, the anchor total and the effective sparsity of
+    the anchors plus the dense tail."""
+    from .stride import effective_sparsity, plan_chunks
+
+    log_mean, log_min, log_gamma, log_n = (t.tolist() for t in logs)
+    chunk_log, idx_parts = [], []
+    for c, (start, end) in enumerate(plan_chunks(s_p, adapt_chunk)):
+        idx_parts.append(torch.arange(start, end, log_gamma[c], dtype=torch.int64)[:log_n[c]])
+        chunk_log.append({"start": int(start), "gamma": int(log_gamma[c]),
+                          "cos_mean": float(log_mean[c]), "cos_min": float(log_min[c]),
+                          "n_anchors": int(log_n[c])})
+    idx = torch.cat(idx_parts) if idx_parts else torch.empty(0, dtype=torch.int64)
+    tail_idx = torch.arange(s_p, s, dtype=torch.int64)
+    return {
+        "kind": "stride", "layer": layer, "seq_len": s,
+        "effective_sparsity": effective_sparsity(torch.cat((idx, tail_idx)), s, window, sink),
+        "n_anchors": int(idx.numel()), "chunks": chunk_log,
+    }
+
+
 class LlamaAttention(nn.Module):
 
     def __init__(self, config, layer_idx: int):
@@ -272,23 +296,23 @@ class LlamaAttention(nn.Module):
         chunk's mean consecutive-delta cosine, variable-stride broadcast
         (kernel 3 with an anchor list), dense cut_n tail.
 
-        The chunk loop runs without reading anything back: each chunk's dense
-        anchor rows (kernel (2) over a row list of max_n slots, -1 past the
-        chunk's anchors), then da_adapt_chunk_step, which takes the chunk's
-        delta cosines rnd(dense - sparse[idx]), logs their mean / min, picks the
-        next stride (stride.py:55-86) and writes the next chunk's row list, all
-        on the device. One read of the per-chunk log after the loop gives the
-        anchor list. With sparse_attn_output None the key-sparse pass runs here,
-        one launch per chunk on a second stream, and each chunk's decision waits
-        only for its own rows of it, so the latency-bound chunk loop runs beside
-        the bandwidth- and MFMA-heavy sparse launches (rows >= s_p, which the
-        dense tail replaces, are not computed). The result equals the reference's
-        cat(apply_delta_variable(...), tail_dense), assembled in place in the
-        sparse pass's output: the anchor deltas rnd(dense - sparse[:, idx]) are
-        formed first (the rounding of stride.py:38), the broadcast then adds
-        them row by row, and the tail rows are written by the query-sparse
-        kernel's scatter epilogue."""
-        from .stride import ADAPT_MARGIN, effective_sparsity, plan_chunks
+        The whole layer is one library call (da_adapt_layer_fwd), which
+        enqueues the chunk loop without reading anything back: each chunk's
+        dense anchor rows (kernel (2) over a row list of max_n slots, -1 past
+        the chunk's anchors), its delta cosines rnd(dense - sparse[idx]) with
+        their mean / min logged and the next stride (stride.py:55-86) and row
+        list decided on the device, then the chunk's broadcast-add in place.
+        With sparse_attn_output None the key-sparse pass runs in the same call,
+        one launch per chunk on a second stream, and each chunk's decision
+        waits only for its own rows of it, so the latency-bound chunk loop runs
+        beside the MFMA-heavy sparse launches (rows >= s_p, which the dense tail
+        replaces, are not computed). The result equals the reference's
+        cat(apply_delta_variable(...), tail_dense): every stride group lies
+        inside one chunk, its delta is rnd(dense - sparse[anchor]) (the
+        rounding of stride.py:38) and its rows get rnd(sparse + delta); the tail
+        rows come from the query-sparse kernel's scatter epilogue. The stride
+        statistics are read from the per-chunk logs when first asked for."""
+        from .stride import ADAPT_MARGIN
 
         cfg = self.config
         device = query_states.device
@@ -304,86 +328,32 @@ class LlamaAttention(nn.Module):
             if out.dtype != q.dtype:
                 out = out.to(q.dtype)
             out = out.contiguous()
-        scale = float(scaling)
-        gamma0 = int(cfg.delta_lambda)
-        g_min, g_max = int(cfg.gamma_min), int(cfg.gamma_max)
-        trigger = getattr(cfg, "stride_trigger", "absolute")
-        chunks = plan_chunks(s_p, int(cfg.adapt_chunk))
-        nc = len(chunks)
-        idx = torch.empty(0, dtype=torch.int64, device=device)
-        chunk_log = []
-        main = torch.cuda.current_stream(device)
-        if nc > 0:
-            # anchor slots per chunk: the finest stride a chunk can get
-            g_low = max(1, min(gamma0, g_min))
-            max_n = max(-(-(end - start) // g_low) for start, end in chunks)
-            # split plans sized for a chunk at the starting stride
-            n_live = min(max_n, max(1, -(-int(cfg.adapt_chunk) // max(gamma0, 1))))
-            # chunk state built on the device (no host-to-device copy to wait
-            # behind the second stream's launches)
-            first = torch.arange(chunks[0][0], chunks[0][1], gamma0, dtype=torch.int64, device=device)
-            rows_all = torch.full((nc, max_n), -1, dtype=torch.int64, device=device)
-            rows_all[0, :first.numel()] = first
-            state = torch.full((2,), gamma0, dtype=torch.int32, device=device)
-            state[1] = first.numel()
-            dense_all = torch.empty((b, h, nc * max_n, d), dtype=q.dtype, device=device)
-            cos_work = torch.empty(b * max(max_n - 1, 1) * h, dtype=torch.float32, device=device)
-            log_mean = torch.empty(nc, dtype=torch.float64, device=device)
-            log_min = torch.empty(nc, dtype=torch.float32, device=device)
-            log_gamma = torch.empty(nc, dtype=torch.int32, device=device)
-            log_n = torch.empty(nc, dtype=torch.int32, device=device)
-            side = None
-            if overlap:
-                side = self._side_stream(device)
-                side.wait_stream(main)
-            for c, (start, end) in enumerate(chunks):
-                ready = None
-                if side is not None:
-                    # this chunk's rows of the key-sparse pass, on the second stream
-                    with torch.cuda.stream(side):
-                        ops.sparse_attention(q, k, v, window=int(cfg.sliding_window),
-                                             sink=self._sink(), sm_scale=scale, out=out,
-                                             rows=(start, end - start))
-                        ready = torch.cuda.Event()
-                        ready.record(side)
-                dense_c = dense_all[:, :, c * max_n:(c + 1) * max_n]
-                # the chunk's rows see keys < end: the split plan sizes its items for that
-                ops.qsparse_attention(q, k[:, :, :end], v[:, :, :end], rows_all[c], scale,
-                                      q_rows=rows_all[c], out=dense_c, n_live=n_live,
-                                      n_dev=state[1:2])
-                nxt = chunks[c + 1] if c + 1 < nc else (0, 0)
-                if ready is not None:
-                    main.wait_event(ready)
-                ops.adapt_chunk_step(
-                    dense_c.transpose(1, 2), out, rows_all[c], state, cos_work, chunk=c,
-                    next_start=nxt[0], next_end=nxt[1],
-                    rows_next=rows_all[c + 1] if c + 1 < nc else None, trigger=trigger,
-                    threshold=float(cfg.adapt_threshold), margin=ADAPT_MARGIN,
-                    k=float(getattr(cfg, "adapt_k", 2.0)), gamma_min=g_min, gamma_max=g_max,
-                    log_mean=log_mean, log_min=log_min, log_gamma=log_gamma, log_n=log_n)
-            # the one read-back of the layer: per-chunk stride, anchors and cosines
-            lg, ln = log_gamma.tolist(), log_n.tolist()
-            lm, lmin = log_mean.tolist(), log_min.tolist()
-            idx_parts, slots = [], []
-            for c, (start, end) in enumerate(chunks):
-                n_c = int(ln[c])
-                idx_parts.append(torch.arange(start, end, lg[c], dtype=torch.int64))
-                slots.append(torch.arange(c * max_n, c * max_n + n_c, dtype=torch.int64))
-                chunk_log.append({"start": int(start), "gamma": int(lg[c]), "cos_mean": float(lm[c]),
-                                  "cos_min": float(lmin[c]), "n_anchors": n_c})
-            idx = torch.cat(idx_parts).to(device)
-            dense_sel = dense_all.index_select(2, torch.cat(slots).to(device)).transpose(1, 2)
-            delta = dense_sel - out[:, idx]        # bf16: one rounding
-            ops.delta_add(out, s_p=s_p, out=out, delta=delta, anchors=idx)
-        tail_idx = torch.arange(s_p, s, device=device)
-        ops.qsparse_attention(q, k, v, tail_idx, scale, q_rows=tail_idx, epi=L.DA_EPI_SCATTER, out=out)
-        self._stride_stats = {
-            "kind": "stride", "layer": int(self.layer_idx), "seq_len": int(s),
-            "effective_sparsity": effective_sparsity(torch.cat((idx, tail_idx)), s,
-                                                     int(cfg.sliding_window), self._sink()),
-            "n_anchors": int(idx.numel()), "chunks": chunk_log,
-        }
+        adapt_chunk = int(cfg.adapt_chunk)
+        logs = ops.adapt_layer(
+            q, k, v, out, s_p=s_p, window=int(cfg.sliding_window), sink=self._sink(),
+            sm_scale=float(scaling), adapt_chunk=adapt_chunk, gamma0=int(cfg.delta_lambda),
+            gamma_min=int(cfg.gamma_min), gamma_max=int(cfg.gamma_max),
+            trigger=getattr(cfg, "stride_trigger", "absolute"),
+            threshold=float(cfg.adapt_threshold), margin=ADAPT_MARGIN,
+            k_sd=float(getattr(cfg, "adapt_k", 2.0)),
+            side_stream=self._side_stream(device) if overlap else None)
+        self._stride_stats = functools.partial(
+            _adaptive_stride_stats, logs, int(self.layer_idx), int(s), int(s_p), adapt_chunk,
+            int(cfg.sliding_window), self._sink())
         return out.to(query_states.dtype)
+
+    @property
+    def _stride_stats(self):
+        """The last adaptive pass's stride statistics (a dict), built from its
+        device logs on first access (the one read-back of the pass)."""
+        rec = self.__dict__.get("_stride_record")
+        if callable(rec):
+            rec = self.__dict__["_stride_record"] = rec()
+        return rec
+
+    @_stride_stats.setter
+    def _stride_stats(self, value):
+        self.__dict__["_stride_record"] = value
 
     def _side_stream(self, device):
         """A second stream (default priority) for the adaptive path's row-chunked

@@ -686,6 +686,55 @@ def adapt_chunk_step(dense: torch.Tensor, sparse: torch.Tensor, rows: torch.Tens
     L.check(rc, "da_adapt_chunk_step")
 
 
+def adapt_layer(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor, *,
+                s_p: int, window: int, sink: int, sm_scale: float, adapt_chunk: int,
+                gamma0: int, gamma_min: int, gamma_max: int, trigger: str, threshold: float,
+                margin: float, k_sd: float = 2.0, side_stream: Optional[torch.cuda.Stream] = None,
+                q_block: int = Q_BLOCK):
+    """The adaptive-stride layer in one library call (da_adapt_layer_fwd):
+    per adapt_chunk rows of [0, s_p), kernel (2) over the chunk's anchors at
+    its stride, the chunk's delta cosines and next stride on the device, and
+    the chunk's broadcast-add in place in `out`; then the dense tail rows
+    [s_p, S). With side_stream, the key-sparse pass runs here on it, chunk by
+    chunk (out's rows [0, s_p) are written); without, out must already hold
+    it. q [B,H,S,D], k/v [B,Hkv,S,D], out [B,S,H,D].
+
+    Returns the per-chunk logs (log_mean fp64, log_min fp32, log_gamma int32,
+    log_n int32) on the device; nothing is read back here."""
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    assert k.shape == (B, Hkv, S, D) and v.shape == k.shape, (q.shape, k.shape, v.shape)
+    assert q.dtype == k.dtype == v.dtype == out.dtype and out.shape == (B, S, H, D)
+    assert out.stride(-1) == 1
+    assert trigger in ("absolute", "relative"), trigger
+    dev = _on_gpu(q, k, v, out)
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    nc = -(-s_p // adapt_chunk) if adapt_chunk > 0 else 0
+    nb = L.lib().da_adapt_layer_workspace_bytes(B, H, Hkv, S, D, int(s_p), int(adapt_chunk),
+                                                int(gamma0), int(gamma_min))
+    assert nb > 0, "adaptive layer sizes do not form a launch"
+    workspace = torch.empty(nb, dtype=torch.uint8, device=dev)
+    n_log = max(nc, 1)
+    log_mean = torch.empty(n_log, dtype=torch.float64, device=dev)
+    log_min = torch.empty(n_log, dtype=torch.float32, device=dev)
+    log_gamma = torch.empty(n_log, dtype=torch.int32, device=dev)
+    log_n = torch.empty(n_log, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.lib().da_adapt_layer_fwd(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, Hkv, S, D,
+            L.strides3(q.stride(0), q.stride(1), q.stride(2)),
+            L.strides3(k.stride(0), k.stride(1), k.stride(2)),
+            L.strides3(v.stride(0), v.stride(1), v.stride(2)),
+            L.strides3(out.stride(0), out.stride(2), out.stride(1)),
+            int(window), int(sink), int(q_block), float(sm_scale), int(s_p), int(adapt_chunk),
+            int(gamma0), int(gamma_min), int(gamma_max), 0 if trigger == "absolute" else 1,
+            float(threshold), float(margin), float(k_sd), _ptr(log_mean), _ptr(log_min),
+            _ptr(log_gamma), _ptr(log_n), n_log, _ptr(workspace), nb, _code(q), _stream(dev),
+            side_stream.cuda_stream if side_stream is not None else None)
+    L.check(rc, "da_adapt_layer_fwd")
+    return log_mean, log_min, log_gamma, log_n
+
+
 def anchor_layout(s: int, gamma: int) -> Tuple[int, int, int]:
     """(cut_n, s_p, n_anchor) of delta_forward's fixed-stride layout
     (llama.py:692-693, 711-714): cut_n = s % gamma + max(128, gamma)."""

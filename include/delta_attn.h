@@ -391,6 +391,45 @@ int da_adapt_chunk_step(const void* dense, const int64_t d_str[3],
                         double* log_mean, float* log_min, int* log_gamma, int* log_n,
                         int dtype, void* stream);
 
+/* The whole adaptive-stride layer, replacing the host loop of
+ * LlamaAttention.delta_adaptive_forward (llama.py:759-824) from the key-sparse
+ * pass to the concatenated output: the chunk loop is enqueued here, so the
+ * host neither reads back nor waits per chunk. Chunks are the adapt_chunk-row
+ * ranges [start, end) of rows [0, s_p) (stride.py:111-112); the first uses
+ * stride gamma0, each next one the stride da_adapt_chunk_step picks (trigger,
+ * threshold, margin, k_sd, gamma_min, gamma_max as there). Per chunk c:
+ *   side_stream (when not NULL): kernel (1) over rows [start, end) into out;
+ *   stream: kernel (2) over the chunk's anchor rows start + j * stride
+ *     against keys < end; the chunk's delta cosines, logs and next stride
+ *     (da_adapt_chunk_step, after the chunk's rows of kernel (1)); then rows
+ *     [start, end) of out become rnd(out[r] + rnd(dense[g] - out[anchor g]))
+ *     for r in anchor g's stride group, in place (stride.py:26-40).
+ * Then rows [s_p, S) of out are the dense tail rows (all causal keys), and
+ * `stream` waits for everything given to side_stream. With side_stream NULL,
+ * rows [0, s_p) of out must already hold the key-sparse pass and everything
+ * runs on `stream`.
+ *   q [B, Hq, S, D], k/v [B, Hkv, S, D], out [B, S, Hq, D]: strides as for
+ *           da_sparse_attn_fwd.
+ *   logs    device arrays of n_log >= ceil(s_p / adapt_chunk) entries:
+ *           log_mean (fp64) / log_min (fp32) of each chunk's delta cosines,
+ *           log_gamma / log_n (int32) its stride and anchor count; chunk c's
+ *           anchors are start + j * log_gamma[c] for j < log_n[c].
+ *   workspace  >= da_adapt_layer_workspace_bytes(...) bytes, 256-byte aligned,
+ *           any contents; the same sizes must be passed to both calls.
+ * No counterpart entry point in the reference (it runs the loop as Python). */
+size_t da_adapt_layer_workspace_bytes(int B, int Hq, int Hkv, int S, int D, int s_p,
+                                      int adapt_chunk, int gamma0, int gamma_min);
+int da_adapt_layer_fwd(const void* q, const void* k, const void* v, void* out,
+                       int B, int Hq, int Hkv, int S, int D,
+                       const int64_t q_str[3], const int64_t k_str[3],
+                       const int64_t v_str[3], const int64_t o_str[3],
+                       int window, int sink, int q_block, float sm_scale,
+                       int s_p, int adapt_chunk, int gamma0, int gamma_min, int gamma_max,
+                       int trigger, double threshold, double margin, double k_sd,
+                       double* log_mean, float* log_min, int* log_gamma, int* log_n, int n_log,
+                       void* workspace, size_t ws_bytes, int dtype, void* stream,
+                       void* side_stream);
+
 /*
  * Training path: forward with saved row statistics, and the backward.
  * Together they replace the autograd of delta_forward_train

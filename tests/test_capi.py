@@ -310,6 +310,57 @@ def test_adapt_chunk_step_checks(lib):
     assert call(d_str=_s3(64 * 8 * 128, 8 * 128, 127)) == L.DA_ERR_ALIGNMENT
 
 
+def test_adapt_layer_sizes_and_checks(lib):
+    """The adaptive layer's workspace query (the largest chunk's split plan,
+    one chunk of dense rows, the row lists) and its refusals, all of which
+    precede any launch or event (nothing runs on a GPU here)."""
+    P = ctypes.c_void_p
+    B, H, Hkv, S, D = 1, 32, 8, 131072, 128
+    s_p = S - 128
+    nb = lib.da_adapt_layer_workspace_bytes(B, H, Hkv, S, D, s_p, 4096, 64, 16)
+    # at least: 32 chunk row lists of 256 slots, two buffers of a chunk's 256
+    # dense rows, the 2046 rows at multiples of 64 computed ahead and their
+    # row list, the last chunk's split workspace, the rows-ahead launch's and
+    # the tail's
+    split = lib.da_qsparse_workspace_bytes_live(B, H, Hkv, 256, 64, s_p, D)
+    ahead = lib.da_qsparse_workspace_bytes(B, H, Hkv, 2046, s_p, D)
+    tail = lib.da_qsparse_workspace_bytes(B, H, Hkv, 128, S, D)
+    least = (32 * 256 * 8 + 2 * B * H * 256 * D * 2 + 2046 * 8 + B * H * 2046 * D * 2
+             + split + ahead + tail)
+    assert least <= nb < least + 10 * 256 + B * H * 256 * 4
+    # adapt_chunk not a multiple of the first stride: no rows ahead
+    nb2 = lib.da_adapt_layer_workspace_bytes(B, H, Hkv, S, D, s_p, 4000, 64, 16)
+    assert 0 < nb2 < nb - B * H * 2046 * D * 2 - ahead
+    # no prefix rows: no chunk, only the tail
+    assert lib.da_adapt_layer_workspace_bytes(B, H, Hkv, 128, D, 0, 4096, 64, 16) > 0
+    for args in ((B, H, Hkv, S, 80, s_p, 4096, 64, 16), (B, H, 7, S, D, s_p, 4096, 64, 16),
+                 (B, H, Hkv, S, D, S, 4096, 64, 16), (B, H, Hkv, S, D, -1, 4096, 64, 16),
+                 (B, H, Hkv, S, D, s_p, 0, 64, 16), (B, H, Hkv, S, D, s_p, 4096, 0, 16),
+                 (B, H, Hkv, S, D, s_p, 4096, 64, 0), (0, H, Hkv, S, D, s_p, 4096, 64, 16)):
+        assert lib.da_adapt_layer_workspace_bytes(*args) == 0, args
+
+    q3 = _s3(H * S * D, S * D, D)
+    k3 = _s3(Hkv * S * D, S * D, D)
+    o3 = _s3(S * H * D, D, H * D)
+
+    def call(q=16, out=16, ws=256, ws_bytes=nb, logs=16, n_log=32, D=D, dtype=L.DA_BF16,
+             trigger=0, gmin=16, gmax=256, o_str=o3, s_p=s_p):
+        return lib.da_adapt_layer_fwd(
+            P(q) if q else None, P(16), P(16), P(out) if out else None, B, H, Hkv, S, D,
+            q3, k3, k3, o_str, 2048, 128, 64, 0.088, s_p, 4096, 64, gmin, gmax, trigger,
+            0.95, 0.02, 2.0, P(logs) if logs else None, P(logs) if logs else None,
+            P(logs) if logs else None, P(logs) if logs else None, n_log,
+            P(ws) if ws else None, ws_bytes, dtype, None, None)
+    assert call(dtype=7) == L.DA_ERR_DTYPE
+    assert call(D=80) == L.DA_ERR_HEAD_DIM
+    for kw in ({"q": 0}, {"out": 0}, {"ws": 0}, {"ws_bytes": nb - 1}, {"logs": 0},
+               {"n_log": 31}, {"trigger": 2}, {"gmin": 64, "gmax": 32}, {"s_p": S}):
+        assert call(**kw) == L.DA_ERR_INVALID_ARG, kw
+    assert call(ws=512 + 16) == L.DA_ERR_ALIGNMENT
+    assert call(out=24) == L.DA_ERR_ALIGNMENT
+    assert call(o_str=_s3(S * H * D, D, H * D + 4)) == L.DA_ERR_ALIGNMENT
+
+
 def test_qsparse_live_plan_sizes(lib):
     """The live-rows plan: the grid (and the workspace's item count) covers
     all n slots, the splits per row tile follow n_live rows; n_live >= n is the

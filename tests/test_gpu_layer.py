@@ -230,6 +230,68 @@ def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold
         assert float(cos.min()) == c["cos_min"]
 
 
+@pytest.mark.parametrize("s,chunk,gamma0,gmin", [(4096, 512, 32, 8), (3000, 1024, 64, 16),
+                                                  (2500, 1000, 64, 16)])
+def test_adaptive_layer_composition_is_exact(gpu, s, chunk, gamma0, gmin):
+    """The one-call adaptive layer (da_adapt_layer_fwd) against the same
+    steps issued one by one: the key-sparse pass over all rows; each chunk's
+    dense anchor rows from the same kernel (2) launch as inside, i.e. when
+    gamma0 divides adapt_chunk and the chunk's stride is a multiple of gamma0
+    the rows-ahead launch (every multiple of gamma0 below s_p, keys < s_p),
+    else the chunk's own launch (its -1-padded row list, keys < the chunk's
+    end, the same live-row plan); the deltas rnd(dense - sparse[anchor]) and
+    rows rnd(sparse + delta) in torch bf16 ops (stride.py:26-40); and the dense
+    tail. Bit-identical: the row selection, the per-chunk in-place broadcast,
+    the row ranges of the sparse pass and the tail scatter change no bits."""
+    from delta_attention import ops
+    from delta_attention.llama import LlamaAttention
+    window, sink, H, Hkv = 256, 16, 8, 2
+    scale = 128 ** -0.5
+    q, k, v = gen_qkv(1, H, Hkv, s, 128, seed=21)
+    cfg = _cfg(H, Hkv, 128, stride_policy="adaptive", adapt_chunk=chunk, delta_lambda=gamma0,
+               adapt_threshold=0.97, gamma_min=gmin, gamma_max=128, sliding_window=window,
+               sink_tokens=sink)
+    m = LlamaAttention(cfg, layer_idx=0).cuda().to(torch.bfloat16)
+    out, _ = m.delta_forward(m, q, k, v, None, scaling=scale)
+    st = m._stride_stats
+    cut_n = s % gamma0 + max(128, gamma0)
+    s_p = s - cut_n
+    max_n = -(-min(chunk, s_p) // min(gamma0, gmin))
+    n_live = min(max_n, max(1, -(-chunk // gamma0)))
+    sparse = ops.sparse_attention(q, k, v, window=window, sink=sink, sm_scale=scale)
+    ref = sparse.clone()
+    assert len(st["chunks"]) == -(-s_p // chunk)
+    ahead = None
+    if chunk % gamma0 == 0:
+        ahead_rows = torch.arange(0, s_p, gamma0, device="cuda")
+        ahead = ops.qsparse_attention(q, k[:, :, :s_p], v[:, :, :s_p], ahead_rows, scale,
+                                      q_rows=ahead_rows)
+    recomputed = 0
+    for c in st["chunks"]:
+        start, g, n_c = c["start"], c["gamma"], c["n_anchors"]
+        end = min(start + chunk, s_p)
+        rows = torch.arange(start, end, g, device="cuda")
+        assert rows.numel() == n_c
+        if ahead is not None and g % gamma0 == 0:
+            dense = ahead[:, :, start // gamma0::g // gamma0][:, :, :n_c]
+        else:
+            recomputed += 1
+            padded = torch.full((max_n,), -1, dtype=torch.int64, device="cuda")
+            padded[:n_c] = rows
+            dense = ops.qsparse_attention(
+                q, k[:, :, :end], v[:, :, :end], padded, scale, q_rows=padded, n_live=n_live,
+                n_dev=torch.tensor([n_c], dtype=torch.int32, device="cuda"))[:, :, :n_c]
+        delta = dense.transpose(1, 2) - sparse[:, rows]
+        owner = torch.div(torch.arange(start, end, device="cuda") - start, g, rounding_mode="floor")
+        ref[:, start:end] = sparse[:, start:end] + delta[:, owner]
+    tail = torch.arange(s_p, s, device="cuda")
+    ref[:, s_p:] = ops.qsparse_attention(q, k, v, tail, scale, q_rows=tail).transpose(1, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), (out.float() - ref.float()).abs().max().item()
+    gammas = {c["gamma"] for c in st["chunks"]}
+    print(f"chunks {len(st['chunks'])} strides {sorted(gammas)} recomputed {recomputed}", flush=True)
+
+
 def test_adaptive_policy_sparse_only_returns_the_sparse_pass(gpu):
     """mode "sparse-only" returns before the adaptive branch (llama.py:695-696)."""
     from delta_attention.llama import LlamaAttention
