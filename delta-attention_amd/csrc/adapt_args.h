@@ -52,6 +52,6 @@ struct AdaptArgs {
   int* sel_log;
 };
 
-int adapt_step_launch(const CosArgs& c, const AdaptArgs& a, int dtype, hipStream_t st);
+int adapt_step_launch(const CosArgs& c, const AdaptArgs& a, int n_grid, int dtype, hipStream_t st);
 
 }  // namespace da

@@ -43,7 +43,7 @@ namespace da {
 int delta_add_chunk(void* out, const int64_t o_str[3], const void* dense,
                     const int64_t ds_str[3], const int* sel, const void* alt,
                     const int64_t alt_str[3], const int64_t* anchors, const int* n_dev,
-                    int max_n, int row_end, int s_p, int B, int H, int D, int dtype,
+                    int max_n, int row_end, int s_p, int B, int H, int D, int n_grid, int dtype,
                     hipStream_t s);
 
 namespace {
@@ -263,13 +263,16 @@ extern "C" int da_adapt_layer_fwd(const void* q, const void* k, const void* v, v
     else cs.a = dense;
     ad.chunk = c; ad.next_start = end; ad.next_end = next_end;
     ad.rows_next = next_end > end ? rows_c + max_n : nullptr;
-    if ((r = adapt_step_launch(cs, ad, dtype, st)) != DA_OK) return r;
+    // the grids of the cosines and the broadcast are sized for a chunk at the
+    // first stride and loop over more anchors (fewer empty workgroups; the
+    // launches' time beside the key-sparse launches did not change)
+    if ((r = adapt_step_launch(cs, ad, p.n_live, dtype, st)) != DA_OK) return r;
     if (side && !ok(hipEventRecord(ev_next[c % NEV], st))) return DA_ERR_LAUNCH;
     return use_ahead
         ? delta_add_chunk(out, o_str, ahead, ah_bhr, sel_log + 2 * c, dense, dn_bhr, rows_c,
-                          log_n + c, max_n, end, s_p, B, Hq, D, dtype, st)
+                          log_n + c, max_n, end, s_p, B, Hq, D, p.n_live, dtype, st)
         : delta_add_chunk(out, o_str, dense, dn_bhr, nullptr, nullptr, nullptr, rows_c,
-                          log_n + c, max_n, end, s_p, B, Hq, D, dtype, st);
+                          log_n + c, max_n, end, s_p, B, Hq, D, p.n_live, dtype, st);
   };
   for (int c = 0; c < p.nc && rc == DA_OK; ++c) {
     if (side) {

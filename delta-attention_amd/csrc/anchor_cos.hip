@@ -23,6 +23,8 @@
 #include "capi_common.h"
 #include "adapt_args.h"
 
+#include <algorithm>
+
 namespace da {
 
 
@@ -53,40 +55,44 @@ __device__ __forceinline__ void delta_pair(const CosArgs& a, int b, int i, int h
   }
 }
 
+// One wave per pair; with a device-held count the grid may be smaller than
+// the pairs (sized for the expected count), and the waves then loop.
 template <typename T>
 __global__ __launch_bounds__(256) void anchor_cos_kernel(CosArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int n = a.n_dev ? min(max(*a.n_dev, 0), a.n) : a.n;
   const int64_t pairs = n >= 2 ? (int64_t)a.B * (n - 1) * a.H : 0;
-  if (p >= pairs) return;
-  const int h = (int)(p % a.H);
-  const int64_t t = p / a.H;
-  const int i = (int)(t % (n - 1));
-  const int b = (int)(t / (n - 1));
-  float w12 = 0.f, w1 = 0.f, w2 = 0.f;
-  for (int e = 2 * lane; e < a.D; e += 128) {
-    float u0, u1, v0, v1;
-    delta_pair<T>(a, b, i, h, e, u0, u1);
-    delta_pair<T>(a, b, i + 1, h, e, v0, v1);
-    w12 += u0 * v0 + u1 * v1;
-    w1 += u0 * u0 + u1 * u1;
-    w2 += v0 * v0 + v1 * v1;
-  }
+  for (int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); p < pairs;
+       p += (int64_t)gridDim.x * 4) {
+    const int h = (int)(p % a.H);
+    const int64_t t = p / a.H;
+    const int i = (int)(t % (n - 1));
+    const int b = (int)(t / (n - 1));
+    float w12 = 0.f, w1 = 0.f, w2 = 0.f;
+    for (int e = 2 * lane; e < a.D; e += 128) {
+      float u0, u1, v0, v1;
+      delta_pair<T>(a, b, i, h, e, u0, u1);
+      delta_pair<T>(a, b, i + 1, h, e, v0, v1);
+      w12 += u0 * v0 + u1 * v1;
+      w1 += u0 * u0 + u1 * u1;
+      w2 += v0 * v0 + v1 * v1;
+    }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    w12 += __shfl_xor(w12, off);
-    w1 += __shfl_xor(w1, off);
-    w2 += __shfl_xor(w2, off);
-  }
-  if (lane != 0) return;
-  constexpr float EPS = 1e-8f;
-  const float c = w12 / (fmaxf(sqrtf(w1), EPS) * fmaxf(sqrtf(w2), EPS));
-  a.cos[p] = c;
-  if (a.hist && c >= a.lo && c <= a.hi) {
-    int bin = (int)((c - a.lo) * (float)a.bins / (a.hi - a.lo));
-    if (bin >= a.bins) bin = a.bins - 1;
-    atomicAdd(&a.hist[bin], 1);
+    for (int off = 32; off >= 1; off >>= 1) {
+      w12 += __shfl_xor(w12, off);
+      w1 += __shfl_xor(w1, off);
+      w2 += __shfl_xor(w2, off);
+    }
+    if (lane == 0) {
+      constexpr float EPS = 1e-8f;
+      const float c = w12 / (fmaxf(sqrtf(w1), EPS) * fmaxf(sqrtf(w2), EPS));
+      a.cos[p] = c;
+      if (a.hist && c >= a.lo && c <= a.hi) {
+        int bin = (int)((c - a.lo) * (float)a.bins / (a.hi - a.lo));
+        if (bin >= a.bins) bin = a.bins - 1;
+        atomicAdd(&a.hist[bin], 1);
+      }
+    }
   }
 }
 
@@ -175,9 +181,11 @@ __global__ __launch_bounds__(256) void adapt_next_kernel(AdaptArgs a) {
   }
 }
 
-// The two launches of one chunk step (the library's own chunk loop).
-int adapt_step_launch(const CosArgs& c, const AdaptArgs& a, int dtype, hipStream_t st) {
-  const int64_t grid = ((int64_t)c.B * (c.n > 1 ? c.n - 1 : 1) * c.H + 3) / 4;
+// The two launches of one chunk step (the library's own chunk loop); the
+// cosine grid is sized for n_grid deltas (c.n_dev holds the count).
+int adapt_step_launch(const CosArgs& c, const AdaptArgs& a, int n_grid, int dtype, hipStream_t st) {
+  const int ng = std::min(std::max(n_grid, 2), c.n > 1 ? c.n : 2);
+  const int64_t grid = ((int64_t)c.B * (ng - 1) * c.H + 3) / 4;
   if (grid > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
   (void)hipGetLastError();
   if (dtype == DA_BF16)

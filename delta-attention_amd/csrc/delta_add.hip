@@ -11,6 +11,8 @@
 #include "device_common.h"
 #include "capi_common.h"
 
+#include <algorithm>
+
 namespace da {
 
 struct DeltaArgs {
@@ -35,40 +37,11 @@ struct DeltaArgs {
 
 constexpr int DA_ROWS_UNROLL = 16;
 
-
-
+// Rows [r0, r1) of batch b (clamped to [0, s_p)) get the delta of anchor
+// slot aidx.
 template <typename T, bool FROM_DENSE>
-__global__ __launch_bounds__(256) void delta_add_kernel(DeltaArgs a) {
+__device__ __forceinline__ void add_group(const DeltaArgs& a, int b, int r0, int r1, int aidx) {
   using E = Elt<T>;
-  const int b = blockIdx.y;
-  int r0, r1, aidx;
-  if (a.n_dev) {
-    // one chunk of the adaptive stride: group g covers rows anchors[g] ..
-    // anchors[g + 1] - 1, the last one up to the chunk's end; the anchor
-    // count is read on the device
-    const int n = min(*a.n_dev, a.n_anchor);
-    aidx = blockIdx.x;
-    if (aidx >= n) return;
-    r0 = (int)a.anchors[aidx];
-    r1 = aidx + 1 < n ? (int)a.anchors[aidx + 1] : a.row_end;
-  } else if (a.anchors) {
-    // block 0 covers rows before anchors[0]; they take the last anchor's
-    // delta (searchsorted(..., right=True) - 1 == -1 picks the last entry).
-    const int g = (int)blockIdx.x - 1;
-    if (g < 0) {
-      r0 = 0;
-      r1 = (int)a.anchors[0];
-      aidx = a.n_anchor - 1;
-    } else {
-      r0 = (int)a.anchors[g];
-      r1 = g + 1 < a.n_anchor ? (int)a.anchors[g + 1] : a.s_p;
-      aidx = g;
-    }
-  } else {
-    aidx = blockIdx.x;
-    r0 = aidx * a.gamma;
-    r1 = r0 + a.gamma;
-  }
   if (r0 < 0) r0 = 0;
   if (r1 > a.s_p) r1 = a.s_p;
   if (r0 >= r1) return;
@@ -138,6 +111,42 @@ __global__ __launch_bounds__(256) void delta_add_kernel(DeltaArgs a) {
   }
 }
 
+template <typename T, bool FROM_DENSE>
+__global__ __launch_bounds__(256) void delta_add_kernel(DeltaArgs a) {
+  const int b = blockIdx.y;
+  if (a.n_dev) {
+    // one chunk of the adaptive stride: group g covers rows anchors[g] ..
+    // anchors[g + 1] - 1, the last one up to the chunk's end; the anchor
+    // count is read on the device, and the grid (sized for the expected
+    // count) loops over the groups
+    const int n = min(*a.n_dev, a.n_anchor);
+    for (int g = blockIdx.x; g < n; g += gridDim.x)
+      add_group<T, FROM_DENSE>(a, b, (int)a.anchors[g],
+                               g + 1 < n ? (int)a.anchors[g + 1] : a.row_end, g);
+    return;
+  }
+  int r0, r1, aidx;
+  if (a.anchors) {
+    // block 0 covers rows before anchors[0]; they take the last anchor's
+    // delta (searchsorted(..., right=True) - 1 == -1 picks the last entry).
+    const int g = (int)blockIdx.x - 1;
+    if (g < 0) {
+      r0 = 0;
+      r1 = (int)a.anchors[0];
+      aidx = a.n_anchor - 1;
+    } else {
+      r0 = (int)a.anchors[g];
+      r1 = g + 1 < a.n_anchor ? (int)a.anchors[g + 1] : a.s_p;
+      aidx = g;
+    }
+  } else {
+    aidx = blockIdx.x;
+    r0 = aidx * a.gamma;
+    r1 = r0 + a.gamma;
+  }
+  add_group<T, FROM_DENSE>(a, b, r0, r1, aidx);
+}
+
 template <typename T>
 static void launch_delta(const DeltaArgs& a, dim3 grid, bool from_dense, hipStream_t s) {
   if (from_dense)
@@ -153,11 +162,12 @@ static void launch_delta(const DeltaArgs& a, dim3 grid, bool from_dense, hipStre
 // before it writes the group, and no group reads another's rows, so the
 // update is safe in place. dense / alt: [B, H, rows, D] (strides batch, head,
 // anchor), chosen per anchor through sel as DeltaArgs describes (sel null:
-// row g of dense).
+// row g of dense). The grid has n_grid workgroups per batch, which loop over
+// the groups.
 int delta_add_chunk(void* out, const int64_t o_str[3], const void* dense,
                     const int64_t ds_str[3], const int* sel, const void* alt,
                     const int64_t alt_str[3], const int64_t* anchors, const int* n_dev,
-                    int max_n, int row_end, int s_p, int B, int H, int D, int dtype,
+                    int max_n, int row_end, int s_p, int B, int H, int D, int n_grid, int dtype,
                     hipStream_t s) {
   if (max_n < 1 || row_end < 0 || row_end > s_p || B < 1 || B > 65535) return DA_ERR_INVALID_ARG;
   if (!out || !o_str || !dense || !ds_str || !anchors || !n_dev) return DA_ERR_INVALID_ARG;
@@ -173,8 +183,9 @@ int delta_add_chunk(void* out, const int64_t o_str[3], const void* dense,
   a.sel = sel;
   if (sel) { a.dense_alt = alt; a.alt_b = alt_str[0]; a.alt_h = alt_str[1]; a.alt_a = alt_str[2]; }
   (void)hipGetLastError();
-  if (dtype == DA_BF16) launch_delta<__bf16>(a, dim3(max_n, B), true, s);
-  else launch_delta<_Float16>(a, dim3(max_n, B), true, s);
+  const int groups = std::min(std::max(n_grid, 1), max_n);
+  if (dtype == DA_BF16) launch_delta<__bf16>(a, dim3(groups, B), true, s);
+  else launch_delta<_Float16>(a, dim3(groups, B), true, s);
   return hipGetLastError() == hipSuccess ? DA_OK : DA_ERR_LAUNCH;
 }
 
