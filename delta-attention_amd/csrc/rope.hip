@@ -14,6 +14,10 @@
 // shared by every head, with ordinary loads. One launch covers the q rows then
 // the k rows; D/16 consecutive threads own one (token, head) row, 8 + 8
 // elements each (one 16-byte access per half), for D in {32, 64, 128, 256}.
+// Large inputs go through rope_stream_kernel, whose threads each take two
+// such row pieces with every load issued before the arithmetic (60 -> 69 % of
+// HBM at the 128K Llama shape). Indices are 32-bit with the launch's divisors
+// as multiply-shift constants.
 #include "device_common.h"
 #include "capi_common.h"
 
@@ -51,7 +55,18 @@ struct RopeArgs {
   void* vc;
   int64_t vc_b, vc_s, vc_h;
   int64_t v_rows;
+  FastDiv fd_hq, fd_hk, fd_s;   // the launch's divisors (q heads, k heads, tokens)
 };
+
+// Row pieces per thread of the streaming launch (measured at the 128K Llama
+// shape: 1 / 2 / 4 / 8 -> 4.94 / 5.50 / 5.43 / 2.83 TB/s; 8 runs out of
+// registers).
+#ifndef DA_ROPE_R
+#define DA_ROPE_R 2
+#endif
+
+// Thread indices are 32-bit: a launch covers fewer than 2^31 threads.
+constexpr int64_t ROPE_MAX_THREADS = 0x7fffffffLL;
 
 // threads per (token, head) row
 constexpr int rope_tpr(int D) { return D / 16; }
@@ -63,7 +78,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   constexpr int HALF = D / 2;
   constexpr int EPT = HALF / TPR;     // elements per thread in each half
   static_assert(EPT == 8, "one 16-byte access per half");
-  const int64_t gtid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t gtid = blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = gtid / TPR;
   const int part = (int)(gtid % TPR);
   constexpr size_t esz = sizeof(T);
@@ -73,8 +88,9 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   if (a.v_rows > 0 && row >= a.q.rows + a.k.rows) {
     // cache append of v: this thread's 2 x EPT elements, no arithmetic
     if (row >= a.rows || !crow_ok) return;
-    const int64_t vr = row - a.q.rows - a.k.rows;
-    const int hv = (int)(vr % a.k.H), bv = (int)(vr / a.k.H);   // S == 1
+    const uint32_t vr = (uint32_t)(row - a.q.rows - a.k.rows);
+    const uint32_t bv_ = fdiv(vr, a.fd_hk);                      // S == 1
+    const int hv = (int)fmodq(vr, bv_, a.fd_hk), bv = (int)bv_;
     const char* src = (const char*)a.v + ((int64_t)bv * a.v_b + (int64_t)hv * a.v_h) * esz;
     char* dst = (char*)a.vc + ((int64_t)bv * a.vc_b + crow * a.vc_s + (int64_t)hv * a.vc_h) * esz;
     const int j0 = part * EPT;
@@ -87,16 +103,17 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int64_t rr = live ? (kpart ? row - a.q.rows : row) : 0;
   // the part's fields by selects (dynamic indexing of kernel arguments would
   // copy them to scratch)
-  const int H = kpart ? a.k.H : a.q.H;
   const int64_t xs_b = kpart ? a.k.xs_b : a.q.xs_b;
   const int64_t xs_s = kpart ? a.k.xs_s : a.q.xs_s;
   const int64_t xs_h = kpart ? a.k.xs_h : a.q.xs_h;
   const void* w = kpart ? a.k.w : a.q.w;
   char* const xbase = (char*)(kpart ? a.k.x : a.q.x);
-  const int h = (int)(rr % H);
-  const int64_t bs = rr / H;
-  const int s = (int)(bs % a.S);
-  const int b = (int)(bs / a.S);
+  const FastDiv fd_h = kpart ? a.fd_hk : a.fd_hq;
+  const uint32_t bs = fdiv((uint32_t)rr, fd_h);
+  const int h = (int)fmodq((uint32_t)rr, bs, fd_h);
+  const uint32_t b_ = fdiv(bs, a.fd_s);
+  const int s = (int)fmodq(bs, b_, a.fd_s);
+  const int b = (int)b_;
   char* xp = xbase + ((int64_t)b * xs_b + (int64_t)s * xs_s + (int64_t)h * xs_h) * esz;
   const int i0 = part * EPT;          // first element of this thread in the low half
 
@@ -169,6 +186,107 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   }
 }
 
+// The in-place launch over large inputs (no cache append): R row pieces per
+// thread, all their loads issued before any arithmetic, so that each thread
+// keeps 2 R streaming loads (and 4 R loads of the cached cos / sin rows) in
+// flight. Piece j of thread t is unit t + j * T (T threads in the grid):
+// consecutive threads read consecutive 16-byte pieces at every j. The
+// arithmetic is rope_kernel's, operation for operation.
+template <typename T, int D, int R>
+__global__ __launch_bounds__(256) void rope_stream_kernel(RopeArgs a) {
+  using E = Elt<T>;
+  constexpr int TPR = rope_tpr(D);
+  constexpr int HALF = D / 2;
+  constexpr int EPT = HALF / TPR;
+  static_assert(EPT == 8, "one 16-byte access per half");
+  constexpr size_t esz = sizeof(T);
+  const uint32_t nthr = gridDim.x * blockDim.x;
+  const uint32_t t0 = blockIdx.x * blockDim.x + threadIdx.x;
+  const int part = (int)(t0 % TPR);       // nthr is a multiple of TPR
+  const int i0 = part * EPT;
+  char* xp[R];
+  const void* wp[R];
+  u32x4 xl[R], xh[R], cl[R], ch[R], sl[R], sh[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const uint32_t row = (t0 + j * nthr) / TPR;
+    const bool live = row < (uint64_t)a.rows;
+    const bool kpart = live && row >= (uint64_t)a.q.rows;
+    const uint32_t rr = live ? (kpart ? row - (uint32_t)a.q.rows : row) : 0;
+    const FastDiv fd_h = kpart ? a.fd_hk : a.fd_hq;
+    const uint32_t bs = fdiv(rr, fd_h);
+    const int h = (int)fmodq(rr, bs, fd_h);
+    const uint32_t b = fdiv(bs, a.fd_s);
+    const int s = (int)fmodq(bs, b, a.fd_s);
+    const int64_t xs_b = kpart ? a.k.xs_b : a.q.xs_b;
+    const int64_t xs_s = kpart ? a.k.xs_s : a.q.xs_s;
+    const int64_t xs_h = kpart ? a.k.xs_h : a.q.xs_h;
+    char* const xbase = (char*)(kpart ? a.k.x : a.q.x);
+    wp[j] = kpart ? a.k.w : a.q.w;
+    xp[j] = live ? xbase + ((int64_t)b * xs_b + (int64_t)s * xs_s + (int64_t)h * xs_h) * esz : nullptr;
+    const int64_t cs = (int64_t)(a.cs_b ? b : 0) * a.cs_b + (int64_t)s * a.cs_s;
+    const char* cp = (const char*)a.cos + cs * esz;
+    const char* sp = (const char*)a.sin + cs * esz;
+    if (live) {
+      xl[j] = ld_nt4(xp[j] + i0 * esz);
+      xh[j] = ld_nt4(xp[j] + (HALF + i0) * esz);
+    } else {
+      xl[j] = u32x4{0, 0, 0, 0};
+      xh[j] = u32x4{0, 0, 0, 0};
+    }
+    cl[j] = *(const u32x4*)(cp + i0 * esz);
+    ch[j] = *(const u32x4*)(cp + (HALF + i0) * esz);
+    sl[j] = *(const u32x4*)(sp + i0 * esz);
+    sh[j] = *(const u32x4*)(sp + (HALF + i0) * esz);
+  }
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    float lo[EPT], hi[EPT];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lo[2 * e] = E::lo(xl[j][e]); lo[2 * e + 1] = E::hi(xl[j][e]);
+      hi[2 * e] = E::lo(xh[j][e]); hi[2 * e + 1] = E::hi(xh[j][e]);
+    }
+    if (wp[j]) {     // uniform per row: the TPR lanes of a row share it
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
+#pragma unroll
+      for (int off = 1; off < TPR; off <<= 1) ss += __shfl_xor(ss, off);
+      const float r = rsqrtf(ss / (float)D + a.eps);
+      const u32x4 wl4 = *(const u32x4*)((const char*)wp[j] + i0 * esz);
+      const u32x4 wh4 = *(const u32x4*)((const char*)wp[j] + (HALF + i0) * esz);
+#pragma unroll
+      for (int e = 0; e < EPT; e += 2) {
+        uint32_t p = E::pack2(lo[e] * r, lo[e + 1] * r);
+        p = E::pack2(E::lo(wl4[e / 2]) * E::lo(p), E::hi(wl4[e / 2]) * E::hi(p));
+        lo[e] = E::lo(p); lo[e + 1] = E::hi(p);
+        uint32_t q = E::pack2(hi[e] * r, hi[e + 1] * r);
+        q = E::pack2(E::lo(wh4[e / 2]) * E::lo(q), E::hi(wh4[e / 2]) * E::hi(q));
+        hi[e] = E::lo(q); hi[e + 1] = E::hi(q);
+      }
+    }
+    uint32_t olo[EPT / 2], ohi[EPT / 2];
+#pragma unroll
+    for (int e = 0; e < EPT; e += 2) {
+      const float c0 = E::lo(cl[j][e / 2]), c1 = E::hi(cl[j][e / 2]);
+      const float s0 = E::lo(sl[j][e / 2]), s1 = E::hi(sl[j][e / 2]);
+      const float d0 = E::lo(ch[j][e / 2]), d1 = E::hi(ch[j][e / 2]);
+      const float t0_ = E::lo(sh[j][e / 2]), t1_ = E::hi(sh[j][e / 2]);
+      const uint32_t a1 = E::pack2(lo[e] * c0, lo[e + 1] * c1);
+      const uint32_t a2 = E::pack2(-hi[e] * s0, -hi[e + 1] * s1);
+      olo[e / 2] = E::pack2(E::lo(a1) + E::lo(a2), E::hi(a1) + E::hi(a2));
+      const uint32_t b1 = E::pack2(hi[e] * d0, hi[e + 1] * d1);
+      const uint32_t b2 = E::pack2(lo[e] * t0_, lo[e + 1] * t1_);
+      ohi[e / 2] = E::pack2(E::lo(b1) + E::lo(b2), E::hi(b1) + E::hi(b2));
+    }
+    if (xp[j]) {
+      st_nt4(xp[j] + i0 * esz, u32x4{olo[0], olo[1], olo[2], olo[3]});
+      st_nt4(xp[j] + (HALF + i0) * esz, u32x4{ohi[0], ohi[1], ohi[2], ohi[3]});
+    }
+  }
+}
+
 template <typename T, int D, bool NT>
 static void launch_rope_d(const RopeArgs& a, hipStream_t s) {
   const int64_t threads = a.rows * rope_tpr(D);
@@ -186,10 +304,26 @@ static void launch_rope_nt(const RopeArgs& a, hipStream_t s) {
 
 static bool rope_dim_ok(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
 
+constexpr int ROPE_STREAM_R = DA_ROPE_R;   // row pieces per thread of rope_stream_kernel
+
+template <typename T, int D>
+static void launch_rope_stream_d(const RopeArgs& a, hipStream_t s) {
+  const int64_t units = a.rows * rope_tpr(D);
+  const int grid = (int)((units + 256 * ROPE_STREAM_R - 1) / (256 * ROPE_STREAM_R));
+  hipLaunchKernelGGL((rope_stream_kernel<T, D, ROPE_STREAM_R>), dim3(grid), dim3(256), 0, s, a);
+}
+
 template <typename T>
 static void launch_rope(const RopeArgs& a, hipStream_t s) {
-  if (a.rows * a.D * (int64_t)sizeof(T) >= NT_MIN_BYTES) launch_rope_nt<T, true>(a, s);
-  else launch_rope_nt<T, false>(a, s);
+  if (a.rows * a.D * (int64_t)sizeof(T) >= NT_MIN_BYTES) {
+    if (ROPE_STREAM_R <= 1) launch_rope_nt<T, true>(a, s);
+    else if (a.D == 128) launch_rope_stream_d<T, 128>(a, s);
+    else if (a.D == 64) launch_rope_stream_d<T, 64>(a, s);
+    else if (a.D == 256) launch_rope_stream_d<T, 256>(a, s);
+    else launch_rope_stream_d<T, 32>(a, s);
+  } else {
+    launch_rope_nt<T, false>(a, s);
+  }
 }
 
 }  // namespace da
@@ -229,7 +363,10 @@ extern "C" int da_rope_qk(void* q, const int64_t q_str[3], int Hq,
   a.eps = eps; a.B = B; a.S = S; a.D = D;
   a.rows = a.q.rows + a.k.rows;
   if (a.rows == 0) return DA_OK;
-  if (a.rows * rope_tpr(D) / 256 > 0x7fffffffLL) return DA_ERR_INVALID_ARG;
+  if (a.rows * rope_tpr(D) + 255 > ROPE_MAX_THREADS) return DA_ERR_INVALID_ARG;
+  a.fd_hq = make_fastdiv((uint32_t)(Hq > 0 ? Hq : 1));
+  a.fd_hk = make_fastdiv((uint32_t)(Hkv > 0 ? Hkv : 1));
+  a.fd_s = make_fastdiv((uint32_t)S);
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
   if (dtype == DA_BF16) launch_rope<__bf16>(a, s);
@@ -268,6 +405,10 @@ extern "C" int da_rope_qk_append(void* q, const int64_t q_str[3], int Hq,
   a.vc = v_cache; a.vc_b = vc_str[0]; a.vc_s = vc_str[1]; a.vc_h = vc_str[2];
   a.v_rows = (int64_t)B * Hkv;
   a.rows = a.q.rows + a.k.rows + a.v_rows;
+  if (a.rows * rope_tpr(D) + 255 > ROPE_MAX_THREADS) return DA_ERR_INVALID_ARG;
+  a.fd_hq = make_fastdiv((uint32_t)Hq);
+  a.fd_hk = make_fastdiv((uint32_t)Hkv);
+  a.fd_s = make_fastdiv(1u);
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
   if (dtype == DA_BF16) launch_rope_nt<__bf16, false>(a, s);

@@ -51,6 +51,38 @@ def test_rope_bit_exact(gpu, dtype, D, per_batch):
     assert torch.equal(buf[..., (Hq + Hkv) * D:], v_before)     # v untouched
 
 
+@pytest.mark.parametrize("dtype,D,norm", [(torch.bfloat16, 128, False), (torch.float16, 64, False),
+                                          (torch.bfloat16, 32, False), (torch.bfloat16, 256, False),
+                                          (torch.bfloat16, 128, True), (torch.float16, 256, True)])
+def test_rope_large_inputs(gpu, dtype, D, norm):
+    """Inputs of 4 MB and more take the streaming launch (several row pieces
+    per thread); an odd token count leaves the last pieces of the grid empty."""
+    from delta_attention import ops
+    from delta_attention.llama import LlamaRMSNorm, apply_rotary_pos_emb
+    B, S, Hq, Hkv = 1, 4099, 32, 8
+    assert S * (Hq + Hkv) * D * 2 >= 4 << 20
+    buf, q, k = _proj_views(B, S, Hq, Hkv, D, dtype, seed=D + 7)
+    cos, sin = _tables(B, S, D, dtype, False)
+    v_before = buf[..., (Hq + Hkv) * D:].clone()
+    with torch.no_grad():
+        if norm:
+            qn, kn = LlamaRMSNorm(D, 1e-6).cuda().to(dtype), LlamaRMSNorm(D, 1e-6).cuda().to(dtype)
+            torch.nn.init.uniform_(qn.weight, 0.5, 1.5)
+            torch.nn.init.uniform_(kn.weight, 0.5, 1.5)
+            rq, rk = apply_rotary_pos_emb(qn(q).transpose(1, 2), kn(k).transpose(1, 2), cos, sin)
+            ops.rope_qk(q, k, cos, sin, q_norm_w=qn.weight, k_norm_w=kn.weight, eps=1e-6)
+        else:
+            rq, rk = apply_rotary_pos_emb(q.transpose(1, 2).clone(), k.transpose(1, 2).clone(), cos, sin)
+            ops.rope_qk(q, k, cos, sin)
+    torch.cuda.synchronize()
+    if norm:
+        _within_one_rounding(q.transpose(1, 2), rq, "q")
+        _within_one_rounding(k.transpose(1, 2), rk, "k")
+    else:
+        assert torch.equal(q.transpose(1, 2), rq) and torch.equal(k.transpose(1, 2), rk)
+    assert torch.equal(buf[..., (Hq + Hkv) * D:], v_before)     # v untouched
+
+
 @pytest.mark.parametrize("D", [128, 64, 32, 256])
 def test_rope_matches_oracle_bf16(gpu, D):
     from delta_attention import ops
