@@ -177,8 +177,9 @@ def test_adaptive_stride_path(gpu, mode):
     assert_close(np64(out), ref, what=f"adaptive ({mode})")
 
 
-@pytest.mark.parametrize("trigger,threshold,k", [("absolute", None, 2.0), ("relative", 0.95, 0.3)])
-def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold, k):
+@pytest.mark.parametrize("trigger,threshold,k,B", [("absolute", None, 2.0, 1), ("relative", 0.95, 0.3, 1),
+                                                    ("absolute", None, 2.0, 2)])
+def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold, k, B):
     """The adaptive chunk loop decides each next stride on the device
     (da_adapt_chunk_step). Checked against the host rules of stride.py:
     every logged stride follows from the previous chunk's logged mean by
@@ -191,7 +192,7 @@ def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold
     from delta_attention.llama import LlamaAttention
     from delta_attention.stride import next_gamma, next_gamma_relative
     s, chunk, window, sink = 4096, 256, 256, 16
-    q, k_, v = gen_qkv(1, 8, 2, s, 128, seed=12)
+    q, k_, v = gen_qkv(B, 8, 2, s, 128, seed=12)
 
     def run(thr):
         cfg = _cfg(8, 2, 128, stride_policy="adaptive", adapt_chunk=chunk, delta_lambda=32,
@@ -230,9 +231,12 @@ def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold
         assert float(cos.min()) == c["cos_min"]
 
 
-@pytest.mark.parametrize("s,chunk,gamma0,gmin", [(4096, 512, 32, 8), (3000, 1024, 64, 16),
-                                                  (2500, 1000, 64, 16)])
-def test_adaptive_layer_composition_is_exact(gpu, s, chunk, gamma0, gmin):
+@pytest.mark.parametrize("B,s,chunk,gamma0,gmin,dtype", [
+    (1, 4096, 512, 32, 8, torch.bfloat16), (1, 3000, 1024, 64, 16, torch.bfloat16),
+    (1, 2500, 1000, 64, 16, torch.bfloat16),      # adapt_chunk not a multiple of gamma0
+    (2, 3072, 512, 32, 8, torch.bfloat16),        # batch 2: the cosines average over it
+    (1, 2048, 512, 32, 16, torch.float16), (2, 1800, 600, 64, 16, torch.float16)])
+def test_adaptive_layer_composition_is_exact(gpu, B, s, chunk, gamma0, gmin, dtype):
     """The one-call adaptive layer (da_adapt_layer_fwd) against the same
     steps issued one by one: the key-sparse pass over all rows; each chunk's
     dense anchor rows from the same kernel (2) launch as inside, i.e. when
@@ -247,11 +251,11 @@ def test_adaptive_layer_composition_is_exact(gpu, s, chunk, gamma0, gmin):
     from delta_attention.llama import LlamaAttention
     window, sink, H, Hkv = 256, 16, 8, 2
     scale = 128 ** -0.5
-    q, k, v = gen_qkv(1, H, Hkv, s, 128, seed=21)
+    q, k, v = gen_qkv(B, H, Hkv, s, 128, seed=21 + B, dtype=dtype)
     cfg = _cfg(H, Hkv, 128, stride_policy="adaptive", adapt_chunk=chunk, delta_lambda=gamma0,
                adapt_threshold=0.97, gamma_min=gmin, gamma_max=128, sliding_window=window,
                sink_tokens=sink)
-    m = LlamaAttention(cfg, layer_idx=0).cuda().to(torch.bfloat16)
+    m = LlamaAttention(cfg, layer_idx=0).cuda().to(dtype)
     out, _ = m.delta_forward(m, q, k, v, None, scaling=scale)
     st = m._stride_stats
     cut_n = s % gamma0 + max(128, gamma0)
@@ -281,6 +285,7 @@ def test_adaptive_layer_composition_is_exact(gpu, s, chunk, gamma0, gmin):
             dense = ops.qsparse_attention(
                 q, k[:, :, :end], v[:, :, :end], padded, scale, q_rows=padded, n_live=n_live,
                 n_dev=torch.tensor([n_c], dtype=torch.int32, device="cuda"))[:, :, :n_c]
+        assert dense.dtype == dtype
         delta = dense.transpose(1, 2) - sparse[:, rows]
         owner = torch.div(torch.arange(start, end, device="cuda") - start, g, rounding_mode="floor")
         ref[:, start:end] = sparse[:, start:end] + delta[:, owner]
