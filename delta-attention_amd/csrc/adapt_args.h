@@ -42,12 +42,14 @@ struct AdaptArgs {
   float* log_min;
   int* log_gamma;
   int* log_n;
-  // spec_gamma > 0: the dense rows at multiples of spec_gamma are computed
-  // ahead; state holds 5 ints {gamma, n, n_recompute, slot0, step}: a next
-  // chunk whose anchors are all such rows (stride and start multiples of
-  // spec_gamma) reads them at slots slot0 + j * step and recomputes none, any
-  // other gets slot0 = -1 and recomputes its n anchors. sel_log[2 c .. 2 c + 1]
-  // logs this chunk's {slot0, step}.
+  // full_state: state holds 5 ints {gamma, n, n_recompute, slot0, step}, all
+  // written for the next chunk. spec_gamma > 0: the dense rows at multiples of
+  // spec_gamma are computed ahead; a next chunk whose anchors are all such
+  // rows (stride and start multiples of spec_gamma) reads them at slots
+  // slot0 + j * step and recomputes none; any other chunk (every chunk with
+  // spec_gamma 0) gets slot0 = -1 and recomputes its n anchors.
+  // sel_log[2 c .. 2 c + 1] logs this chunk's {slot0, step}.
+  bool full_state;
   int spec_gamma;
   int* sel_log;
 };

@@ -233,6 +233,7 @@ extern "C" int da_adapt_layer_fwd(const void* q, const void* k, const void* v, v
   ad.trigger = trigger; ad.threshold = threshold; ad.margin = margin; ad.k = k_sd;
   ad.gamma_min = gamma_min; ad.gamma_max = gamma_max;
   ad.log_mean = log_mean; ad.log_min = log_min; ad.log_gamma = log_gamma; ad.log_n = log_n;
+  ad.full_state = true;
   ad.spec_gamma = use_ahead ? gamma0 : 0;
   ad.sel_log = use_ahead ? sel_log : nullptr;
 

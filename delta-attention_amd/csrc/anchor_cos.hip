@@ -166,8 +166,9 @@ __global__ __launch_bounds__(256) void adapt_next_kernel(AdaptArgs a) {
     s_next[1] = min(nn, a.max_n);
     a.state[0] = g;
     a.state[1] = min(nn, a.max_n);
-    if (a.spec_gamma > 0) {
-      const bool ahead = g % a.spec_gamma == 0 && a.next_start % a.spec_gamma == 0;
+    if (a.full_state) {
+      const bool ahead = a.spec_gamma > 0 && g % a.spec_gamma == 0 &&
+                         a.next_start % a.spec_gamma == 0;
       a.state[2] = ahead ? 0 : min(nn, a.max_n);
       a.state[3] = ahead ? a.next_start / a.spec_gamma : -1;
       a.state[4] = ahead ? g / a.spec_gamma : 1;

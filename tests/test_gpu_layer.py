@@ -234,6 +234,8 @@ def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold
 @pytest.mark.parametrize("B,s,chunk,gamma0,gmin,dtype", [
     (1, 4096, 512, 32, 8, torch.bfloat16), (1, 3000, 1024, 64, 16, torch.bfloat16),
     (1, 2500, 1000, 64, 16, torch.bfloat16),      # adapt_chunk not a multiple of gamma0
+    # no rows ahead, and chunks of 63 and 125 anchors (more row tiles than the first chunk's 16)
+    (1, 4500, 1000, 64, 8, torch.bfloat16),
     (2, 3072, 512, 32, 8, torch.bfloat16),        # batch 2: the cosines average over it
     (1, 2048, 512, 32, 16, torch.float16), (2, 1800, 600, 64, 16, torch.float16)])
 def test_adaptive_layer_composition_is_exact(gpu, B, s, chunk, gamma0, gmin, dtype):
@@ -294,7 +296,10 @@ def test_adaptive_layer_composition_is_exact(gpu, B, s, chunk, gamma0, gmin, dty
     torch.cuda.synchronize()
     assert torch.equal(out, ref), (out.float() - ref.float()).abs().max().item()
     gammas = {c["gamma"] for c in st["chunks"]}
-    print(f"chunks {len(st['chunks'])} strides {sorted(gammas)} recomputed {recomputed}", flush=True)
+    print(f"chunks {len(st['chunks'])} strides {sorted(gammas)} recomputed {recomputed} "
+          f"anchors {[c['n_anchors'] for c in st['chunks']]}", flush=True)
+    if (s, chunk) == (4500, 1000):
+        assert max(c["n_anchors"] for c in st["chunks"]) > 64, st["chunks"]
 
 
 def test_adaptive_policy_sparse_only_returns_the_sparse_pass(gpu):
