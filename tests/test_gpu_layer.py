@@ -237,6 +237,9 @@ def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold
     # no rows ahead, and chunks of 63 and 125 anchors (more row tiles than the first chunk's 16)
     (1, 4500, 1000, 64, 8, torch.bfloat16),
     (2, 3072, 512, 32, 8, torch.bfloat16),        # batch 2: the cosines average over it
+    (1, 1000, 2048, 64, 16, torch.bfloat16),      # one chunk, shorter than adapt_chunk
+    (1, 2600, 256, 128, 16, torch.bfloat16),      # starting stride 128: chunks of 2 anchors
+    (1, 1500, 96, 16, 4, torch.bfloat16),         # many short chunks, strides down to 4
     (1, 2048, 512, 32, 16, torch.float16), (2, 1800, 600, 64, 16, torch.float16)])
 def test_adaptive_layer_composition_is_exact(gpu, B, s, chunk, gamma0, gmin, dtype):
     """The one-call adaptive layer (da_adapt_layer_fwd) against the same
