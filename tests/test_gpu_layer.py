@@ -305,6 +305,25 @@ def test_adaptive_layer_composition_is_exact(gpu, B, s, chunk, gamma0, gmin, dty
         assert max(c["n_anchors"] for c in st["chunks"]) > 64, st["chunks"]
 
 
+def test_adaptive_layer_strided_inputs(gpu):
+    """The module hands over q/k/v as [B,H,S,D] views of [B,S,H,D] projections:
+    the one-call adaptive layer reads them through their strides, with the
+    bits of the same call on contiguous copies."""
+    from delta_attention.llama import LlamaAttention
+    q, k, v = gen_qkv(2, 8, 2, 2304, 128, seed=33, model_layout=True)
+    assert not q.is_contiguous()
+    cfg = _cfg(8, 2, 128, stride_policy="adaptive", adapt_chunk=512, delta_lambda=32,
+               adapt_threshold=0.97, gamma_min=8, gamma_max=128)
+    m = LlamaAttention(cfg, layer_idx=0).cuda().to(torch.bfloat16)
+    out_v, _ = m.delta_forward(m, q, k, v, None, scaling=128 ** -0.5)
+    st_v = m._stride_stats
+    out_c, _ = m.delta_forward(m, q.contiguous(), k.contiguous(), v.contiguous(), None,
+                               scaling=128 ** -0.5)
+    torch.cuda.synchronize()
+    assert m._stride_stats["chunks"] == st_v["chunks"]
+    assert torch.equal(out_v, out_c)
+
+
 def test_adaptive_policy_sparse_only_returns_the_sparse_pass(gpu):
     """mode "sparse-only" returns before the adaptive branch (llama.py:695-696)."""
     from delta_attention.llama import LlamaAttention
