@@ -52,6 +52,13 @@ class LlamaConfig:
     sliding_window: int = 2048
     sink_tokens: int = 128
     stride_policy: str = "fixed"
+    # adaptive stride (stride_policy "adaptive"), the defaults of config.Config
+    gamma_min: int = 16
+    gamma_max: int = 256
+    adapt_chunk: int = 4096
+    adapt_threshold: float = 0.95
+    stride_trigger: str = "absolute"
+    adapt_k: float = 2.0
     log_drift: bool = False
     decode_mode: str = "dense"
     gamma_dec: int = 32

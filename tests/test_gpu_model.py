@@ -95,3 +95,40 @@ def test_small_model_matches_reference_layer_ops(gpu, D):
     assert cos_rows.min() > 0.999, cos_rows.min()
     assert (lg * lr).sum() / (np.linalg.norm(lg) * np.linalg.norm(lr)) > 0.999
     assert tok.shape == (1,) and int(tok[0]) == int(ref_tok[0])
+
+
+def test_small_model_adaptive_policy(gpu):
+    """stride_policy "adaptive" through the whole model: with the stride pinned
+    (gamma_min = gamma_max = delta_lambda) every chunk keeps the fixed stride,
+    so the model matches the fixed-stride model to rounding (the dense anchor
+    rows come from other launches); every layer leaves its stride statistics,
+    read from the device logs on first access; with the stride free, the
+    prefill still gives a finite greedy token."""
+    from delta_attention.model import LlamaConfig, random_llama
+    base = dict(vocab_size=512, hidden_size=1024, intermediate_size=2048, num_hidden_layers=2,
+                num_attention_heads=8, num_key_value_heads=2, head_dim=128, delta_lambda=64,
+                sliding_window=256, sink_tokens=16)
+    S = 3000
+    ids = torch.randint(0, 512, (1, S), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(9))
+    outs = {}
+    for policy, gmin, gmax in (("fixed", 16, 256), ("adaptive", 64, 64), ("adaptive", 16, 256)):
+        cfg = LlamaConfig(**base, stride_policy=policy, adapt_chunk=512, gamma_min=gmin,
+                          gamma_max=gmax, adapt_threshold=0.95)
+        m = random_llama(cfg, "cuda", torch.bfloat16, seed=5)
+        with torch.inference_mode():
+            outs[(policy, gmin)] = (m.model(ids), m.prefill_next_token(ids))
+        if policy == "adaptive":
+            for layer in m.model.layers:
+                st = layer.self_attn._stride_stats
+                assert st["kind"] == "stride" and st["seq_len"] == S
+                assert len(st["chunks"]) == -(-(S - (S % 64 + 128)) // 512)
+                if gmin == gmax:
+                    assert {c["gamma"] for c in st["chunks"]} == {64}
+    g = np64(outs[("adaptive", 64)][0])[0]
+    r = np64(outs[("fixed", 16)][0])[0]
+    cos_rows = (g * r).sum(-1) / (np.linalg.norm(g, axis=-1) * np.linalg.norm(r, axis=-1))
+    assert cos_rows.min() > 0.999, cos_rows.min()
+    assert int(outs[("adaptive", 64)][1][0]) == int(outs[("fixed", 16)][1][0])
+    free = outs[("adaptive", 16)]
+    assert torch.isfinite(free[0]).all() and 0 <= int(free[1][0]) < 512
