@@ -82,9 +82,10 @@ def parse():
                    help="time delta_forward_train's forward and backward (the training "
                         "path) at --seq/--gamma/--window/--sink instead of the prefill")
     p.add_argument("--adaptive", action="store_true",
-                   help="time the adaptive-stride layer (stride_policy \"adaptive\": per "
-                        "--adapt-chunk rows a dense pass at the current stride, the inter-anchor "
-                        "delta cosine, one host sync per chunk) beside the fixed-stride layer")
+                   help="time the adaptive-stride layer (stride_policy \"adaptive\", one "
+                        "library call: per --adapt-chunk rows the inter-anchor delta cosine and "
+                        "the next stride decided on the device) beside the fixed-stride layer; "
+                        "with --model, every layer of the model uses it")
     p.add_argument("--adapt-chunk", type=int, default=4096)
     p.add_argument("--adapt-threshold", type=float, default=0.95)
     p.add_argument("--copy-calibration", action="store_true",
@@ -379,6 +380,10 @@ def model_prefill(a, dev):
     from oracle import delta_oracle as O
     cfg = LlamaConfig(num_hidden_layers=a.layers, delta_lambda=a.gamma, sliding_window=a.window,
                       sink_tokens=a.sink)
+    if a.adaptive:
+        # --model --adaptive: every layer with stride_policy "adaptive"
+        cfg.stride_policy, cfg.adapt_chunk = "adaptive", a.adapt_chunk
+        cfg.adapt_threshold, cfg.gamma_min, cfg.gamma_max = a.adapt_threshold, 16, 256
     B, S = a.batch, a.seq
     t0 = time.perf_counter()
     model = random_llama(cfg, dev, torch.bfloat16, seed=a.seed)
@@ -403,7 +408,24 @@ def model_prefill(a, dev):
     counts = O.sparse_row_counts(S, a.window, a.sink)
     rows = ops.fused_delta_rows(H, Hkv)
     f_sparse = 4.0 * D * H * B * float(counts[:s_p].sum() if rows and rows % a.gamma == 0 else counts.sum())
-    f_attn = L * (f_sparse + O.flops_qsparse(B, H, D, O.selected_rows(S, a.gamma)))
+    strides = None
+    if a.adaptive:
+        # each layer's own anchors (from its stride statistics) plus the dense tail
+        f_attn = 0.0
+        strides = {"anchors_per_layer": [], "chunks_per_stride": {}}
+        for layer in model.model.layers:
+            st = layer.self_attn._stride_stats
+            strides["anchors_per_layer"].append(st["n_anchors"])
+            for c in st["chunks"]:
+                key = str(c["gamma"])
+                strides["chunks_per_stride"][key] = strides["chunks_per_stride"].get(key, 0) + 1
+            sel = [r for c in st["chunks"]
+                   for r in range(c["start"], c["start"] + c["n_anchors"] * c["gamma"], c["gamma"])]
+            sel = np.array(sel + list(range(s_p, S)))
+            # the key-sparse pass covers rows below s_p (the tail rows are dense)
+            f_attn += 4.0 * D * H * B * float(counts[:s_p].sum()) + O.flops_qsparse(B, H, D, sel)
+    else:
+        f_attn = L * (f_sparse + O.flops_qsparse(B, H, D, O.selected_rows(S, a.gamma)))
     hid, inter = cfg.hidden_size, cfg.intermediate_size
     per_tok = 2 * (hid * (H + 2 * Hkv) * D + H * D * hid + 3 * hid * inter)
     f_gemm = L * per_tok * B * S + 2 * B * hid * cfg.vocab_size
@@ -416,7 +438,8 @@ def model_prefill(a, dev):
         "data": "synthetic (random token ids, weights ~ N(0, 0.02) per the reference's _init_weights)",
         "config": {"workload": "llama-3.1-8b-architecture causal LM prefill, delta attention in every layer",
                    "layers": L, "batch": B, "seq_len": S, "window": a.window, "sink": a.sink,
-                   "gamma": a.gamma, "params": sum(p.numel() for p in model.parameters()),
+                   "gamma": a.gamma, "stride_policy": cfg.stride_policy,
+                   "params": sum(p.numel() for p in model.parameters()),
                    "rope_scaling": cfg.rope_scaling, "parallelism": "none (1 GPU)"},
         "attention_share": round(attn_ms / timed_total, 4),
         "tokens_per_s": round(B * S / (ttft * 1e-3), 1),
@@ -427,6 +450,8 @@ def model_prefill(a, dev):
                    "model": round((f_attn + f_gemm) / (ttft * 1e-3) / 1e12, 1)},
         "first_token": int(tok[0]), "init_s": round(init_s, 2),
     }
+    if strides is not None:
+        line["adaptive_strides"] = strides
     if a.decode_tokens > 1:
         # generation after the prefill: ms per decode token, dense vs delta
         # decode, each step launched eagerly or replayed from HIP graphs
