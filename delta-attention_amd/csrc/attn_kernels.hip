@@ -68,6 +68,12 @@ namespace da {
 // of the 256-CU gfx950 (two per CU), so the items run in a single round
 // (dense row over 131072 keys: 106-111 us against 118 us at 1024 items and
 // 131 us at 2048).
+// Shortest split item of a selected-rows launch, in key tiles (binding on
+// short launches such as 638 rows at 32K: 40 / 48 / 56 / 64 / 80 tiles ->
+// kernel (2) 0.255 / 0.258 / 0.243 / 0.254 / 0.260 ms).
+#ifndef DA_ROWS_MIN_TILES
+#define DA_ROWS_MIN_TILES 56
+#endif
 #ifndef DA_DECODE_ITEMS
 #define DA_DECODE_ITEMS 512
 #endif
@@ -1096,7 +1102,7 @@ static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
   const int64_t vis = (Skv + BN - 1) / BN;
   const int64_t tiles = (int64_t)B * Hkv * (((int64_t)n * (Hq / Hkv) + BM - 1) / BM);
   if (tiles < 64) return plan_qsparse(B, Hq, Hkv, n, vis, D, 1024, 16);
-  return plan_qsparse(B, Hq, Hkv, n, vis, D, DA_ROWS_ITEMS, 56);
+  return plan_qsparse(B, Hq, Hkv, n, vis, D, DA_ROWS_ITEMS, DA_ROWS_MIN_TILES);
 }
 
 // Split plan for n rows of which about n_live hold keys (the others are -1
