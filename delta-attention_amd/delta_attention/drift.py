@@ -19,11 +19,22 @@ def drift_summary(dense_sparse_diff, layer_idx: int, gamma: int, seq_len: int) -
     The cosines and the histogram come from one kernel pass over the delta
     buffer (ops.anchor_delta_cos); the mean and quantiles are taken over the
     [b, n-1, h] cosines."""
-    import torch
+    return drift_summary_of(*drift_cosines(dense_sparse_diff), layer_idx, gamma, seq_len)
 
+
+def drift_cosines(dense_sparse_diff):
+    """The device half of drift_summary: the [b, n-1, h] cosines and their
+    histogram, launched on the current stream, nothing read back."""
     from . import ops
 
-    cos, hist = ops.anchor_delta_cos(dense_sparse_diff, hist_bins=HIST_BINS, hist_range=HIST_RANGE)
+    return ops.anchor_delta_cos(dense_sparse_diff, hist_bins=HIST_BINS, hist_range=HIST_RANGE)
+
+
+def drift_summary_of(cos, hist, layer_idx: int, gamma: int, seq_len: int) -> Dict[str, Any]:
+    """The host half of drift_summary: the summary of drift_cosines' output
+    (one device sync)."""
+    import torch
+
     flat = cos.flatten()
     qs = torch.quantile(flat, torch.tensor([0.1, 0.5, 0.9], device=flat.device))
     mean, p10, p50, p90 = torch.cat((flat.mean()[None], qs)).tolist()   # one device sync

@@ -176,7 +176,32 @@ def _adaptive_stride_stats(logs, layer, s, s_p, adapt_chunk, window, sink):
     }
 
 
+class _LazyStats:
+    """An attribute that may be set to a zero-argument callable which builds
+    its value: the first read calls it and keeps the result. The layer stores
+    its telemetry this way, so that reading it back (a device sync) waits
+    until someone asks."""
+
+    def __set_name__(self, owner, name):
+        self.key = "_lazy" + name
+
+    def __get__(self, obj, objtype=None):
+        if obj is None:
+            return self
+        value = obj.__dict__.get(self.key)
+        if callable(value):
+            value = obj.__dict__[self.key] = value()
+        return value
+
+    def __set__(self, obj, value):
+        obj.__dict__[self.key] = value
+
+
 class LlamaAttention(nn.Module):
+    # telemetry of the last prefill, read back on first access: the drift
+    # summary (log_drift) and the adaptive stride's statistics
+    _drift_stats = _LazyStats()
+    _stride_stats = _LazyStats()
 
     def __init__(self, config, layer_idx: int):
         super().__init__()
@@ -279,12 +304,17 @@ class LlamaAttention(nn.Module):
         if q.dtype == torch.float32:
             q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
         log_drift = bool(getattr(cfg, "log_drift", False)) and mode == "delta"
-        out, delta = ops.delta_prefill(q, k, v, gamma=lambd, window=window, sink=self._sink(),
-                                       sm_scale=float(scaling), mode=mode, return_delta=True)
-        if log_drift and delta is not None and delta.shape[1] >= 2:
-            from .drift import drift_summary
+        out = ops.delta_prefill(q, k, v, gamma=lambd, window=window, sink=self._sink(),
+                                sm_scale=float(scaling), mode=mode, return_delta=log_drift)
+        delta = None
+        if log_drift:
+            out, delta = out
+        if delta is not None and delta.shape[1] >= 2:
+            from .drift import drift_cosines, drift_summary_of
 
-            self._drift_stats = drift_summary(delta, self.layer_idx, lambd, s)
+            # the cosines are launched now; the summary is read back on first access
+            self._drift_stats = functools.partial(drift_summary_of, *drift_cosines(delta),
+                                                  int(self.layer_idx), lambd, s)
         if out.dtype != original_dtype:
             out = out.to(original_dtype)
         return out, None
@@ -342,18 +372,6 @@ class LlamaAttention(nn.Module):
             int(cfg.sliding_window), self._sink())
         return out.to(query_states.dtype)
 
-    @property
-    def _stride_stats(self):
-        """The last adaptive pass's stride statistics (a dict), built from its
-        device logs on first access (the one read-back of the pass)."""
-        rec = self.__dict__.get("_stride_record")
-        if callable(rec):
-            rec = self.__dict__["_stride_record"] = rec()
-        return rec
-
-    @_stride_stats.setter
-    def _stride_stats(self, value):
-        self.__dict__["_stride_record"] = value
 
     def _side_stream(self, device):
         """A second stream (default priority) for the adaptive path's row-chunked
