@@ -179,6 +179,18 @@ def test_wrapper_construction_and_drift_log(tmp_path, monkeypatch):
     assert at[1]._drift_stats is None and at[0]._dec_drift_points is None
     w._flush_drift_stats()
     assert len(log.read_text().splitlines()) == 3
+    # a layer stores its summary as a deferred call (no device read inside the
+    # layer); the first read runs it once and keeps the value
+    calls = []
+    at[1]._drift_stats = lambda: calls.append(1) or {"layer": 1, "cos": 0.5}
+    assert calls == []
+    assert at[1]._drift_stats == {"layer": 1, "cos": 0.5}
+    assert at[1]._drift_stats["cos"] == 0.5 and calls == [1]
+    at[0]._stride_stats = lambda: {"layer": 0, "gamma": 16}
+    w._flush_drift_stats()
+    lines = [json.loads(x) for x in log.read_text().splitlines()][3:]
+    assert lines == [{"layer": 0, "gamma": 16}, {"layer": 1, "cos": 0.5}]
+    assert at[1]._drift_stats is None and at[0]._stride_stats is None
 
 
 _orig_init = sample.init_model
