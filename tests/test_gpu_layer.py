@@ -231,7 +231,12 @@ def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold
         assert float(cos.min()) == c["cos_min"]
 
 
-@pytest.mark.parametrize("B,s,chunk,gamma0,gmin,dtype", [
+def _with_heads(cases, H=8, Hkv=2, D=128):
+    """Pad (B, s, chunk, gamma0, gmin, dtype[, H, Hkv[, D]]) cases to full length."""
+    return [c + (H, Hkv, D)[len(c) - 6:] for c in cases]
+
+
+@pytest.mark.parametrize("B,s,chunk,gamma0,gmin,dtype,H,Hkv,D", _with_heads([
     (1, 4096, 512, 32, 8, torch.bfloat16), (1, 3000, 1024, 64, 16, torch.bfloat16),
     (1, 2500, 1000, 64, 16, torch.bfloat16),      # adapt_chunk not a multiple of gamma0
     # no rows ahead, and chunks of 63 and 125 anchors (more row tiles than the first chunk's 16)
@@ -240,8 +245,12 @@ def test_adaptive_device_decisions_follow_the_host_rules(gpu, trigger, threshold
     (1, 1000, 2048, 64, 16, torch.bfloat16),      # one chunk, shorter than adapt_chunk
     (1, 2600, 256, 128, 16, torch.bfloat16),      # starting stride 128: chunks of 2 anchors
     (1, 1500, 96, 16, 4, torch.bfloat16),         # many short chunks, strides down to 4
-    (1, 2048, 512, 32, 16, torch.float16), (2, 1800, 600, 64, 16, torch.float16)])
-def test_adaptive_layer_composition_is_exact(gpu, B, s, chunk, gamma0, gmin, dtype):
+    (1, 2048, 512, 32, 16, torch.float16), (2, 1800, 600, 64, 16, torch.float16),
+    # head layouts other than 8 / 2 at head_dim 128: five query heads per KV
+    # head (a row tile holds 25.6 query rows), one, and head_dim 64
+    (1, 3000, 512, 32, 8, torch.bfloat16, 10, 2), (1, 2200, 1024, 64, 16, torch.bfloat16, 4, 4),
+    (1, 2600, 512, 32, 8, torch.bfloat16, 8, 2, 64)]))
+def test_adaptive_layer_composition_is_exact(gpu, B, s, chunk, gamma0, gmin, dtype, H, Hkv, D):
     """The one-call adaptive layer (da_adapt_layer_fwd) against the same
     steps issued one by one: the key-sparse pass over all rows; each chunk's
     dense anchor rows from the same kernel (2) launch as inside, i.e. when
@@ -254,10 +263,10 @@ def test_adaptive_layer_composition_is_exact(gpu, B, s, chunk, gamma0, gmin, dty
     the row ranges of the sparse pass and the tail scatter change no bits."""
     from delta_attention import ops
     from delta_attention.llama import LlamaAttention
-    window, sink, H, Hkv = 256, 16, 8, 2
-    scale = 128 ** -0.5
-    q, k, v = gen_qkv(B, H, Hkv, s, 128, seed=21 + B, dtype=dtype)
-    cfg = _cfg(H, Hkv, 128, stride_policy="adaptive", adapt_chunk=chunk, delta_lambda=gamma0,
+    window, sink = 256, 16
+    scale = D ** -0.5
+    q, k, v = gen_qkv(B, H, Hkv, s, D, seed=21 + B, dtype=dtype)
+    cfg = _cfg(H, Hkv, D, stride_policy="adaptive", adapt_chunk=chunk, delta_lambda=gamma0,
                adapt_threshold=0.97, gamma_min=gmin, gamma_max=128, sliding_window=window,
                sink_tokens=sink)
     m = LlamaAttention(cfg, layer_idx=0).cuda().to(dtype)
