@@ -16,7 +16,6 @@ pipeline knobs of `config.PIPELINE_FIELDS`.
 
 from __future__ import annotations
 
-import functools
 from typing import Optional, Tuple
 
 import torch
@@ -197,6 +196,21 @@ class _LazyStats:
         obj.__dict__[self.key] = value
 
 
+def _deferred(fn, *args, device=None):
+    """A zero-argument call of fn(*args) that runs on the stream current now
+    (the one that produced the device values fn reads back), whatever stream
+    is current when it is finally called."""
+    stream = torch.cuda.current_stream(device) if device is not None and device.type == "cuda" else None
+
+    def call():
+        if stream is None:
+            return fn(*args)
+        with torch.cuda.stream(stream):
+            return fn(*args)
+
+    return call
+
+
 class LlamaAttention(nn.Module):
     # telemetry of the last prefill, read back on first access: the drift
     # summary (log_drift) and the adaptive stride's statistics
@@ -313,8 +327,8 @@ class LlamaAttention(nn.Module):
             from .drift import drift_cosines, drift_summary_of
 
             # the cosines are launched now; the summary is read back on first access
-            self._drift_stats = functools.partial(drift_summary_of, *drift_cosines(delta),
-                                                  int(self.layer_idx), lambd, s)
+            self._drift_stats = _deferred(drift_summary_of, *drift_cosines(delta),
+                                          int(self.layer_idx), lambd, s, device=delta.device)
         if out.dtype != original_dtype:
             out = out.to(original_dtype)
         return out, None
@@ -367,9 +381,9 @@ class LlamaAttention(nn.Module):
             threshold=float(cfg.adapt_threshold), margin=ADAPT_MARGIN,
             k_sd=float(getattr(cfg, "adapt_k", 2.0)),
             side_stream=self._side_stream(device) if overlap else None)
-        self._stride_stats = functools.partial(
+        self._stride_stats = _deferred(
             _adaptive_stride_stats, logs, int(self.layer_idx), int(s), int(s_p), adapt_chunk,
-            int(cfg.sliding_window), self._sink())
+            int(cfg.sliding_window), self._sink(), device=device)
         return out.to(query_states.dtype)
 
 

@@ -116,6 +116,29 @@ def test_module_delta_forward_matches_ops(gpu):
     assert anchor_exactness_check(m, gamma=64, window=256, s=2048) > 0.999
 
 
+def test_module_drift_stats_read_from_another_stream(gpu):
+    """The layer leaves its drift summary as a deferred read on the stream it
+    ran on: a layer run on a side stream and read from the default stream
+    gives the summary of the same deltas computed in one go."""
+    from delta_attention import ops
+    from delta_attention.drift import drift_summary
+    from delta_attention.llama import LlamaAttention
+    cfg = _cfg(8, 2, 128, log_drift=True)
+    m = LlamaAttention(cfg, layer_idx=3).cuda().to(torch.bfloat16)
+    q, k, v = gen_qkv(1, 8, 2, 4096, 128, seed=9, model_layout=True)
+    _, delta = ops.delta_prefill(q, k, v, gamma=64, window=256, sink=16, sm_scale=m.scaling,
+                                 return_delta=True)
+    want = drift_summary(delta, 3, 64, 4096)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        m.delta_forward(m, q, k, v, None, scaling=m.scaling)
+    got = m._drift_stats
+    assert got == want
+    assert m._drift_stats is got     # read back once, then kept
+    torch.cuda.current_stream().wait_stream(side)
+
+
 def test_module_forward_and_qwen3(gpu):
     from delta_attention.llama import LlamaAttention, rope_cos_sin
     from delta_attention.qwen3 import Qwen3DeltaAttention
