@@ -30,6 +30,11 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMAs the compiler emits keep their accumulators in VGPRs also in the
+    # one-wave-per-SIMD kernels (their default there is the AGPR form, whose
+    # score tiles the softmax would have to copy out); the accumulators meant
+    # for AGPRs are placed there by inline asm
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -9,15 +9,20 @@
 //                                    merged by qsparse_merge_kernel, which also
 //                                    runs the output / delta / dense epilogues.
 //
-// Tiling (one workgroup = 4 waves = 256 threads, two workgroups per CU):
-//   * M tile: BM = 128 flattened (query row, head-in-group) pairs. The G
-//     query heads that share one key/value head are packed into the same
-//     tile, so K/V tiles are read once per group (no repeat_kv copies).
-//   * Each wave owns 32 flattened rows. Scores are formed transposed,
-//     S^T = K * Q^T, with v_mfma_f32_32x32x16 (A = 32 keys x 16 dims from LDS,
-//     B = Q^T fragment kept in registers). In the 32x32 accumulator layout a
-//     lane holds one query row (lane % 32) and 16 of its keys, so the softmax
-//     row max/sum is in-lane plus one permlane32 swap.
+// Tiling (one workgroup = 4 waves = 256 threads):
+//   * M tile: BM flattened (query row, head-in-group) pairs. The G query heads
+//     that share one key/value head are packed into the same tile, so K/V
+//     tiles are read once per group (no repeat_kv copies).
+//   * Each wave owns RG groups of 32 flattened rows. RG = 2 at head_dim 128
+//     (64 rows per wave, BM = 256, one workgroup and one wave per SIMD per CU):
+//     every K and V fragment read from LDS feeds one MFMA per row group, half
+//     the LDS bytes per MFMA of RG = 1 (32 rows per wave, BM = 128, two
+//     workgroups per CU), which the other head dims and the decode rows use.
+//   * Scores are formed transposed, S^T = K * Q^T, with v_mfma_f32_32x32x16
+//     (A = 32 keys x 16 dims from LDS, B = Q^T fragment kept in registers). In
+//     the 32x32 accumulator layout a lane holds one query row (lane % 32) of
+//     each row group and 16 of its keys, so the softmax row max/sum is in-lane
+//     plus one permlane32 swap.
 //   * O^T = V^T * P^T: the probabilities leave the score accumulator directly
 //     as the B operand, and the O^T accumulator again keeps one query row per
 //     lane, so the online-softmax rescale is a per-lane scalar.
@@ -31,67 +36,74 @@
 //     its V^T A-fragments come from transposed reads (ds_read_b64_tr_b16).
 //   * Softmax: one FMA + exp2 per score, row sum by v_dot2 over the packed P.
 //     Lazy rescale: the running max only moves when a row's tile max exceeds
-//     it by more than 40 (log2 domain). The first pass over the tiles takes
-//     no per-tile row max once every row has its first max; a row sum above
-//     2^39 (a max that would have moved) sends the workgroup through a second,
-//     exact pass, whose bits equal the first pass's for every other row.
-//   * Per key tile, 32 MFMAs in one scheduling region keep the matrix pipe
-//     fed: the exponentials of tile t run under the score MFMAs of tile t+1,
-//     then the PV MFMAs of tile t follow with their V reads running ahead.
-//     In the key-sparse modes that region runs at raised wave priority.
+//     it by more than a bound (log2 domain: 40 for bf16, 15 for fp16, whose
+//     packed probabilities must stay below 65504). The first pass over the
+//     tiles takes no per-tile row max once every row has its first max; a row
+//     sum above half of 2^bound (a max that would have moved) sends the
+//     workgroup through a second, exact pass, whose bits equal the first
+//     pass's for every other row.
+//   * Per key tile, one scheduling region keeps the matrix pipe fed: the
+//     exponentials of tile t run under the score MFMAs of tile t+1, then the
+//     PV MFMAs of tile t follow with their V reads running ahead.
 #include <mutex>
 #include <type_traits>
 
 #include "device_common.h"
+#include "agpr_tiles.h"
 #include "capi_common.h"
 
 namespace da {
 
-// Build options for controlled experiments (defaults measured fastest):
-// DA_SCHED=1 pins the interleave of MFMAs, LDS fragment reads and VALU work
-// in the key-tile loop with scheduling-group barriers (0: compiler order,
-// 1.5-2 % faster). DA_WAVES=8 makes one 8-wave workgroup per CU share every
-// K/V tile (half the DMA per MFMA); 4-wave workgroups, two per CU, measured
-// faster: the two waves on a SIMD then belong to different workgroups and
-// are not held at the same barrier.
-#ifndef DA_SCHED
-#define DA_SCHED 0
-#endif
-#ifndef DA_WAVES
-#define DA_WAVES 4
-#endif
 // Split items a selected-rows launch aims for.
 #ifndef DA_ROWS_ITEMS
 #define DA_ROWS_ITEMS 8192
 #endif
-// Split items a decode-row launch aims for: one workgroup per resident slot
-// of the 256-CU gfx950 (two per CU), so the items run in a single round
-// (dense row over 131072 keys: 106-111 us against 118 us at 1024 items and
-// 131 us at 2048).
 // Shortest split item of a selected-rows launch, in key tiles (binding on
 // short launches such as 638 rows at 32K: 40 / 48 / 56 / 64 / 80 tiles ->
 // kernel (2) 0.255 / 0.258 / 0.243 / 0.254 / 0.260 ms).
 #ifndef DA_ROWS_MIN_TILES
 #define DA_ROWS_MIN_TILES 56
 #endif
+// Split items a decode-row launch aims for: one workgroup per resident slot
+// of the 256-CU gfx950 (two per CU), so the items run in a single round
+// (dense row over 131072 keys: 106-111 us against 118 us at 1024 items and
+// 131 us at 2048).
 #ifndef DA_DECODE_ITEMS
 #define DA_DECODE_ITEMS 512
 #endif
-constexpr int NWAVE = DA_WAVES;
-static_assert(NWAVE == 4 || NWAVE == 8, "4 or 8 waves per workgroup");
+// Row groups per wave of the head_dim-128 key-sparse launches and of the
+// selected-rows launches (1 or 2).
+#ifndef DA_RG_SPARSE
+#define DA_RG_SPARSE 2
+#endif
+#ifndef DA_RG_ROWS
+#define DA_RG_ROWS 1
+#endif
+constexpr int NWAVE = 4;
 constexpr int NTHR = 64 * NWAVE;
-constexpr int BM = 32 * NWAVE;       // flattened (row, head) pairs per workgroup
 constexpr int BN = 64;               // keys per tile
 constexpr int NH = BN / 32;          // 32-key halves per tile
 constexpr int MTHR = 256;            // threads of the split-merge kernel
 constexpr int NSTAGE = 2;            // LDS stages for K and for V
+constexpr int BM_MAX = 32 * NWAVE * 2;
+constexpr int bm_of(int rg) { return 32 * NWAVE * rg; }   // flattened (row, head) pairs per workgroup
+constexpr float NEG_BIG = -1.0e30f;  // finite "minus infinity" for the running max
+
 // Lazy-rescale bound (log2 domain): a row's running max moves only when a
-// tile's max exceeds it by more than this, so P <= 2^40 and l <= 2^40 * keys.
-// The same bound on a row's sum tells the tile loop that ran without row
-// maxima that no row needed a move (P <= l).
-constexpr float RESCALE_THRESH = 40.0f;
-constexpr float RESCALE_LSUM = 1099511627776.0f;   // 2^RESCALE_THRESH
-constexpr float NEG_BIG = -1.0e30f;      // finite "minus infinity" for the running max
+// tile's max exceeds it by more than `thresh`, so P <= 2^thresh and
+// l <= 2^thresh * keys. A row sum above lsum / 2 tells the tile loop that ran
+// without row maxima that a max would have moved (P <= l). The probabilities
+// are packed into the element type for the PV product: fp16 holds at most
+// 65504, so its bound is 15.
+template <typename T> struct Rescale;
+template <> struct Rescale<__bf16> {
+  static constexpr float thresh = 40.0f;
+  static constexpr float lsum = 1099511627776.0f;   // 2^40
+};
+template <> struct Rescale<_Float16> {
+  static constexpr float thresh = 15.0f;
+  static constexpr float lsum = 32768.0f;           // 2^15
+};
 
 // MODE_FUSED is MODE_SPARSE with the delta broadcast-add in its epilogue.
 enum { MODE_SPARSE = 0, MODE_QSPARSE = 1, MODE_FUSED = 2 };
@@ -110,7 +122,8 @@ struct AttnArgs {
   int n_rows;       // query rows per (batch, head)
   int n_q;          // rows of q (selected rows index into it)
   int n_kv;         // keys
-  int n_mtiles;     // ceil(n_rows * G / BM)
+  int bm;           // flattened (row, head) pairs per workgroup: bm_of(RG) of the launch
+  int n_mtiles;     // ceil(n_rows * G / bm)
   int n_items;      // work items before padding the grid to a multiple of 8
   float scale_log2; // sm_scale * log2(e)
   int window, sink, q_block;
@@ -128,9 +141,9 @@ struct AttnArgs {
   // [0, n_rows]) are computed; the items of their row tiles are spread over
   // the XCDs in contiguous ranges and the other blocks exit at once
   const int* n_rows_dev;
-  uint32_t* part_o; // [item][ws_rows][D / 2]: bf16 pairs of each row's O / l
+  uint32_t* part_o; // [item][ws_rows][D / 2]: element pairs of each row's O / l
   float* part_ml;   // [item][2][ws_rows]  (running max, row sum)
-  int ws_rows;      // workspace rows per item: min(BM, n_rows * G) (a tile's valid rows)
+  int ws_rows;      // workspace rows per item: min(bm, n_rows * G) (a tile's valid rows)
   // MODE_FUSED: dense anchor rows [B, n_anchor, Hq, D] (strides batch, head,
   // anchor), optional delta output (same layout), stride and rows < s_p
   const void* dsel;
@@ -142,9 +155,9 @@ struct AttnArgs {
   // scaled scores, +inf for a row without visible keys), for the backward
   float* lse;
   // divisions by the launch's fixed divisors: n_hs, n_mtiles, n_splits, Hkv,
-  // Gs (heads per row tile), q_block, gamma
+  // Gs (heads per tile), q_block, gamma
   FastDiv fd_hs, fd_mt, fd_sp, fd_hkv, fd_gt, fd_qb, fd_gamma;
-  int tile_rows;    // BM / Gs: query rows per row tile
+  int tile_rows;    // bm / Gs: query rows per row tile
   int n_grp;        // MODE_FUSED: stride groups per row tile (tile_rows / gamma)
 };
 
@@ -202,23 +215,28 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Scheduling-group barrier masks (LLVM AMDGPU IGroupLP).
-enum : int { SG_VALU = 0x2, SG_MFMA = 0x8, SG_DS_READ = 0x100 };
+// Workgroups per CU: two at 32 rows per wave and head_dim <= 128; one at 64
+// rows per wave (a wave's accumulators, scores and Q fragments take most of a
+// SIMD's 512 registers) and at head_dim 256 (whose K/V stages take 128 KB).
+constexpr int attn_occupancy(int D, int RG) { return (D > 128 || RG > 1) ? 1 : 2; }
 
-// Workgroups per CU: two at head_dim <= 128; one at 256, whose accumulator
-// and fragments need a whole SIMD's registers and whose K/V stages take 128 KB.
-constexpr int attn_occupancy(int D) { return D > 128 ? 1 : 2; }
-
-template <typename T, int D, int MODE>
-__global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnArgs a) {
+template <typename T, int D, int MODE, int RG>
+__global__ __launch_bounds__(NTHR, attn_occupancy(D, RG)) void attn_fwd_kernel(AttnArgs a) {
   using TL = Tile<D>;
   constexpr int DCH = TL::DCH;
   constexpr int RB = TL::RB;
+  constexpr int BMK = bm_of(RG);
   constexpr int NDS = D / 16;                // MFMA k-steps of K.Q^T
   constexpr int NDT = D / 32;                // 32-row tiles of O^T
-  constexpr int NQK = NDS * NH;              // MFMAs per score tile
-  [[maybe_unused]] constexpr int NPV = 2 * NH * NDT;   // MFMAs per PV tile
+  constexpr int NQK = NDS * NH;              // K fragments per score tile
   constexpr int NDMA = TL::BYTES / (NTHR * 16);   // 16-byte DMA chunks per thread per K (or V) tile
+  constexpr float THRESH = Rescale<T>::thresh;
+  constexpr float LSUM = Rescale<T>::lsum;
+  // 64 rows per wave: O lives in the reserved AGPR tiles of agpr_tiles.h
+  // (tile NDT * rg + dt), accumulated, scaled and read by asm only; the score
+  // MFMAs, whose results the softmax reads, stay compiler-built in VGPRs
+  constexpr bool AGPR_O = RG > 1;
+  static_assert(!AGPR_O || RG * NDT <= 8, "eight reserved accumulator tiles");
   using E = Elt<T>;
 
   // [stage][K, V][tile bytes]
@@ -247,7 +265,7 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     // a contiguous range of them (the row tiles of one split share its
     // key/value chunk in that XCD's L2); blocks past the range exit
     const int n_live = min(max(*a.n_rows_dev, 0), a.n_rows);
-    const int mt_live = (int)(((int64_t)n_live * a.G + BM - 1) / BM);
+    const int mt_live = (int)(((int64_t)n_live * a.G + BMK - 1) / BMK);
     const int total = a.B * a.Hkv * a.n_splits * mt_live;
     const int per = (total + 7) >> 3;
     if (mt_live == 0 || (int)(blockIdx.x >> 3) >= per) return;
@@ -283,31 +301,37 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   const int GT = KSPARSE ? a.Gs : G;   // heads packed in this row tile
   const int n_kv = (KSPARSE || !a.n_kv_dev) ? a.n_kv : min(max(*a.n_kv_dev, 1), a.n_kv);
   // Fused epilogue: a tile wholly in the dense tail writes nothing. The other
-  // tiles keep the row grouping of the plain launch (the wave-wide rescale
-  // decisions, hence the rounded results, are the same).
+  // tiles keep the row grouping of the plain launch (the per-row rescale
+  // decisions make the rounded results independent of it anyway).
   if (MODE == MODE_FUSED && mt * a.tile_rows >= a.s_p) return;
 
-  // ---- this lane's (query row, head): flattened pair mt * BM + 32 * wave + ln
-  //      of the tile's GT heads hk * G + hs * GT + (0 .. GT-1) ----
-  const int mflat = mt * BM + wave * 32 + ln;
-  const bool valid = mflat < a.n_rows * GT;
-  const int mq = (int)fdiv(mflat, a.fd_gt);
-  const int irow = (KSPARSE ? a.row0 : 0) + (valid ? mq : 0);
-  const int hin = valid ? (int)fmodq(mflat, mq, a.fd_gt) : 0;   // head within the tile
-  const int hrow = hk * G + hs * GT + hin;
-  int qrow, lo, hi;
-  if (KSPARSE) {
-    qrow = irow;
-    hi = valid ? irow : -1;
-    lo = (int)fdiv(irow, a.fd_qb) * a.q_block + a.q_block - a.window;
-  } else {
-    // row_last == NULL: every row sees all keys (a decode row at the end of
-    // the cache); window > 0: the row sees sinks + its last `window` keys
-    qrow = a.q_rows ? (int)min(max(a.q_rows[irow], (int64_t)0), (int64_t)(a.n_q - 1)) : irow;
-    int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + irow] : (int64_t)n_kv - 1;
-    if (lim > n_kv - 1) lim = n_kv - 1;
-    hi = valid ? (int)(lim < -1 ? -1 : lim) : -1;
-    lo = a.window > 0 ? hi - a.window + 1 : 0;
+  // ---- this lane's (query row, head) of row group rg: flattened pair
+  //      mt * BMK + 32 * (RG * wave + rg) + ln of the tile's GT heads
+  //      hk * G + hs * GT + (0 .. GT-1) ----
+  bool valid[RG];
+  int irow[RG], hin[RG], hrow[RG], qrow[RG], lo[RG], hi[RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    const int mflat = mt * BMK + (RG * wave + rg) * 32 + ln;
+    valid[rg] = mflat < a.n_rows * GT;
+    const int mq = (int)fdiv(mflat, a.fd_gt);
+    irow[rg] = (KSPARSE ? a.row0 : 0) + (valid[rg] ? mq : 0);
+    hin[rg] = valid[rg] ? (int)fmodq(mflat, mq, a.fd_gt) : 0;   // head within the tile
+    hrow[rg] = hk * G + hs * GT + hin[rg];
+    if (KSPARSE) {
+      qrow[rg] = irow[rg];
+      hi[rg] = valid[rg] ? irow[rg] : -1;
+      lo[rg] = (int)fdiv(irow[rg], a.fd_qb) * a.q_block + a.q_block - a.window;
+    } else {
+      // row_last == NULL: every row sees all keys (a decode row at the end of
+      // the cache); window > 0: the row sees sinks + its last `window` keys
+      qrow[rg] = a.q_rows ? (int)min(max(a.q_rows[irow[rg]], (int64_t)0), (int64_t)(a.n_q - 1))
+                          : irow[rg];
+      int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + irow[rg]] : (int64_t)n_kv - 1;
+      if (lim > n_kv - 1) lim = n_kv - 1;
+      hi[rg] = valid[rg] ? (int)(lim < -1 ? -1 : lim) : -1;
+      lo[rg] = a.window > 0 ? hi[rg] - a.window + 1 : 0;
+    }
   }
   const int sink = (KSPARSE || a.window > 0) ? a.sink : 0;
   constexpr size_t esz = sizeof(T);
@@ -317,20 +341,34 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   //      the query-sparse mode loads them once the item is known not to be
   //      past the end of its tile's list (about half of the split items at
   //      long causal row lists), still ahead of the first K/V wait ----
-  u32x4 qf[NDS];
-  auto load_q = [&]() {
-    const char* qp = (const char*)a.q +
-                     ((int64_t)b * a.qs_b + (int64_t)hrow * a.qs_h + (int64_t)qrow * a.qs_s) * esz;
+  u32x4 qf[RG][NDS];
+  auto load_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds)
-      qf[ds] = valid ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
+    for (int rg = 0; rg < RG; ++rg) {
+      const char* qp = (const char*)a.q + ((int64_t)b * a.qs_b + (int64_t)hrow[rg] * a.qs_h +
+                                           (int64_t)qrow[rg] * a.qs_s) * esz;
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds)
+        qf[rg][ds] = valid[rg] ? *(const u32x4*)(qp + (16 * ds + 8 * lg) * esz) : (u32x4){0, 0, 0, 0};
+    }
+  };
+  // 64 rows per wave: the Q fragments stay in AGPRs, from which the score
+  // MFMAs read their B operand directly (the VGPRs hold the two score tiles,
+  // the packed probabilities and the addressing)
+  auto pin_q = [&]() __attribute__((always_inline)) {
+    if constexpr (RG > 1) {
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) asm volatile("" : "+a"(qf[rg][ds]));
+    }
   };
   if constexpr (KSPARSE) load_q();
 
   // ---- tile-wide bounds over the valid rows ----
   int hi_min, hi_max, lo_min, lo_max;
   if (KSPARSE) {
-    // the tile holds rows r0 .. r1 (BM / GT of them, the last tile fewer);
+    // the tile holds rows r0 .. r1 (BMK / GT of them, the last tile fewer);
     // hi = row and lo grow with the row
     const int r0 = a.row0 + mt * a.tile_rows;
     const int r1 = min(r0 + a.tile_rows, a.row0 + a.n_rows) - 1;
@@ -339,8 +377,14 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     lo_min = (int)fdiv(r0, a.fd_qb) * a.q_block + a.q_block - a.window;
     lo_max = (int)fdiv(r1, a.fd_qb) * a.q_block + a.q_block - a.window;
   } else {
-    int v_hmin = valid ? hi : 0x7fffffff, v_hmax = valid ? hi : -1;
-    int v_lmin = valid ? lo : 0x7fffffff, v_lmax = valid ? lo : (int)0x80000000;
+    int v_hmin = 0x7fffffff, v_hmax = -1, v_lmin = 0x7fffffff, v_lmax = (int)0x80000000;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      v_hmin = min(v_hmin, valid[rg] ? hi[rg] : 0x7fffffff);
+      v_hmax = max(v_hmax, valid[rg] ? hi[rg] : -1);
+      v_lmin = min(v_lmin, valid[rg] ? lo[rg] : 0x7fffffff);
+      v_lmax = max(v_lmax, valid[rg] ? lo[rg] : (int)0x80000000);
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       v_hmin = min(v_hmin, __shfl_xor(v_hmin, off));
@@ -397,25 +441,25 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     koff[c] = (uint32_t)row * krow_b + (uint32_t)((pc ^ TL::kswz(row)) * 16);
     voff[c] = (uint32_t)row * vrow_b + (uint32_t)((pc ^ TL::vswz(row)) * 16);
   }
-  auto tile_n0 = [&](int t) -> int {
+  auto tile_n0 = [&](int t) __attribute__((always_inline)) -> int {
     const int u = t + t_off;
     return (u < n_first ? u : second_t0 + (u - n_first)) * BN;
   };
   // DMA of key tile t into LDS stage `slot` (K) / (V); the buffer covers the
   // rows from the tile start to the last key (n0 <= hi_max < n_kv), so the
   // hardware range check zero-fills keys past the end
-  auto tile_rsrc = [&](const char* base, uint64_t end, uint32_t row_b, int t) {
+  auto tile_rsrc = [&](const char* base, uint64_t end, uint32_t row_b, int t) __attribute__((always_inline)) {
     const uint64_t p = (uint64_t)base + (uint64_t)(uint32_t)tile_n0(t) * row_b;
     const uint64_t rem = end - p;
     return make_rsrc((const void*)p, (rem >> 32) ? 0xffffffffu : (uint32_t)rem);
   };
-  auto issue_k = [&](int t, int slot) {
+  auto issue_k = [&](int t, int slot) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase, kend, krow_b, t);
 #pragma unroll
     for (int c = 0; c < NDMA; ++c)
       dma16(rk, (DA_LDS void*)(&smem[slot][0][(c * NWAVE + wave) * 1024]), koff[c]);
   };
-  auto issue_v = [&](int t, int slot) {
+  auto issue_v = [&](int t, int slot) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase, vend, vrow_b, t);
 #pragma unroll
     for (int c = 0; c < NDMA; ++c)
@@ -443,44 +487,49 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     }
   }
 
-  f32x16 acc[NDT];
-  float m_i, l_i;
+  f32x16 acc[RG][NDT];
+  float m_i[RG], l_i[RG];
   // First pass: a wave takes row maxima only while one of its rows has no
   // reference max yet and can still see keys.
   bool track = true;
   const float c2 = a.scale_log2;
   const DA_LDS char* lds0 = (const DA_LDS char*)&smem[0][0][0];
 
-  // S^T = K(stage) Q^T into x (raw scores): x[hf] holds keys 32 hf .. 32 hf + 31
-  // of the tile. MFMA q uses k-step q / NH of half q % NH, so consecutive
-  // MFMAs alternate between the two accumulators.
-  auto qk = [&](int stage, f32x16 (&x)[NH]) {
+  // S^T = K(stage) Q^T into x (raw scores): x[rg][hf] holds keys 32 hf ..
+  // 32 hf + 31 of the tile for row group rg. K fragment q (k-step q / NH of
+  // half q % NH) is read once and feeds the MFMA of every row group.
+  auto qk = [&](int stage, f32x16 (&x)[RG][NH]) __attribute__((always_inline)) {
     const DA_LDS char* ks = lds0 + stage * (2 * TL::BYTES);
 #pragma unroll
-    for (int hf = 0; hf < NH; ++hf)
+    for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) x[hf][j] = 0.f;
+      for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) x[rg][hf][j] = 0.f;
 #pragma unroll
     for (int q = 0; q < NQK; ++q) {
       const int ds = q / NH, hf = q % NH;
       const u32x4 ka = *(const DA_LDS u32x4*)(ks + kread[ds] + 32 * hf * RB);
-      x[hf] = E::mfma(ka, qf[ds], x[hf]);
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) x[rg][hf] = E::mfma(ka, qf[rg][ds], x[rg][hf]);
     }
   };
   // mask of tile t: element j of half hf is key n0 + 32 hf + 16 (j / 8) + 8 lg + j % 8
-  auto mask = [&](int t, f32x16 (&x)[NH]) {
+  auto mask = [&](int t, f32x16 (&x)[RG][NH]) __attribute__((always_inline)) {
     const int n0 = tile_n0(t);
     const int n1 = n0 + BN - 1;
     const bool full = (n1 <= hi_min) && (n1 < n_kv) && (n1 < sink || n0 >= lo_max);
     if (!full) {
 #pragma unroll
-      for (int hf = 0; hf < NH; ++hf)
+      for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = n0 + 32 * hf + 16 * (j >> 3) + 8 * lg + (j & 7);
-          const bool vis = key <= hi && (key < sink || key >= lo);
-          x[hf][j] = vis ? x[hf][j] : -INFINITY;
-        }
+        for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int key = n0 + 32 * hf + 16 * (j >> 3) + 8 * lg + (j & 7);
+            const bool vis = key <= hi[rg] && (key < sink || key >= lo[rg]);
+            x[rg][hf][j] = vis ? x[rg][hf][j] : -INFINITY;
+          }
     }
   };
   // scaled row max of a score tile: four independent chains, then one
@@ -488,7 +537,7 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   // IEEE `maximum` (v_maximum3_f32) instead of fmaxf: fmaxf must quiet
   // signalling NaNs first, one extra v_max per chain start on the MFMA
   // results; scores hold no NaN, where the two agree.
-  auto rowmax = [&](const f32x16 (&x)[NH]) -> float {
+  auto rowmax = [&](const f32x16 (&x)[NH]) __attribute__((always_inline)) -> float {
     float p[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -504,29 +553,47 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     swap32(mx, s0, s1);
     return __builtin_elementwise_maximum(s0, s1) * c2;   // scaling by c2 > 0 keeps the max
   };
-  // lazy online-softmax update with the scaled tile max: a row's running max
-  // moves (and its O, l are rescaled) only when its tile max exceeds it by
-  // more than RESCALE_THRESH (log2 domain). The decision is per row (the other
-  // rows of the wave multiply by exactly 1), so a row's result does not depend
-  // on which rows share its wave: every head packing and row grouping gives
-  // the same bits.
-  auto update = [&](float mx) {
-    const bool up = mx > m_i + RESCALE_THRESH;
-    if (__any(up)) {
-      const float alpha = up ? fast_exp2(m_i - mx) : 1.f;
-      m_i = up ? mx : m_i;
-      l_i *= alpha;
+  // lazy online-softmax update of every row group with its scaled tile max:
+  // a row's running max moves (and its O, l are rescaled) only when its tile
+  // max exceeds it by more than THRESH (log2 domain). The decision is per row
+  // (the other rows of the wave multiply by exactly 1), so a row's result does
+  // not depend on which rows share its wave: every head packing and row
+  // grouping gives the same bits.
+  auto update = [&](const f32x16 (&x)[RG][NH]) __attribute__((always_inline)) {
+    StaticFor<0, RG>::run([&](auto rg_c) __attribute__((always_inline)) {
+      constexpr int rg = decltype(rg_c)::value;
+      const float mx = rowmax(x[rg]);
+      const bool up = mx > m_i[rg] + THRESH;
+      // a row without a max yet has O = 0 and l = 0: it only takes the max
+      const bool first = m_i[rg] == NEG_BIG;
+      if (__any(up && first)) m_i[rg] = up && first ? mx : m_i[rg];
+      if (__any(up && !first)) {
+        const float alpha = up ? fast_exp2(m_i[rg] - mx) : 1.f;
+        m_i[rg] = up ? mx : m_i[rg];
+        l_i[rg] *= alpha;
+        if constexpr (AGPR_O) {
+          ot_pad();
+          StaticFor<0, NDT>::run([&](auto dt_c) __attribute__((always_inline)) {
+            ot_scale<NDT * rg + decltype(dt_c)::value>(alpha);
+          });
+        } else {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+          for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[dt][j] *= alpha;
-    }
+            for (int j = 0; j < 16; ++j) acc[rg][dt][j] *= alpha;
+        }
+      }
+    });
   };
   // Whether a row of this wave has no reference max yet (nothing visible in
   // the tiles so far) but can still see a key from tile t on: the list runs
   // through increasing keys, and a row sees no key above `hi`.
-  auto pending = [&](int t) -> bool {
-    return __any(valid && m_i == NEG_BIG && hi >= tile_n0(t));
+  auto pending = [&](int t) __attribute__((always_inline)) -> bool {
+    const int n0 = tile_n0(t);
+    bool p = false;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) p = p || (valid[rg] && m_i[rg] == NEG_BIG && hi[rg] >= n0);
+    return __any(p);
   };
 
   // Step t. On entry: S(t) (masked) is in `cur` and the running max covers it;
@@ -541,69 +608,153 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   //   Then S(t+1) is masked (boundary tiles only), its max taken (overlapping
   //   the PV MFMAs still in the pipe) and the running max moved if needed,
   //   when `track` is set; wait for the DMA, barrier.
-  auto step = [&](int t, auto last_tag, auto exact_tag, f32x16 (&cur)[NH], f32x16 (&nxt)[NH]) __attribute__((always_inline)) {
+  auto step = [&](int t, auto last_tag, auto exact_tag, f32x16 (&cur)[RG][NH],
+                  f32x16 (&nxt)[RG][NH]) __attribute__((always_inline)) {
     constexpr bool LAST = decltype(last_tag)::value;   // t == nt - 1
     constexpr bool EXACT = decltype(exact_tag)::value;
-    // Key-sparse modes: the wave runs its MFMA block (exponentials, score
-    // MFMAs, PV MFMAs) at raised priority and drops it for the mask, row max,
-    // DMA wait and barrier, so that the other wave on the SIMD fills those
-    // phases instead of competing for issue while this one's MFMAs are ready
-    // (kernel (1) 0.9-1.3 % faster; the query-sparse mode measured neutral
-    // to slower and keeps one priority).
-    if constexpr (KSPARSE) __builtin_amdgcn_s_setprio(1);
+    // Key-sparse modes with two waves per SIMD: the wave runs its MFMA block
+    // (exponentials, score MFMAs, PV MFMAs) at raised priority and drops it
+    // for the mask, row max, DMA wait and barrier, so that the other wave on
+    // the SIMD fills those phases instead of competing for issue while this
+    // one's MFMAs are ready (kernel (1) 0.9-1.3 % faster; the query-sparse
+    // mode measured neutral to slower and keeps one priority).
+    constexpr bool PRIO = KSPARSE && RG == 1;
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
     const int P = t & 1;
     if (t + 2 < nt) issue_k(t + 2, P);
     if (t + 1 < nt) issue_v(t + 1, P ^ 1);
 
-    uint32_t pk[8 * NH];
-    const float nm = -m_i;
-#pragma unroll
-    for (int hf = 0; hf < NH; ++hf)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        pk[8 * hf + j] = E::pack2(fast_exp2(fmaf(cur[hf][2 * j], c2, nm)),
-                                  fast_exp2(fmaf(cur[hf][2 * j + 1], c2, nm)));
-#pragma unroll
-    for (int j = 0; j < 8 * NH; ++j) l_i = E::add_pair(pk[j], l_i);
-    if (!LAST) qk(P ^ 1, nxt);
-
+    uint32_t pk[RG][8 * NH];
     const DA_LDS char* vs = lds0 + TL::BYTES + P * (2 * TL::BYTES);
+    // V^T fragment (kk, dt): keys 16 kk .. 16 kk + 15, d-rows 32 dt .. 32 dt + 31
+    auto vfrag = [&](int kk, int dt) __attribute__((always_inline)) -> u32x4 {
+      const u32x2 v0 = read_tr16(vs + vread[dt] + (16 * kk) * RB);
+      const u32x2 v1 = read_tr16(vs + vread[dt] + (16 * kk + 4) * RB);
+      return (u32x4){v0[0], v0[1], v1[0], v1[1]};
+    };
+    if constexpr (RG > 1) {
+      // One wave per SIMD: nothing else on the SIMD hides the softmax or the
+      // latencies of its dependent chain (FMA -> exp -> pack -> dot2), so the
+      // step is one static software-pipelined schedule of NSL = 64 slots, one
+      // MFMA each: slots 0..31 the score MFMAs of S(t+1) (K fragment s / 2,
+      // row group s % 2; none in the last step), slots 32..63 the PV MFMAs
+      // (fragment f = (s - 32) / 2 = NDT kk + dt, row group s % 2). The 64
+      // score elements per lane of S(t), in the order the PV MFMAs consume
+      // their pairs (e = 2 p + i, pair p = 8 kk + 4 rg + jj), have their
+      // exponential in slot xs(e) = 54 e / 64, the FMA one slot earlier, the
+      // pack one slot after the pair's second exponential and the row-sum dot2
+      // two slots after that; a pair is packed at least two slots before its
+      // first PV MFMA (the asm MFMAs' 2 wait states after a VALU write). K
+      // and V fragment reads run two fragments (four slots) ahead. Scheduling
+      // barriers between slots keep this order.
+      constexpr int NSL = 64, XS = 54;
+      static_assert(NQK * RG == 32 && 2 * NH * NDT * RG == 32 && RG * NH * 16 == 64,
+                    "64 MFMA slots and 64 score elements per lane");
+      // element e -> (rg, hf, index within the half)
+      auto erg = [](int e) constexpr { return ((e / 2) / 4) % 2; };
+      auto ehf = [](int e) constexpr { return ((e / 2) / 8) / 2; };
+      auto ej = [](int e) constexpr { return 2 * (4 * (((e / 2) / 8) % 2) + (e / 2) % 4) + e % 2; };
+      const DA_LDS char* ks = lds0 + (P ^ 1) * (2 * TL::BYTES);
+      auto kfrag = [&](int q) __attribute__((always_inline)) -> u32x4 {
+        return *(const DA_LDS u32x4*)(ks + kread[q / NH] + 32 * (q % NH) * RB);
+      };
+      u32x4 kq[3], vq[3];
+      float fv[64], xv[64];
+      if (!LAST) {
 #pragma unroll
-    for (int kk = 0; kk < 2 * NH; ++kk) {
-      const u32x4 pf = {pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]};
+        for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const u32x2 v0 = read_tr16(vs + vread[dt] + (16 * kk) * RB);
-        const u32x2 v1 = read_tr16(vs + vread[dt] + (16 * kk + 4) * RB);
-        const u32x4 va = {v0[0], v0[1], v1[0], v1[1]};
-        acc[dt] = E::mfma(va, pf, acc[dt]);
+          for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+            for (int jx = 0; jx < 16; ++jx) nxt[rg][hf][jx] = 0.f;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // first element whose exponential is in slot x (xs is monotonic)
+      auto e_lo = [](int x) constexpr { return (64 * x + XS - 1) / XS; };
+      StaticFor<0, NSL + 1>::run([&](auto i_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(i_c)::value - 1;
+        // fragment reads for the MFMAs four slots on
+        if constexpr (sl >= -1 && sl <= 2 * (NQK - 1) - 4) {
+          if (!LAST) {
+            if constexpr (sl == -1) {
+              kq[0] = kfrag(0);
+              kq[1] = kfrag(1);
+            } else if constexpr (sl % 2 == 0) {
+              kq[((sl + 4) / 2) % 3] = kfrag((sl + 4) / 2);
+            }
+          }
+        }
+        if constexpr (sl >= 28 && sl % 2 == 0 && (sl - 28) / 2 < 2 * NH * NDT) {
+          constexpr int f = (sl - 28) / 2;
+          vq[f % 3] = vfrag(f / NDT, f % NDT);
+        }
+        // this slot's MFMA
+        if constexpr (sl >= 0 && sl < 32) {
+          if (!LAST) {
+            constexpr int q = sl / 2, rg = sl % 2;
+            nxt[rg][q % NH] = E::mfma(kq[q % 3], qf[rg][q / NH], nxt[rg][q % NH]);
+          }
+        } else if constexpr (sl >= 32) {
+          constexpr int f = (sl - 32) / 2, rg = sl % 2, kk = f / NDT, dt = f % NDT;
+          const u32x4 pf = {pk[rg][4 * kk], pk[rg][4 * kk + 1], pk[rg][4 * kk + 2],
+                            pk[rg][4 * kk + 3]};
+          ot_mfma<T, NDT * rg + dt>(vq[f % 3], pf);
+        }
+        // this slot's softmax work: FMAs of the elements exponentiated in the
+        // next slot (slot -1 also those of slot 0), exponentials, packs of the
+        // pairs completed in the previous slot, dot2s three slots after
+        constexpr int f0 = sl == -1 ? 0 : e_lo(sl + 1), f1 = sl + 2 <= XS ? e_lo(sl + 2) : 64;
+#pragma unroll
+        for (int e = f0; e < f1; ++e) fv[e] = fmaf(cur[erg(e)][ehf(e)][ej(e)], c2, -m_i[erg(e)]);
+        if constexpr (sl >= 0 && sl < XS) {
+#pragma unroll
+          for (int e = e_lo(sl); e < e_lo(sl + 1); ++e) xv[e] = fast_exp2(fv[e]);
+        }
+        if constexpr (sl >= 1 && sl <= XS) {
+#pragma unroll
+          for (int e = e_lo(sl - 1) | 1; e < e_lo(sl); e += 2)
+            pk[erg(e)][8 * ehf(e) + ej(e) / 2] = E::pack2(xv[e - 1], xv[e]);
+        }
+        if constexpr (sl >= 3 && sl <= XS + 2) {
+#pragma unroll
+          for (int e = e_lo(sl - 3) | 1; e < e_lo(sl - 2); e += 2)
+            l_i[erg(e)] = E::add_pair(pk[erg(e)][8 * ehf(e) + ej(e) / 2], l_i[erg(e)]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    } else {
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) {
+        const float nm = -m_i[rg];
+#pragma unroll
+        for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+          for (int jx = 0; jx < 8; ++jx)
+            pk[rg][8 * hf + jx] = E::pack2(fast_exp2(fmaf(cur[rg][hf][2 * jx], c2, nm)),
+                                           fast_exp2(fmaf(cur[rg][hf][2 * jx + 1], c2, nm)));
+#pragma unroll
+        for (int jx = 0; jx < 8 * NH; ++jx) l_i[rg] = E::add_pair(pk[rg][jx], l_i[rg]);
+      }
+      if (!LAST) qk(P ^ 1, nxt);
+#pragma unroll
+      for (int kk = 0; kk < 2 * NH; ++kk) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const u32x4 va = vfrag(kk, dt);
+#pragma unroll
+          for (int rg = 0; rg < RG; ++rg) {
+            const u32x4 pf = {pk[rg][4 * kk], pk[rg][4 * kk + 1], pk[rg][4 * kk + 2],
+                              pk[rg][4 * kk + 3]};
+            acc[rg][dt] = E::mfma(va, pf, acc[rg][dt]);
+          }
+        }
       }
     }
-    if constexpr (KSPARSE) __builtin_amdgcn_s_setprio(0);
-#if DA_SCHED
-    if (!LAST) {
-      // phase A: K reads run 3 MFMAs ahead, ~6 of the 96 softmax VALU ops
-      // under each score MFMA
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 3, 0);
-#pragma unroll
-      for (int q = 0; q < NQK; ++q) {
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-        if (q + 3 < NQK) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_VALU, 6, 0);
-      }
-    }
-    // phase B: V reads run 2 MFMAs ahead (2 transposed reads per MFMA)
-    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 0);
-#pragma unroll
-    for (int q = 0; q < NPV; ++q) {
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      if (q + 2 < NPV) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
-    }
-#endif
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     if (!LAST) {
       mask(t + 1, nxt);
       if (EXACT || track) {
-        update(rowmax(nxt));
+        update(nxt);
         if (!EXACT) track = pending(t + 2);
       }
       // K(t+2) and V(t+1) must have landed (nothing younger is in flight)
@@ -621,7 +772,6 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     pre = n_grp * GT * D * (int)esz <= DPRE_BYTES;
     if (pre) {
       const int g0 = mt * n_grp;
-      static_assert(NWAVE == 4, "dpre holds one block per wave");
       const int slot = (lane / DCH) * NWAVE + wave, ch = lane % DCH;
       const int gl = (int)fdiv(slot, a.fd_gt), hl = (int)fmodq(slot, gl, a.fd_gt);
       const int64_t span = ((int64_t)(a.n_anchor - 1) * a.dsel_a + (int64_t)(a.Hq - 1) * a.dsel_h + D) * esz;
@@ -636,27 +786,39 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
   }
 
   // Two passes at most. Every row's reference max is its first visible tile's
-  // max; it moves only by more than RESCALE_THRESH. The first pass takes row
-  // maxima only while a row lacks its reference (in the key-sparse modes with
-  // sinks, the first tile sets every row's), which keeps the max reduction
-  // off the per-tile path between the PV products and the barrier. A row
-  // whose max would have moved has a tile probability above
-  // 2^(RESCALE_THRESH - 1), hence a larger partial sum; if any row of the
-  // workgroup shows one (or a non-finite sum), all its tiles run again with
-  // every row max taken. Rows whose max never moves go through identical
-  // operations in both passes, so each row's bits are those of the exact
-  // pass whichever rows share its workgroup.
-  f32x16 sa[NH], sb[NH];
+  // max; it moves only by more than THRESH. The first pass takes row maxima
+  // only while a row lacks its reference (in the key-sparse modes with sinks,
+  // the first tile sets every row's), which keeps the max reduction off the
+  // per-tile path between the PV products and the barrier. A row whose max
+  // would have moved has a tile probability above 2^(THRESH - 1), hence a
+  // larger partial sum; if any row of the workgroup shows one (or a
+  // non-finite sum), all its tiles run again with every row max taken. Rows
+  // whose max never moves go through identical operations in both passes, so
+  // each row's bits are those of the exact pass whichever rows share its
+  // workgroup.
+  f32x16 sa[RG][NH], sb[RG][NH];
   using NotLast = std::integral_constant<bool, false>;
   using Last = std::integral_constant<bool, true>;
   auto run = [&](auto exact_tag) __attribute__((always_inline)) {
     constexpr bool EXACT = decltype(exact_tag)::value;
+    if constexpr (AGPR_O) {
+      ot_pad();
+      StaticFor<0, RG * NDT>::run([&](auto i_c) __attribute__((always_inline)) {
+        ot_zero<decltype(i_c)::value>();
+      });
+    } else {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+      for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
-    m_i = NEG_BIG;
-    l_i = 0.f;
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[rg][dt][j] = 0.f;
+    }
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      m_i[rg] = NEG_BIG;
+      l_i[rg] = 0.f;
+    }
     if (nt > 0) {
       // prologue: K(0), V(0), K(1); S(0) and its running max
       issue_k(0, 0);
@@ -664,9 +826,12 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
       if (nt > 1) issue_k(1, 1);
       wait_vmcnt<0>();
       __syncthreads();
+      // (64 rows per wave) Q into AGPRs only now, so that the prologue waits
+      // for the Q loads and the first DMAs at once
+      pin_q();
       qk(0, sa);
       mask(0, sa);
-      update(rowmax(sa));
+      update(sa);
       if (!EXACT) track = pending(1);
       __syncthreads();   // every wave is done with K stage 0 before it is refilled
     }
@@ -690,15 +855,27 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     run(std::false_type());
     // the barrier inside also orders the first pass's last LDS reads before
     // the second pass refills the stages
-    if (__syncthreads_or(valid && !(l_i <= 0.5f * RESCALE_LSUM))) run(std::true_type());
+    bool big = false;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) big = big || (valid[rg] && !(l_i[rg] <= 0.5f * LSUM));
+    if (__syncthreads_or(big)) run(std::true_type());
   }
 
   // ---- epilogue ----
+  if constexpr (AGPR_O) {
+    ot_pad();
+    StaticFor<0, RG>::run([&](auto rg_c) __attribute__((always_inline)) {
+      StaticFor<0, NDT>::run([&](auto dt_c) __attribute__((always_inline)) {
+        constexpr int rg = decltype(rg_c)::value, dt = decltype(dt_c)::value;
+        acc[rg][dt] = ot_read<NDT * rg + dt>();
+      });
+    });
+  }
   // Row stores of 16 bytes: lanes l and l + 32 hold dims 8 jq + 0..3 and
   // + 4..7 of the same row; one permlane32 swap per register pair gives lane
   // l dims 8 (2p) + 0..7 and lane l + 32 dims 8 (2p + 1) + 0..7, so each
   // store instruction writes 32 rows x 32 bytes instead of 32 rows x 16.
-  auto store_rows16 = [&](char* op, u32x2 (&o)[NDT][4]) {
+  auto store_rows16 = [&](char* op, u32x2 (&o)[NDT][4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -715,115 +892,134 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
         *(u32x4*)(op + (32 * dt + 16 * p2 + 8 * lg) * esz) = v;
       }
   };
-  const float l_tot = sum32(l_i);
+  float l_tot[RG], inv[RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    l_tot[rg] = sum32(l_i[rg]);
+    inv[rg] = l_tot[rg] > 0.f ? 1.f / l_tot[rg] : 0.f;
+  }
   if (MODE == MODE_FUSED) {
     // out[r] = rnd(rnd(sparse[r]) + delta[r / gamma]) for rows r < s_p, with
     // delta[g] = rnd(dense[g] - rnd(sparse[g * gamma])) formed by the anchor
     // row's lanes (gamma divides the tile height, so every group of the tile
     // has its anchor in it) and shared through LDS. Rows >= s_p are not
     // written: they hold the dense tail.
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    u32x2 sp[NDT][4];
+    u32x2 sp[RG][NDT][4];
+    bool rlive[RG];
+    int ga[RG];
+    DA_LDS u32x2* dl[RG];
+    DA_LDS u32x2* dn_pre[RG];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int rg = 0; rg < RG; ++rg) {
 #pragma unroll
-      for (int jq = 0; jq < 4; ++jq) {
-        sp[dt][jq][0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
-        sp[dt][jq][1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
-      }
-    const bool live = valid && irow < a.s_p;
-    const int ga = (int)fdiv(irow, a.fd_gamma);      // this row's stride group
-    const int gl = ga - mt * a.n_grp;                // its group within the tile (gamma
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          sp[rg][dt][jq][0] = E::pack2(acc[rg][dt][4 * jq + 0] * inv[rg], acc[rg][dt][4 * jq + 1] * inv[rg]);
+          sp[rg][dt][jq][1] = E::pack2(acc[rg][dt][4 * jq + 2] * inv[rg], acc[rg][dt][4 * jq + 3] * inv[rg]);
+        }
+      rlive[rg] = valid[rg] && irow[rg] < a.s_p;
+      ga[rg] = (int)fdiv(irow[rg], a.fd_gamma);      // this row's stride group
+      const int gl = ga[rg] - mt * a.n_grp;          // its group within the tile (gamma
                                                      // divides the tile's rows)
-    // delta rows in LDS. With the dense rows prefetched (dpre, [group][head][D]),
-    // each anchor lane writes its delta elements to the padded slots of dlt,
-    // so one barrier suffices. Otherwise they go to the K/V stage memory
-    // ([group][head][lg][D/2]) once every wave is done with it.
-    DA_LDS u32x2* dl;
-    DA_LDS u32x2* dn_pre = nullptr;
-    if (pre) {
-      static_assert(DLT_BYTES >= DPRE_BYTES + (DPRE_BYTES / (2 * 32)) * DPAD, "padded slots fit");
-      {
-        const int ps = gl * GT + hin;      // this row's dpre slot
-        dn_pre = (DA_LDS u32x2*)&dpre[(ps % NWAVE) * DPRE_BLOCK + (ps / NWAVE) * RB] + lg;
+      // delta rows in LDS. With the dense rows prefetched (dpre,
+      // [group][head][D]), each anchor lane writes its delta elements to the
+      // padded slots of dlt, so one barrier suffices. Otherwise they go to the
+      // K/V stage memory ([group][head][lg][D/2]) once every wave is done with it.
+      if (pre) {
+        const int ps = gl * GT + hin[rg];      // this row's dpre slot
+        dn_pre[rg] = (DA_LDS u32x2*)&dpre[(ps % NWAVE) * DPRE_BLOCK + (ps / NWAVE) * RB] + lg;
+        dl[rg] = (DA_LDS u32x2*)&dlt[(gl * GT + hin[rg]) * (D * (int)esz + DPAD)] + lg;
+      } else {
+        dn_pre[rg] = nullptr;
+        dl[rg] = (DA_LDS u32x2*)&smem[0][0][0] + ((gl * GT + hin[rg]) * 2 + lg) * (NDT * 4);
       }
-      dl = (DA_LDS u32x2*)&dlt[(gl * GT + hin) * (D * (int)esz + DPAD)] + lg;
+    }
+    static_assert(DLT_BYTES >= DPRE_BYTES + (DPRE_BYTES / (2 * 32)) * DPAD, "padded slots fit");
+    static_assert(BM_MAX * 2 * D <= NSTAGE * 2 * TL::BYTES, "delta slots fit the stages");
+    if (pre) {
       if (nt == 0) {     // no key tile ran: make every wave's dpre DMA visible
         wait_vmcnt<0>();
         __syncthreads();
       }
     } else {
-      dl = (DA_LDS u32x2*)&smem[0][0][0] + ((gl * GT + hin) * 2 + lg) * (NDT * 4);
+      wait_vmcnt<0>();
       __syncthreads();   // every wave is done with the K/V stages
     }
     // element (dt, jq) of this lane: dims 32 dt + 8 jq + 4 lg .. +3. One code
     // path per delta layout (PRE: the prefetched dense rows), so that the
     // anchor lanes issue all their reads, then all their writes, instead of
     // one LDS round trip per element while the other waves wait.
-    auto fused_out = [&](auto pre_tag) {
+    auto fused_out = [&](auto pre_tag) __attribute__((always_inline)) {
       constexpr bool PRE = decltype(pre_tag)::value;
-      auto dslot = [&](int dt, int jq) -> DA_LDS u32x2* {
-        return PRE ? dl + 8 * dt + 2 * jq : dl + dt * 4 + jq;
+      auto dslot = [&](int rg, int dt, int jq) __attribute__((always_inline)) -> DA_LDS u32x2* {
+        return PRE ? dl[rg] + 8 * dt + 2 * jq : dl[rg] + dt * 4 + jq;
       };
-      if (live && irow == ga * a.gamma) {
-        const int64_t g = ga;
-        u32x2 dn[NDT][4];
-        if constexpr (PRE) {
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt)
+      for (int rg = 0; rg < RG; ++rg) {
+        if (rlive[rg] && irow[rg] == ga[rg] * a.gamma) {
+          const int64_t g = ga[rg];
+          u32x2 dn[NDT][4];
+          if constexpr (PRE) {
 #pragma unroll
-            for (int jq = 0; jq < 4; ++jq) dn[dt][jq] = dn_pre[8 * dt + 2 * jq];
-        } else {
-          const char* dp = (const char*)a.dsel +
-                           ((int64_t)b * a.dsel_b + (int64_t)hrow * a.dsel_h + g * a.dsel_a) * esz;
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt)
+              for (int jq = 0; jq < 4; ++jq) dn[dt][jq] = dn_pre[rg][8 * dt + 2 * jq];
+          } else {
+            const char* dp = (const char*)a.dsel +
+                             ((int64_t)b * a.dsel_b + (int64_t)hrow[rg] * a.dsel_h + g * a.dsel_a) * esz;
 #pragma unroll
-            for (int jq = 0; jq < 4; ++jq)
-              dn[dt][jq] = *(const u32x2*)(dp + (32 * dt + 8 * jq + 4 * lg) * esz);
-        }
-        u32x2 dv[NDT][4];
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-          for (int jq = 0; jq < 4; ++jq)
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-              dv[dt][jq][e] = E::pack2(E::lo(dn[dt][jq][e]) - E::lo(sp[dt][jq][e]),
-                                       E::hi(dn[dt][jq][e]) - E::hi(sp[dt][jq][e]));
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-          for (int jq = 0; jq < 4; ++jq) *dslot(dt, jq) = dv[dt][jq];
-        if (a.dout) {
-          char* op = (char*)a.dout +
-                     ((int64_t)b * a.dout_b + (int64_t)hrow * a.dout_h + g * a.dout_a) * esz;
+              for (int jq = 0; jq < 4; ++jq)
+                dn[dt][jq] = *(const u32x2*)(dp + (32 * dt + 8 * jq + 4 * lg) * esz);
+          }
+          u32x2 dv[NDT][4];
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int jq = 0; jq < 4; ++jq)
-              *(u32x2*)(op + (32 * dt + 8 * jq + 4 * lg) * esz) = dv[dt][jq];
+#pragma unroll
+              for (int e = 0; e < 2; ++e)
+                dv[dt][jq][e] = E::pack2(E::lo(dn[dt][jq][e]) - E::lo(sp[rg][dt][jq][e]),
+                                         E::hi(dn[dt][jq][e]) - E::hi(sp[rg][dt][jq][e]));
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) *dslot(rg, dt, jq) = dv[dt][jq];
+          if (a.dout) {
+            char* op = (char*)a.dout +
+                       ((int64_t)b * a.dout_b + (int64_t)hrow[rg] * a.dout_h + g * a.dout_a) * esz;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+              for (int jq = 0; jq < 4; ++jq)
+                *(u32x2*)(op + (32 * dt + 8 * jq + 4 * lg) * esz) = dv[dt][jq];
+          }
         }
       }
       __syncthreads();
-      if (live) {
-        char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
-                                 (int64_t)qrow * a.os_s) * esz;
-        u32x2 dv[NDT][4];
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+      for (int rg = 0; rg < RG; ++rg) {
+        if (rlive[rg]) {
+          char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow[rg] * a.os_h +
+                                   (int64_t)qrow[rg] * a.os_s) * esz;
+          u32x2 dv[NDT][4];
 #pragma unroll
-          for (int jq = 0; jq < 4; ++jq) dv[dt][jq] = *dslot(dt, jq);
-        u32x2 o[NDT][4];
+          for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+            for (int jq = 0; jq < 4; ++jq) dv[dt][jq] = *dslot(rg, dt, jq);
+          u32x2 o[NDT][4];
 #pragma unroll
-          for (int jq = 0; jq < 4; ++jq)
+          for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-            for (int e = 0; e < 2; ++e)
-              o[dt][jq][e] = E::pack2(E::lo(sp[dt][jq][e]) + E::lo(dv[dt][jq][e]),
-                                      E::hi(sp[dt][jq][e]) + E::hi(dv[dt][jq][e]));
-        store_rows16(op, o);
+            for (int jq = 0; jq < 4; ++jq)
+#pragma unroll
+              for (int e = 0; e < 2; ++e)
+                o[dt][jq][e] = E::pack2(E::lo(sp[rg][dt][jq][e]) + E::lo(dv[dt][jq][e]),
+                                        E::hi(sp[rg][dt][jq][e]) + E::hi(dv[dt][jq][e]));
+          store_rows16(op, o);
+        }
       }
     };
     if (pre) fused_out(std::true_type());
@@ -831,54 +1027,58 @@ __global__ __launch_bounds__(NTHR, attn_occupancy(D)) void attn_fwd_kernel(AttnA
     return;
   }
   if (MODE == MODE_SPARSE) {
-    if (!valid) return;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (a.lse && lg == 0)
-      a.lse[((int64_t)b * a.Hq + hrow) * a.n_rows + irow] =
-          l_tot > 0.f ? m_i + __builtin_log2f(l_tot) : INFINITY;
-    char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow * a.os_h +
-                             (int64_t)qrow * a.os_s) * esz;
-    u32x2 o[NDT][4];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int rg = 0; rg < RG; ++rg) {
+      if (!valid[rg]) continue;
+      if (a.lse && lg == 0)
+        a.lse[((int64_t)b * a.Hq + hrow[rg]) * a.n_rows + irow[rg]] =
+            l_tot[rg] > 0.f ? m_i[rg] + __builtin_log2f(l_tot[rg]) : INFINITY;
+      char* op = (char*)a.o + ((int64_t)b * a.os_b + (int64_t)hrow[rg] * a.os_h +
+                               (int64_t)qrow[rg] * a.os_s) * esz;
+      u32x2 o[NDT][4];
 #pragma unroll
-      for (int jq = 0; jq < 4; ++jq) {
-        o[dt][jq][0] = E::pack2(acc[dt][4 * jq + 0] * inv, acc[dt][4 * jq + 1] * inv);
-        o[dt][jq][1] = E::pack2(acc[dt][4 * jq + 2] * inv, acc[dt][4 * jq + 3] * inv);
-      }
-    store_rows16(op, o);
-  } else {
-    if (!valid) return;   // the merge reads the rows of the selection only
-    const int r = wave * 32 + ln;
-    // normalised split rows O / l in bf16, a 16-byte row piece per lane after
-    // one permlane32 swap (the merge reads them back once). At half the fp32
-    // volume, plain stores through L2 measured 0.5-1 % faster than
-    // non-temporal ones; with fp32 partials the non-temporal form had kept
-    // the shared key/value chunk in L2 (split-kernel fetch 1.78 -> 1.59 GB).
-    uint32_t* po = a.part_o + ((int64_t)w * a.ws_rows + r) * (D / 2);
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    using B16 = Elt<__bf16>;
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int p2 = 0; p2 < 2; ++p2) {
-        u32x2 x0, x1;
-        const int j0 = 2 * p2, j1 = 2 * p2 + 1;
-        x0[0] = B16::pack2(acc[dt][4 * j0 + 0] * inv, acc[dt][4 * j0 + 1] * inv);
-        x0[1] = B16::pack2(acc[dt][4 * j0 + 2] * inv, acc[dt][4 * j0 + 3] * inv);
-        x1[0] = B16::pack2(acc[dt][4 * j1 + 0] * inv, acc[dt][4 * j1 + 1] * inv);
-        x1[1] = B16::pack2(acc[dt][4 * j1 + 2] * inv, acc[dt][4 * j1 + 3] * inv);
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          auto sw = __builtin_amdgcn_permlane32_swap(x0[e], x1[e], false, false);
-          x0[e] = sw[0];
-          x1[e] = sw[1];
+        for (int jq = 0; jq < 4; ++jq) {
+          o[dt][jq][0] = E::pack2(acc[rg][dt][4 * jq + 0] * inv[rg], acc[rg][dt][4 * jq + 1] * inv[rg]);
+          o[dt][jq][1] = E::pack2(acc[rg][dt][4 * jq + 2] * inv[rg], acc[rg][dt][4 * jq + 3] * inv[rg]);
         }
-        *(u32x4*)(po + (32 * dt + 16 * p2 + 8 * lg) / 2) = (u32x4){x0[0], x0[1], x1[0], x1[1]};
+      store_rows16(op, o);
+    }
+  } else {
+    // normalised split rows O / l in the element type, a 16-byte row piece
+    // per lane after one permlane32 swap (the merge reads them back once).
+    // At half the fp32 volume, plain stores through L2 measured 0.5-1 %
+    // faster than non-temporal ones; with fp32 partials the non-temporal form
+    // had kept the shared key/value chunk in L2 (split-kernel fetch 1.78 ->
+    // 1.59 GB).
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      if (!valid[rg]) continue;   // the merge reads the rows of the selection only
+      const int r = (RG * wave + rg) * 32 + ln;
+      uint32_t* po = a.part_o + ((int64_t)w * a.ws_rows + r) * (D / 2);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int p2 = 0; p2 < 2; ++p2) {
+          u32x2 x0, x1;
+          const int j0 = 2 * p2, j1 = 2 * p2 + 1;
+          x0[0] = E::pack2(acc[rg][dt][4 * j0 + 0] * inv[rg], acc[rg][dt][4 * j0 + 1] * inv[rg]);
+          x0[1] = E::pack2(acc[rg][dt][4 * j0 + 2] * inv[rg], acc[rg][dt][4 * j0 + 3] * inv[rg]);
+          x1[0] = E::pack2(acc[rg][dt][4 * j1 + 0] * inv[rg], acc[rg][dt][4 * j1 + 1] * inv[rg]);
+          x1[1] = E::pack2(acc[rg][dt][4 * j1 + 2] * inv[rg], acc[rg][dt][4 * j1 + 3] * inv[rg]);
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            auto sw = __builtin_amdgcn_permlane32_swap(x0[e], x1[e], false, false);
+            x0[e] = sw[0];
+            x1[e] = sw[1];
+          }
+          *(u32x4*)(po + (32 * dt + 16 * p2 + 8 * lg) / 2) = (u32x4){x0[0], x0[1], x1[0], x1[1]};
+        }
+      if (lg == 0) {
+        a.part_ml[(int64_t)w * 2 * a.ws_rows + r] = m_i[rg];
+        a.part_ml[(int64_t)w * 2 * a.ws_rows + a.ws_rows + r] = l_tot[rg];
       }
-    if (lg == 0) {
-      a.part_ml[(int64_t)w * 2 * a.ws_rows + r] = m_i;
-      a.part_ml[(int64_t)w * 2 * a.ws_rows + a.ws_rows + r] = l_tot;
     }
   }
 }
@@ -900,9 +1100,10 @@ struct MergeArgs {
   int window, sink;
   int lanes;        // P: threads sharing one (row, 8-column) task, splits s = p mod P
   int wgs;          // workgroups per row tile
-  const uint32_t* part_o;   // bf16 pairs of O / l per split row
+  const uint32_t* part_o;   // element pairs of O / l per split row
   const float* part_ml;
   int ws_rows;      // as in AttnArgs
+  int bm;           // as in AttnArgs: flattened rows per row tile of the split launch
   int epi, n_anchor, n_q;
   void* o;
   int64_t os_b, os_h, os_s;
@@ -926,7 +1127,7 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   if (a.n_rows_dev) {
     // live row tiles of every (b, kv head) first, as the split items
     const int n_live = min(max(*a.n_rows_dev, 0), a.n_rows);
-    const int mt_live = (n_live * a.G + BM - 1) / BM;
+    const int mt_live = (n_live * a.G + a.bm - 1) / a.bm;
     if (mt_live == 0 || tile >= a.B * a.Hkv * mt_live) return;
     tile = (tile / mt_live) * a.n_mtiles + tile % mt_live;
   }
@@ -940,8 +1141,8 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
   // Same tile list as the split kernel saw, hence the same set of written splits.
   const int n_kv = a.n_kv_dev ? min(max(*a.n_kv_dev, 1), a.n_kv) : a.n_kv;
   int my_hmax = -1, my_lmin = 0x7fffffff;
-  if (tid < BM) {
-    const int mflat = mt * BM + tid;
+  if (tid < a.bm) {
+    const int mflat = mt * a.bm + tid;
     if (mflat < a.n_rows * G) {
       int64_t lim = a.row_last ? a.row_last[(int64_t)b * a.rl_b + mflat / G] : (int64_t)n_kv - 1;
       if (lim > n_kv - 1) lim = n_kv - 1;
@@ -974,9 +1175,9 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
     const int task = sub * (MTHR / P) + tid / P;
     const int r = task / CPR;
     const int c = task % CPR;
-    const int mflat = mt * BM + r;
+    const int mflat = mt * a.bm + r;
     // whole P-lane groups leave together (the shuffles stay inside a group)
-    if (r >= BM || mflat >= a.n_rows * G) return;
+    if (r >= a.bm || mflat >= a.n_rows * G) return;
     const int i = mflat / G;
     const int h = hk * G + mflat % G;
 
@@ -990,7 +1191,6 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    using B16 = Elt<__bf16>;
     for (int s = p; s < nsv; s += P) {
       const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
       // split weight exp2(m_s - M) l_s on the stored O_s / l_s
@@ -1000,8 +1200,8 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
       const u32x4 x = *(const u32x4*)(a.part_o + (w * a.ws_rows + r) * (D / 2) + 4 * c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        acc[2 * e] += sc * B16::lo(x[e]);
-        acc[2 * e + 1] += sc * B16::hi(x[e]);
+        acc[2 * e] += sc * E::lo(x[e]);
+        acc[2 * e + 1] += sc * E::hi(x[e]);
       }
     }
     for (int off = 1; off < P; off <<= 1) {
@@ -1060,17 +1260,30 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
 struct QsparsePlan {
   int n_mtiles, n_splits, chunk, n_items;
   int ws_rows;      // workspace rows per item: a tile's valid (row, head) pairs at most
+  int bm;           // flattened (row, head) pairs per row tile of the split launch
   size_t ws_bytes;
 };
+
+// Rows per workgroup of a launch: 64 rows per wave (bm 256) for the
+// head_dim-128 key-sparse launches and, when DA_RG_ROWS is 2, selected-rows
+// launches; 32 rows per wave (bm 128) for the other head dims and for decode
+// rows (one query row per batch).
+static int sparse_bm(int D) { return D == 128 ? bm_of(DA_RG_SPARSE) : bm_of(1); }
+static int rows_bm(int D) { return D == 128 ? bm_of(DA_RG_ROWS) : bm_of(1); }
+
+// Merge workgroups per row tile at most: bm rows x D / 8 column chunks x 16
+// lanes per task, 256 threads each.
+constexpr int64_t MERGE_WGS_MAX = (int64_t)BM_MAX * (256 / 8) * 16 / MTHR;
 
 // Split plan over the tile lists: `vis` bounds a row tile's list length, each
 // item takes `chunk` consecutive tiles of it (at least `min_chunk`); `target`
 // items in total.
 static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int D, int target,
-                                int min_chunk = 1) {
+                                int min_chunk, int bm) {
   QsparsePlan p;
   const int G = Hq / Hkv;
-  p.n_mtiles = (int)(((int64_t)n * G + BM - 1) / BM);
+  p.bm = bm;
+  p.n_mtiles = (int)(((int64_t)n * G + bm - 1) / bm);
   const int64_t base = (int64_t)B * Hkv * p.n_mtiles;
   if (vis < 1) vis = 1;
   int64_t want = (target + base - 1) / base;
@@ -1080,11 +1293,11 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
   if (p.chunk < min_chunk) p.chunk = (int)min((int64_t)min_chunk, vis);
   p.n_splits = (int)((vis + p.chunk - 1) / p.chunk);
   const int64_t items = base * p.n_splits;
-  // grids past 2^31 workgroups (split kernel, or merge at <= 128 per tile)
-  // are refused by the entry points (n_items = 0)
-  const bool fits = items <= 0x7fffff00LL && base * 128 <= 0x7fffff00LL;
+  // grids past 2^31 workgroups (split kernel or merge) are refused by the
+  // entry points (n_items = 0)
+  const bool fits = items <= 0x7fffff00LL && base * MERGE_WGS_MAX <= 0x7fffff00LL;
   p.n_items = fits ? (int)items : 0;
-  p.ws_rows = (int)min((int64_t)BM, (int64_t)n * G);
+  p.ws_rows = (int)min((int64_t)bm, (int64_t)n * G);
   p.ws_bytes = fits ? (size_t)p.n_items * p.ws_rows * (D * sizeof(uint16_t) + 2 * sizeof(float)) : 0;
   return p;
 }
@@ -1100,9 +1313,10 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
 // at least 16 tiles instead.
 static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
   const int64_t vis = (Skv + BN - 1) / BN;
-  const int64_t tiles = (int64_t)B * Hkv * (((int64_t)n * (Hq / Hkv) + BM - 1) / BM);
-  if (tiles < 64) return plan_qsparse(B, Hq, Hkv, n, vis, D, 1024, 16);
-  return plan_qsparse(B, Hq, Hkv, n, vis, D, DA_ROWS_ITEMS, DA_ROWS_MIN_TILES);
+  const int bm = rows_bm(D);
+  const int64_t tiles = (int64_t)B * Hkv * (((int64_t)n * (Hq / Hkv) + bm - 1) / bm);
+  if (tiles < 64) return plan_qsparse(B, Hq, Hkv, n, vis, D, 1024, 16, bm);
+  return plan_qsparse(B, Hq, Hkv, n, vis, D, DA_ROWS_ITEMS, DA_ROWS_MIN_TILES, bm);
 }
 
 // Split plan for n rows of which about n_live hold keys (the others are -1
@@ -1112,12 +1326,12 @@ static QsparsePlan plan_rows_live(int B, int Hq, int Hkv, int n, int n_live, int
   if (n_live >= n || n_live < 1) return plan_rows(B, Hq, Hkv, n, Skv, D);
   QsparsePlan p = plan_rows(B, Hq, Hkv, n_live, Skv, D);
   const int G = Hq / Hkv;
-  p.n_mtiles = (int)(((int64_t)n * G + BM - 1) / BM);
+  p.n_mtiles = (int)(((int64_t)n * G + p.bm - 1) / p.bm);
   const int64_t base = (int64_t)B * Hkv * p.n_mtiles;
   const int64_t items = base * p.n_splits;
-  const bool fits = p.n_items > 0 && items <= 0x7fffff00LL && base * 128 <= 0x7fffff00LL;
+  const bool fits = p.n_items > 0 && items <= 0x7fffff00LL && base * MERGE_WGS_MAX <= 0x7fffff00LL;
   p.n_items = fits ? (int)items : 0;
-  p.ws_rows = (int)min((int64_t)BM, (int64_t)n * G);
+  p.ws_rows = (int)min((int64_t)p.bm, (int64_t)n * G);
   p.ws_bytes = fits ? (size_t)p.n_items * p.ws_rows * (D * sizeof(uint16_t) + 2 * sizeof(float)) : 0;
   return p;
 }
@@ -1128,13 +1342,20 @@ static QsparsePlan plan_decode(int B, int Hq, int Hkv, int n_keys, int D, int wi
   const int64_t all = (n_keys + BN - 1) / BN;
   int64_t vis = all;
   if (window > 0) vis = min(all, (int64_t)(min(sink, n_keys) + BN - 1) / BN + (window + BN - 1) / BN + 1);
-  return plan_qsparse(B, Hq, Hkv, 1, vis, D, DA_DECODE_ITEMS);
+  return plan_qsparse(B, Hq, Hkv, 1, vis, D, DA_DECODE_ITEMS, 1, bm_of(1));
 }
 
 template <typename T, int D, int MODE>
 static void launch_attn(const AttnArgs& a, hipStream_t stream) {
   const int grid = (a.n_items + 7) / 8 * 8;
-  hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE>), dim3(grid), dim3(NTHR), 0, stream, a);
+  constexpr bool has_rg2 = D == 128 && (MODE != MODE_QSPARSE || DA_RG_ROWS == 2);
+  if constexpr (has_rg2) {
+    if (a.bm == bm_of(2)) {
+      hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE, 2>), dim3(grid), dim3(NTHR), 0, stream, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE, 1>), dim3(grid), dim3(NTHR), 0, stream, a);
 }
 
 template <int MODE>
@@ -1157,11 +1378,17 @@ static void launch_merge(const MergeArgs& m, int n_tiles, hipStream_t s) {
   hipLaunchKernelGGL((qsparse_merge_kernel<T, D>), dim3(n_tiles), dim3(MTHR), 0, s, m);
 }
 
-// Query heads per key-sparse row tile: two of an even GQA group (64-row
-// tiles), else one (128-row tiles), so that a stride group of up to 64 (128)
-// rows has its anchor in the tile. Sharing each K/V tile between fewer heads
-// measured free (the tiles of one row block read K/V from L2 back to back).
-static int tile_heads(int G) { return (G % 2 == 0) ? 2 : 1; }
+// Query heads per key-sparse row tile: bm / 64 heads (64-row tiles) when
+// they divide the GQA group, else half as many, down to one head (bm-row
+// tiles). Short tiles keep the window's tile list close to the keys each row
+// sees, and a stride group of up to 64 rows has its anchor in the tile.
+// Sharing each K/V tile between fewer heads measured free (the tiles of one
+// row block read K/V from L2 back to back).
+static int tile_heads(int G, int bm) {
+  int gs = bm / 64;
+  while (gs > 1 && G % gs != 0) gs /= 2;
+  return gs;
+}
 
 // Key/value row strides (elements) in [0, 2^23): row byte strides below 2^24.
 static bool kv_rows_ok(const int64_t k_str[3], const int64_t v_str[3]) {
@@ -1196,7 +1423,8 @@ static int sparse_args(AttnArgs& a, const void* q, const void* k, const void* v,
   a.os_b = o_str[0]; a.os_h = o_str[1]; a.os_s = o_str[2];
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv;
   a.n_rows = S; a.n_q = S; a.n_kv = S;
-  a.Gs = tile_heads(a.G); a.n_hs = a.G / a.Gs;
+  a.bm = sparse_bm(D);
+  a.Gs = tile_heads(a.G, a.bm); a.n_hs = a.G / a.Gs;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.window = window; a.sink = sink; a.q_block = q_block;
   a.fd_hkv = make_fastdiv(Hkv); a.fd_qb = make_fastdiv(q_block);
@@ -1206,11 +1434,11 @@ static int sparse_args(AttnArgs& a, const void* q, const void* k, const void* v,
 
 // Work items for rows [0, n_rows) of the argument block.
 static int sparse_items(AttnArgs& a) {
-  a.n_mtiles = (int)(((int64_t)a.n_rows * a.Gs + BM - 1) / BM);
+  a.n_mtiles = (int)(((int64_t)a.n_rows * a.Gs + a.bm - 1) / a.bm);
   const int64_t items = (int64_t)a.B * a.Hkv * a.n_hs * a.n_mtiles;
   if (items > 0x7fffff00LL) return DA_ERR_INVALID_ARG;
   a.n_items = (int)items;
-  a.tile_rows = BM / a.Gs;
+  a.tile_rows = a.bm / a.Gs;
   a.fd_hs = make_fastdiv(a.n_hs); a.fd_mt = make_fastdiv(a.n_mtiles);
   a.fd_gt = make_fastdiv(a.Gs);
   return DA_OK;
@@ -1273,7 +1501,7 @@ extern "C" int da_sparse_attn_fwd_lse(const void* q, const void* k, const void* 
 
 extern "C" int da_fused_delta_rows(int Hq, int Hkv) {
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return 0;
-  return BM;
+  return bm_of(1);   // every launch's rows per workgroup is a multiple of it
 }
 
 extern "C" int da_sparse_attn_delta_fwd(const void* q, const void* k, const void* v, void* out,
@@ -1303,9 +1531,11 @@ extern "C" int da_sparse_attn_delta_fwd(const void* q, const void* k, const void
   a.gamma = gamma; a.s_p = s_p; a.n_anchor = s_p / gamma;
   a.fd_gamma = make_fastdiv(gamma);
   // every stride group needs its anchor in the row tile: a gamma that does not
-  // divide the two-head tile height takes one head per 128-row tile (the
+  // divide the tile height takes tiles of fewer heads and more rows (the
   // per-row softmax makes the packing invisible in the results)
-  if ((BM / a.Gs) % gamma != 0) { a.Gs = 1; a.n_hs = a.G; }
+  while (a.Gs > 1 && (a.bm / a.Gs) % gamma != 0) a.Gs /= 2;
+  a.n_hs = a.G / a.Gs;
+  if (a.bm % gamma != 0) return DA_ERR_INVALID_ARG;
   if ((rc = sparse_items(a)) != DA_OK) return rc;
   a.n_grp = a.tile_rows / gamma;
   (void)hipGetLastError();
@@ -1336,9 +1566,10 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   a.vs_b = v_str[0]; a.vs_h = v_str[1]; a.vs_s = v_str[2];
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.Gs = a.G; a.n_hs = 1;
   a.n_rows = n; a.n_q = Sq; a.n_kv = Skv;
+  a.bm = p.bm;
   a.n_mtiles = p.n_mtiles;
   a.n_items = p.n_items;
-  a.tile_rows = BM / a.Gs;
+  a.tile_rows = a.bm / a.Gs;
   a.fd_hs = make_fastdiv(1); a.fd_mt = make_fastdiv(p.n_mtiles);
   a.fd_sp = make_fastdiv(p.n_splits); a.fd_hkv = make_fastdiv(Hkv);
   a.fd_gt = make_fastdiv(a.Gs); a.fd_qb = make_fastdiv(1); a.fd_gamma = make_fastdiv(1);
@@ -1362,10 +1593,10 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   m.lanes = 1;
   while (m.lanes < 16 && m.lanes * 4 < p.n_splits) m.lanes <<= 1;
   {
-    const int64_t rows = min((int64_t)BM, (int64_t)n * a.G);
+    const int64_t rows = min((int64_t)p.bm, (int64_t)n * a.G);
     m.wgs = (int)((rows * (D / 8) * m.lanes + MTHR - 1) / MTHR);
   }
-  m.part_o = a.part_o; m.part_ml = a.part_ml; m.ws_rows = p.ws_rows;
+  m.part_o = a.part_o; m.part_ml = a.part_ml; m.ws_rows = p.ws_rows; m.bm = p.bm;
   m.epi = epi; m.n_anchor = (epi == DA_EPI_DELTA || epi == DA_EPI_DENSE) ? n_anchor : 0;
   m.o = o; m.os_b = o_str[0]; m.os_h = o_str[1]; m.os_s = o_str[2];
   m.delta = delta;

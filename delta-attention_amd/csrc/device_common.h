@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace da {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -61,6 +63,16 @@ template <> struct Elt<_Float16> {
   }
 };
 
+// Separates VALU producers of MFMA operands from MFMAs written as inline asm,
+// which the compiler's hazard recognizer does not see: a VALU write of a
+// register needs 2 wait states before an MFMA reads it. Also a scheduling
+// barrier, so the producers cannot move past it.
+__device__ __forceinline__ void mfma_src_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 1");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Both halves of the wave exchange a value with the lane 32 away:
 // returns {x[l], x[l ^ 32]} in some order, so a symmetric combine of the
 // pair (max, +) gives the same answer on both lanes.
@@ -83,6 +95,20 @@ __device__ __forceinline__ float sum32(float x) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 #define DA_LDS __attribute__((address_space(3)))
+
+// f(std::integral_constant<int, I>) for I = B .. E-1, unrolled at compile
+// time (for indices that must be template arguments, e.g. register tiles)
+template <int B, int E>
+struct StaticFor {
+  template <typename F>
+  static __device__ __forceinline__ void run(F&& f) {
+    if constexpr (B < E) {
+      f(std::integral_constant<int, B>{});
+      StaticFor<B + 1, E>::run(f);
+    }
+  }
+};
+
 
 // Streaming (non-temporal) 16- and 8-byte global accesses for data touched
 // once. Used where every store instruction writes whole contiguous lines (the
