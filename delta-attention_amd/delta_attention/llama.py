@@ -461,15 +461,14 @@ class LlamaAttention(nn.Module):
 
     def delta_decode_forward(self, module, query_states, key_states, value_states,
                              scaling: float = 1.0, **kwargs):
-        """Decode step with sparse attention + cached delta correction
-        (llama.py:551-657). Per-layer state `_dec_state` = {last_delta, steps
-        since anchor, last_sparse, cos_hist}, reset for every new prompt.
-        Anchor when: no delta yet | fixed policy and steps >= gamma_dec | drift
-        policy and cos(sparse_t, sparse_{t-1}) < drift_threshold | drift_rel
-        and that cosine falls below mean - drift_k * std of the last 16 steps
-        (>= 8 of them) | steps >= gamma_dec_max. Anchors output the dense row
-        and refresh delta = dense - sparse; other steps output sparse + delta.
-        log_drift records per-step points in `_dec_drift_points`."""
+        """Decode step of the sparse / delta decode (semantics: llama.py:551-634).
+        `decode_policy.RefreshRule` decides whether this step is an anchor;
+        anchors output the dense row and keep dense - sparse in `_dec_state`,
+        the other steps output sparse + that correction (recorded decode steps
+        take `_delta_decode_recorded`, whose non-anchor steps add it in the
+        sparse row's launch). log_drift appends a record per step to
+        `_dec_drift_points`."""
+        from . import decode_policy as dp
         assert query_states.size(0) == 1, "sparse/delta decode supports batch size 1 only"
         mode = self.config.decode_mode
         assert mode in ("sparse", "delta"), mode
@@ -477,62 +476,27 @@ class LlamaAttention(nn.Module):
         if kwargs.get("n_keys") is not None:
             return self._delta_decode_recorded(q, k, v, scaling, kwargs["n_keys"],
                                                bool(kwargs.get("decode_anchor")), query_states.dtype)
-        sparse_out = self._decode_sparse_row(q, k, v, scaling)
+
+        def emit(x):
+            return x.transpose(1, 2).contiguous().to(query_states.dtype), None
+
         if mode == "sparse":
-            return sparse_out.transpose(1, 2).contiguous().to(query_states.dtype), None
-
-        st = getattr(self, "_dec_state", None) or {
-            "last_delta": None, "steps": 0, "last_sparse": None, "cos_hist": []}
-        log_drift = bool(getattr(self.config, "log_drift", False))
-        policy = getattr(self.config, "refresh_policy", "fixed")
-
-        def _cos(a, b):
-            return torch.nn.functional.cosine_similarity(
-                a.flatten().float(), b.flatten().float(), dim=0).item()
-
-        if st["last_delta"] is None:
-            anchor, cur = True, 0
-        else:
-            cur = st["steps"] + 1
-            anchor = cur >= int(getattr(self.config, "gamma_dec_max", 128))
-            if policy == "fixed" and cur >= int(self.config.gamma_dec):
-                anchor = True
-            if not anchor and policy in ("drift", "drift_rel") and st["last_sparse"] is not None:
-                c = _cos(sparse_out, st["last_sparse"])
-                if policy == "drift":
-                    anchor = c < float(self.config.drift_threshold)
-                else:
-                    hist = st["cos_hist"]
-                    if len(hist) >= 8:
-                        mu = sum(hist) / len(hist)
-                        sd = (sum((x - mu) ** 2 for x in hist) / len(hist)) ** 0.5
-                        anchor = c < mu - float(getattr(self.config, "drift_k", 2.0)) * sd
-                    hist.append(c)
-                    del hist[:-16]
-
-        dense_out = None
-        if anchor or log_drift:
-            dense_out = ops.decode_attention(q, k, v, window=0, sink=0, sm_scale=float(scaling))
-        if anchor:
-            st["last_delta"] = dense_out - sparse_out
-            st["steps"] = 0
-            out = dense_out
-        else:
-            out = sparse_out + st["last_delta"]
-            st["steps"] = cur
-        if log_drift:
-            true_delta = dense_out - sparse_out
+            return emit(self._decode_sparse_row(q, k, v, scaling))
+        state = getattr(self, "_dec_state", None) or dp.new_state()
+        rule = dp.RefreshRule.of(self.config)
+        logging = bool(getattr(self.config, "log_drift", False))
+        sparse = self._decode_sparse_row(q, k, v, scaling)
+        anchor, since = rule.decide(state, sparse)
+        dense = (ops.decode_attention(q, k, v, window=0, sink=0, sm_scale=float(scaling))
+                 if anchor or logging else None)
+        out = dense if anchor else sparse + state["last_delta"]
+        dp.commit(state, anchor, since, sparse, dense, out)
+        if logging:
             pts = getattr(self, "_dec_drift_points", None) or []
-            pts.append({
-                "steps_since_anchor": int(cur),
-                "anchor": bool(anchor),
-                "drift_cos": _cos(true_delta, st["last_delta"]),
-                "applied_vs_true_cos": _cos(out, dense_out),
-            })
+            pts.append(dp.drift_point(state, since, anchor, sparse, dense, out))
             self._dec_drift_points = pts
-        st["last_sparse"] = sparse_out
-        self._dec_state = st
-        return out.transpose(1, 2).contiguous().to(query_states.dtype), None
+        self._dec_state = state
+        return emit(out)
 
     # -- projections and dispatch -----------------------------------------------
     def _qkv(self, hidden_states, hidden_shape):

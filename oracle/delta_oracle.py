@@ -16,7 +16,12 @@ prefill (file:line cite the reference, singhh5050/delta-attention):
   apply_delta_variable   stride.py:26-40
   decode_row             llama.py:537-549 (_decode_sparse_row: sink + last window
                          keys of the cache) and the dense decode row of :598-600
-  delta_decode_steps     llama.py:551-657 (fixed-stride delta decode composition)
+  decode_anchor_flags    llama.py:578-604: when a delta decode step recomputes its
+                         dense row (fixed / drift / drift_rel policies and the
+                         gamma_dec_max guard), from the per-step cosines of
+                         consecutive sparse rows
+  delta_decode_steps     llama.py:551-634 (delta decode composition under those
+                         policies)
   round_bf16, *_bf16     the bf16 elementwise arithmetic of llama.py:740-751 and
                          stride.py:38-40 (fp32 op, one round-to-nearest-even)
   rope / rms_norm        llama.py:129-192 (rotate_half RoPE), llama.py:60-74 (RMSNorm),
@@ -251,23 +256,67 @@ def decode_row(q: np.ndarray, k: np.ndarray, v: np.ndarray, window: int, sink: i
     return masked_attention(q, k, v, allowed, scale)
 
 
+def decode_anchor_flags(cosines: Sequence[Optional[float]], policy: str = "fixed",
+                        gamma_dec: int = 8, gamma_dec_max: int = 128,
+                        drift_threshold: float = 0.95, drift_k: float = 2.0,
+                        warmup: int = 8, history: int = 16) -> list:
+    """Anchor decisions of a delta decode run (llama.py:578-604). cosines[t] is
+    cos(sparse_t, sparse_{t-1}) over the whole row (None at t = 0, where there
+    is no previous row). Step 0 anchors (no delta yet). Later steps count
+    n = steps since the last anchor, and anchor when n reaches gamma_dec_max,
+    or (fixed) gamma_dec; otherwise, for drift, when the cosine is below
+    drift_threshold, and for drift_rel, when at least `warmup` cosines are
+    recorded and the cosine is below their mean minus drift_k population
+    standard deviations. drift_rel records each cosine it tests, after the
+    test, keeping the last `history`; steps anchored by the count record
+    nothing."""
+    flags, since, rec = [], None, np.zeros(0)
+    for t, c in enumerate(cosines):
+        if since is None:
+            flags.append(True)
+            since = 0
+            continue
+        n = since + 1
+        hit = n >= gamma_dec_max or (policy == "fixed" and n >= gamma_dec)
+        if not hit and policy in ("drift", "drift_rel") and c is not None:
+            if policy == "drift":
+                hit = c < drift_threshold
+            else:
+                if rec.size >= warmup:
+                    hit = c < rec.mean() - drift_k * np.sqrt(((rec - rec.mean()) ** 2).mean())
+                rec = np.append(rec, c)[-history:]
+        flags.append(bool(hit))
+        since = 0 if hit else n
+    return flags
+
+
+def flat_cos(a: np.ndarray, b: np.ndarray) -> float:
+    """Cosine of two arrays flattened (torch cosine_similarity over one dim,
+    norms clamped to 1e-8)."""
+    a, b = np.ravel(a).astype(np.float64), np.ravel(b).astype(np.float64)
+    return float(a @ b / max(np.sqrt(a @ a) * np.sqrt(b @ b), 1e-8))
+
+
 def delta_decode_steps(qs: Sequence[np.ndarray], k: np.ndarray, v: np.ndarray, window: int,
-                       sink: int, scale: float, gamma_dec: int) -> list:
-    """Fixed-policy delta decode over successive query rows against one cache
-    (llama.py:551-657): the first step and every gamma_dec-th one output the
-    dense row and refresh delta = dense - sparse; the others output
-    sparse + delta."""
-    outs, delta, steps = [], None, 0
-    for q in qs:
-        sp = decode_row(q, k, v, window, sink, scale)
-        if delta is None or steps + 1 >= gamma_dec:
+                       sink: int, scale: float, gamma_dec: int, policy: str = "fixed",
+                       gamma_dec_max: int = 128, drift_threshold: float = 0.95,
+                       drift_k: float = 2.0, return_flags: bool = False):
+    """Delta decode over successive query rows against one cache
+    (llama.py:551-634): anchor steps (decode_anchor_flags over the cosines of
+    consecutive sparse rows) output the dense row and refresh delta = dense -
+    sparse; the others output sparse + delta."""
+    sparse = [decode_row(q, k, v, window, sink, scale) for q in qs]
+    cos = [None] + [flat_cos(sparse[t], sparse[t - 1]) for t in range(1, len(sparse))]
+    flags = decode_anchor_flags(cos, policy, gamma_dec, gamma_dec_max, drift_threshold, drift_k)
+    outs, delta = [], None
+    for q, sp, anchor in zip(qs, sparse, flags):
+        if anchor:
             dn = decode_row(q, k, v, 0, 0, scale)
-            delta, steps = dn - sp, 0
+            delta = dn - sp
             outs.append(dn)
         else:
-            steps += 1
             outs.append(sp + delta)
-    return outs
+    return (outs, flags) if return_flags else outs
 
 
 # ---------------------------------------------------------------------------

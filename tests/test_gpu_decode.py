@@ -190,6 +190,74 @@ def test_drift_policies(gpu):
     assert len(rel._dec_state["cos_hist"]) == 3
 
 
+def _walk_qs(n, seed, sig):
+    """Query rows that random-walk with step sizes sig[t], kept at unit RMS:
+    small steps keep consecutive sparse rows close (cosine near 1), large ones
+    break them."""
+    g = torch.Generator().manual_seed(seed)
+    cur = torch.randn(1, 8, 1, 128, generator=g)
+    qs = []
+    for t in range(n):
+        cur = cur + sig[t % len(sig)] * torch.randn(1, 8, 1, 128, generator=g)
+        cur = cur / cur.pow(2).mean().sqrt()
+        qs.append(cur.to(torch.bfloat16).cuda())
+    return qs
+
+
+def _margins(cos, policy, threshold, k):
+    """Distance of each tested cosine from its decision bound (the oracle's
+    rule without the count triggers): a comparison of GPU and oracle flags is
+    only well posed when every margin is clear of the rows' rounding."""
+    out, rec = [], []
+    for c in cos[1:]:
+        if policy == "drift":
+            out.append(abs(c - threshold))
+        else:
+            if len(rec) >= 8:
+                m = float(np.mean(rec))
+                out.append(abs(c - (m - k * float(np.std(rec)))))
+            rec = (rec + [c])[-16:]
+    return out
+
+
+@pytest.mark.parametrize("policy", ["fixed", "drift", "drift_rel"])
+@pytest.mark.parametrize("log_drift", [False, True])
+def test_policies_match_oracle(gpu, policy, log_drift):
+    """Each refresh policy over 26 decode steps: outputs and anchor steps
+    against the oracle's delta_decode_steps (llama.py:551-634), with the drift
+    thresholds placed between the realised cosines of consecutive sparse rows."""
+    _, k, v = _rand(1, 8, 2, 3000, 128, seed=60)
+    qs = _walk_qs(26, seed=61, sig=[0.02, 0.03, 0.02, 1.5, 0.02, 0.04, 0.02, 0.03, 0.02,
+                                    0.03, 0.02, 0.05, 3.0])
+    scale = 128 ** -0.5
+    qn = [np64(q) for q in qs]
+    sp = [O.decode_row(q, np64(k), np64(v), 512, 64, scale) for q in qn]
+    cos = [None] + [O.flat_cos(sp[t], sp[t - 1]) for t in range(1, len(sp))]
+    params = dict(gamma_dec=5, gamma_dec_max=11, drift_threshold=0.9, drift_k=2.0)
+    if policy == "drift":
+        srt = sorted(c for c in cos[1:])
+        gap = max(range(len(srt) - 1), key=lambda i: srt[i + 1] - srt[i])
+        params["drift_threshold"] = 0.5 * (srt[gap] + srt[gap + 1])
+    if policy != "fixed":
+        marg = _margins(cos, policy, params["drift_threshold"], params["drift_k"])
+        assert marg and min(marg) > 1e-3, f"test inputs too close to the bound: {min(marg)}"
+    ref, flags = O.delta_decode_steps(qn, np64(k), np64(v), 512, 64, scale, policy=policy,
+                                      return_flags=True, **params)
+    assert any(flags[1:]) and not all(flags[1:]), flags
+    m = _module(refresh_policy=policy, log_drift=log_drift, **params)
+    got_flags = []
+    for t, q in enumerate(qs):
+        out = _step(m, q, k, v)
+        got_flags.append(m._dec_state["steps"] == 0)
+        assert_close(np64(out).transpose(0, 2, 1, 3), ref[t], what=f"{policy} step {t}")
+    assert got_flags == flags
+    if log_drift:
+        pts = m._dec_drift_points
+        assert [p["anchor"] for p in pts] == flags
+        assert all(abs(p["drift_cos"] - 1.0) < 1e-5 for p, f in zip(pts, flags) if f)
+        assert all(abs(p["applied_vs_true_cos"] - 1.0) < 1e-5 for p, f in zip(pts, flags) if f)
+
+
 def _small_model(**kw):
     from delta_attention.model import LlamaConfig, random_llama
     cfg = LlamaConfig(vocab_size=512, hidden_size=2048, intermediate_size=4096, num_hidden_layers=2,

@@ -443,3 +443,88 @@ def test_head_row_cos_against_library_and_closed_forms():
     np.testing.assert_allclose(O.head_row_cos(a, b), O.head_row_cos(0.01 * a, 40 * b), atol=1e-13)
     no_sqrt = (a * b).sum(-1) / ((a * a).sum(-1) * (b * b).sum(-1))
     assert np.abs(no_sqrt - ref).max() > 0.1
+
+
+# ---------------------------------------------------------------------------
+# delta decode refresh policies (llama.py:578-604), hand-built schedules
+
+def test_decode_anchor_flags_fixed_and_cap():
+    T, F = True, False
+    # fixed: step 0 has no delta; then every gamma_dec-th step since the last anchor
+    assert O.decode_anchor_flags([None] + [0.5] * 9, "fixed", gamma_dec=3) == \
+        [T, F, F, T, F, F, T, F, F, T]
+    # gamma_dec_max guards every policy: a drift threshold that never fires
+    assert O.decode_anchor_flags([None] + [0.5] * 9, "drift", drift_threshold=-2.0,
+                                 gamma_dec_max=4) == [T, F, F, F, T, F, F, F, T, F]
+    # fixed with gamma_dec above the cap: the cap decides
+    assert O.decode_anchor_flags([None] + [0.5] * 5, "fixed", gamma_dec=50,
+                                 gamma_dec_max=2) == [T, F, T, F, T, F]
+
+
+def test_decode_anchor_flags_drift():
+    T, F = True, False
+    # anchor exactly where cos(sparse_t, sparse_{t-1}) < threshold, including
+    # the step right after an anchor
+    cos = [None, 0.99, 0.5, 0.2, 0.99, 0.9, 0.89]
+    assert O.decode_anchor_flags(cos, "drift", drift_threshold=0.9) == [T, F, T, T, F, F, T]
+    # the drift policy ignores gamma_dec
+    assert O.decode_anchor_flags([None] + [0.99] * 6, "drift", gamma_dec=2,
+                                 drift_threshold=0.9) == [T] + [F] * 6
+
+
+def test_decode_anchor_flags_drift_rel():
+    T, F = True, False
+    # no test until 8 cosines are recorded; then cos < mean - k * pstd
+    base = [None] + [0.8, 1.0] * 4              # history 0.8 x4, 1.0 x4: mean 0.9, pstd 0.1
+    assert O.decode_anchor_flags(base + [0.71], "drift_rel", drift_k=2.0) == [T] + [F] * 9
+    assert O.decode_anchor_flags(base + [0.69], "drift_rel", drift_k=2.0) == [T] + [F] * 8 + [T]
+    assert O.decode_anchor_flags(base + [0.69], "drift_rel", drift_k=3.0) == [T] + [F] * 9
+    # a constant history (pstd 0): anything below the mean anchors
+    assert O.decode_anchor_flags([None] + [0.9] * 8 + [0.89999, 0.9], "drift_rel") == \
+        [T] + [F] * 8 + [T, F]
+    # the 8th recorded cosine is the first one tested against: 7 recorded -> no test
+    assert O.decode_anchor_flags([None] + [0.9] * 7 + [0.1], "drift_rel") == [T] + [F] * 8
+    # a rolling window of 16: an early outlier (0.0) widens the spread while it
+    # is in the window (0.85 passes), and once 16 later cosines have pushed it
+    # out the spread is 0 and 0.85 anchors
+    hist = [None, 0.0] + [0.9] * 15
+    assert O.decode_anchor_flags(hist + [0.85], "drift_rel")[-1] is False
+    assert O.decode_anchor_flags(hist + [0.9, 0.85], "drift_rel")[-1] is True
+    # steps anchored by the count record nothing: with gamma_dec_max 3 every
+    # third step anchors by the count, and its cosine (0.1 at step 3) never
+    # enters the history; had it, the spread would keep 0.85 at step 13 (the
+    # first test, 8 cosines of 0.9 recorded) from anchoring
+    cos = [None, 0.9, 0.9, 0.1] + [0.9] * 9 + [0.85]
+    assert O.decode_anchor_flags(cos, "drift_rel", gamma_dec_max=3) == \
+        [T, F, F] * 4 + [T, T]
+    cos2 = [None] + [0.9] * 8 + [0.1, 0.2]
+    assert O.decode_anchor_flags(cos2, "drift_rel") == [T] + [F] * 8 + [T, T]
+
+
+def test_delta_decode_steps_composition():
+    """Outputs follow the flags: anchors are the dense row, the other steps
+    sparse + the last anchor's delta (checked against decode_row directly)."""
+    rng = np.random.default_rng(5)
+    k = rng.standard_normal((1, 2, 300, 16))
+    v = rng.standard_normal((1, 2, 300, 16))
+    q0 = rng.standard_normal((1, 4, 1, 16))
+    qs = [q0 + 0.05 * t * rng.standard_normal(q0.shape) for t in range(7)]
+    outs, flags = O.delta_decode_steps(qs, k, v, 64, 8, 0.25, gamma_dec=3, policy="fixed",
+                                       return_flags=True)
+    assert flags == [True, False, False, True, False, False, True]
+    delta = None
+    for q, o, f in zip(qs, outs, flags):
+        sp = O.decode_row(q, k, v, 64, 8, 0.25)
+        dn = O.decode_row(q, k, v, 0, 0, 0.25)
+        if f:
+            delta = dn - sp
+            np.testing.assert_allclose(o, dn, rtol=0, atol=1e-12)
+        else:
+            np.testing.assert_allclose(o, sp + delta, rtol=0, atol=1e-12)
+    # drift: the flags come from the cosines of consecutive sparse rows
+    sp = [O.decode_row(q, k, v, 64, 8, 0.25) for q in qs]
+    cos = [None] + [O.flat_cos(sp[t], sp[t - 1]) for t in range(1, 7)]
+    thr = float(np.median([c for c in cos[1:]]))
+    _, fl = O.delta_decode_steps(qs, k, v, 64, 8, 0.25, gamma_dec=3, policy="drift",
+                                 drift_threshold=thr, return_flags=True)
+    assert fl == [True] + [c < thr for c in cos[1:]]
