@@ -7,7 +7,8 @@ on it directly when `log_drift` is set.
 
 from __future__ import annotations
 
-from typing import Any, Dict, Iterable, List
+from functools import reduce
+from typing import Any, Dict, Iterable, List, Tuple
 
 HIST_BINS = 40
 HIST_RANGE = (-1.0, 1.0)
@@ -50,29 +51,39 @@ def drift_summary_of(cos, hist, layer_idx: int, gamma: int, seq_len: int) -> Dic
 def _check_binning(summary: Dict[str, Any]) -> None:
     """A summary binned differently from this module (another version wrote
     it) cannot be summed with the others."""
-    bins, rng, hist = summary["hist_bins"], list(summary["hist_range"]), summary["hist"]
-    if bins != HIST_BINS or rng != list(HIST_RANGE) or len(hist) != HIST_BINS:
+    bins, rng = summary["hist_bins"], list(summary["hist_range"])
+    if bins != HIST_BINS or rng != list(HIST_RANGE):
         raise ValueError(
             f"drift sidecar bins/range {bins}/{rng} do not match {HIST_BINS}/{list(HIST_RANGE)} "
             "(mixed-version sidecar files)")
+
+
+def _fold_mean(acc: Tuple[float, int], summary: Dict[str, Any]) -> Tuple[float, int]:
+    """Running n-weighted mean, one summary at a time in input order (the
+    aggregated means of the reference's sidecar tools carry exactly these
+    roundings)."""
+    mean, n = acc
+    total = n + int(summary["n"])
+    if total > 0:
+        mean = (mean * n + float(summary["mean"]) * int(summary["n"])) / total
+    return mean, total
 
 
 def aggregate_drift(lines: Iterable[Dict[str, Any]]) -> Dict[int, Dict[str, Any]]:
     """Per-request summaries -> one entry per layer, the reference's schema
     (drift.py:52-77): `n` and `hist` summed, `mean` the n-weighted mean (0.0
     for a layer without cosines), `requests` the number of summaries, `gamma`
-    the first summary's. Pure Python; a summary with other bins is an error."""
+    the first summary's. Pure Python; a summary with other bins or range is
+    an error."""
     groups: Dict[int, List[Dict[str, Any]]] = {}
     for summary in lines:
         _check_binning(summary)
         groups.setdefault(int(summary["layer"]), []).append(summary)
     result: Dict[int, Dict[str, Any]] = {}
     for layer, group in groups.items():
-        n = sum(int(g["n"]) for g in group)
-        weighted = sum(float(g["mean"]) * int(g["n"]) for g in group)
+        mean, n = reduce(_fold_mean, group, (0.0, 0))
         result[layer] = {
-            "layer": layer, "n": n, "mean": weighted / n if n else 0.0,
-            "requests": len(group),
+            "layer": layer, "n": n, "mean": mean, "requests": len(group),
             "hist": [sum(col) for col in zip(*(g["hist"] for g in group))],
             "hist_bins": HIST_BINS, "hist_range": list(HIST_RANGE), "gamma": group[0]["gamma"],
         }
@@ -80,6 +91,8 @@ def aggregate_drift(lines: Iterable[Dict[str, Any]]) -> Dict[int, Dict[str, Any]
 
 
 def hist_bin_edges() -> List[float]:
-    """The HIST_BINS + 1 bin edges over HIST_RANGE (torch.histc's equal bins)."""
+    """The HIST_BINS + 1 bin edges over HIST_RANGE (torch.histc's equal bins),
+    as the reference's eval tools write them: lo + i * (span / bins)."""
     lo, hi = HIST_RANGE
-    return [lo + (hi - lo) * i / HIST_BINS for i in range(HIST_BINS + 1)]
+    width = (hi - lo) / HIST_BINS
+    return [lo + i * width for i in range(HIST_BINS + 1)]

@@ -27,6 +27,9 @@ from .delta_kernel import attention as qsa_kernel
 from .timing import region
 
 
+# per-device side streams of the adaptive path (LlamaAttention._side_stream)
+_SIDE_STREAMS: dict = {}
+
 class LlamaRMSNorm(nn.Module):
     """x / sqrt(mean(x^2) + eps) in float32, times the weight, in the input
     dtype (llama.py:60-74)."""
@@ -387,13 +390,16 @@ class LlamaAttention(nn.Module):
         return out.to(query_states.dtype)
 
 
-    def _side_stream(self, device):
-        """A second stream (default priority) for the adaptive path's row-chunked
-        key-sparse pass, one per device."""
-        streams = self.__dict__.setdefault("_adapt_streams", {})
-        st = streams.get(device)
+    @staticmethod
+    def _side_stream(device):
+        """The second stream (default priority) of the adaptive path's
+        row-chunked key-sparse pass: one per device, shared by every layer
+        (the layers run one after another)."""
+        idx = torch.device(device).index
+        idx = torch.cuda.current_device() if idx is None else idx
+        st = _SIDE_STREAMS.get(idx)
         if st is None:
-            st = streams[device] = torch.cuda.Stream(device=device)
+            st = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
         return st
 
     # -- decode (llama.py:498-657) ---------------------------------------------------

@@ -151,7 +151,12 @@ def test_module_forward_and_qwen3(gpu):
         x = torch.randn(1, 1024, H * 128, device="cuda", dtype=torch.bfloat16)
         pos = torch.arange(1024, device="cuda")[None]
         cos, sin = rope_cos_sin(pos, 128, 500000.0, torch.bfloat16)
-        y, _ = m(x, (cos, sin))
+        seen = []   # the attention output, as o_proj receives it
+        hook = m.o_proj.register_forward_pre_hook(lambda mod, args: seen.append(args[0].clone()))
+        try:
+            y, _ = m(x, (cos, sin))
+        finally:
+            hook.remove()
         torch.cuda.synchronize()
         # oracle: the same prologue in numpy, then delta_forward
         hs = (1, 1024, -1, 128)
@@ -167,6 +172,10 @@ def test_module_forward_and_qwen3(gpu):
         qr, kr = O.round_bf16(qr).astype(np.float64), O.round_bf16(kr).astype(np.float64)
         vr = O.round_bf16(vp).astype(np.float64)
         att = O.delta_forward(qr, kr, vr, 64, 256, 16, 128 ** -0.5)
+        # the layer's delta attention itself, at the north-star bar
+        assert len(seen) == 1 and seen[0].shape == (1, 1024, H * 128)
+        assert_close(np64(seen[0]).reshape(1, 1024, H, 128), att, what=f"{cls.__name__} attention")
+        # and through o_proj (a bf16 GEMM of 1024 x H*128 by the random weights)
         y_ref = att.reshape(1, 1024, -1) @ np64(m.o_proj.weight).T
         assert_close(np64(y)[0], y_ref[0], cos_min=0.99, atol=5e-2, what=f"{cls.__name__} forward")
 

@@ -95,10 +95,12 @@ def test_aggregate_drift():
     assert agg[3]["n"] == 64 and agg[3]["requests"] == 2
     assert agg[3]["mean"] == pytest.approx((s["mean"] + 1.0) / 2)
     assert agg[3]["hist"][30] == 64 and sum(agg[3]["hist"]) == 64
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match="mixed-version"):
         drift.aggregate_drift([dict(s, hist_bins=10)])
-    with pytest.raises(ValueError):
-        drift.aggregate_drift([dict(s, hist=hist[:-1])])
+    with pytest.raises(ValueError, match="mixed-version"):
+        drift.aggregate_drift([dict(s, hist_range=[0.0, 1.0])])
+    # the reference pairs histograms with zip: a shorter one truncates the sum
+    assert len(drift.aggregate_drift([s, dict(s, hist=hist[:-1])])[3]["hist"]) == drift.HIST_BINS - 1
     # several layers, unequal weights, an empty request
     h2 = [0] * drift.HIST_BINS
     h2[0], h2[39] = 5, 3
@@ -112,8 +114,19 @@ def test_aggregate_drift():
     assert drift.aggregate_drift([dict(s, n=0)])[3]["mean"] == 0.0
     assert set(agg[3]) == {"layer", "n", "mean", "requests", "hist", "hist_bins", "hist_range",
                            "gamma"}
+    # means fold one summary at a time, (m * n + m_i * n_i) / (n + n_i), the
+    # order whose roundings the reference's sidecar aggregates carry: these
+    # three summaries give a different last bit than sum(m_i n_i) / sum(n_i)
+    parts = [(47, 0.604), (38, 0.891), (21, -0.939)]
+    m, n = 0.0, 0
+    for n_i, m_i in parts:
+        m, n = (m * n + m_i * n_i) / (n + n_i), n + n_i
+    assert m != sum(a * b for a, b in parts) / n
+    agg = drift.aggregate_drift([dict(s, n=n_i, mean=m_i) for n_i, m_i in parts])
+    assert agg[3]["mean"] == m
     # the edges are torch.histc's: a value just inside each edge lands in that bin
     edges = drift.hist_bin_edges()
+    assert edges == [-1.0 + i * (2.0 / drift.HIST_BINS) for i in range(drift.HIST_BINS + 1)]
     np.testing.assert_allclose(edges, np.linspace(*drift.HIST_RANGE, drift.HIST_BINS + 1),
                                rtol=0, atol=1e-15)
     probe = torch.tensor(edges[:-1], dtype=torch.float64) + 1e-9

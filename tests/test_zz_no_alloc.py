@@ -74,15 +74,25 @@ def test_noalloc_decode_matches_workspace_entry(gpu, first, second):
 
 def test_noalloc_decode_refuses_sizes_past_the_scratch(gpu):
     """GQA 128 x 8 KV heads at 131072 keys needs more partials than the 16 MiB
-    scratch holds: refused on the host before any launch."""
+    scratch holds: refused on the host before any launch. The call gets real
+    device buffers of the shapes it names (q, out [1, 1024, 1, 128], k/v
+    [1, 8, 131072, 128], the key count), so that only the scratch size is out
+    of range."""
     lib = L.lib()
     B, H, Hkv, cap, D = 1, 1024, 8, 131072, 128
     need = lib.da_decode_workspace_bytes(B, H, Hkv, cap, D, 0, 0)
     assert need > lib.da_decode_scratch_bytes()
+    q = torch.zeros(B, H, 1, D, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty_like(q)
+    k = torch.zeros(B, Hkv, cap, D, dtype=torch.bfloat16, device="cuda")
+    v = torch.zeros_like(k)
+    nk = torch.full((1,), cap, dtype=torch.int32, device="cuda")
     P = ctypes.c_void_p
     s3 = L.strides3(H * D, D, D)
     k3 = L.strides3(Hkv * cap * D, cap * D, D)
-    rc = lib.da_decode_attn_fwd_dev_noalloc(P(16), P(16), P(16), P(16), B, H, Hkv, P(16), cap, D,
+    rc = lib.da_decode_attn_fwd_dev_noalloc(P(q.data_ptr()), P(k.data_ptr()), P(v.data_ptr()),
+                                            P(out.data_ptr()), B, H, Hkv, P(nk.data_ptr()), cap, D,
                                             s3, k3, k3, s3, 0, 0, 0.1, None, None, L.DA_BF16,
                                             None)
+    torch.cuda.synchronize()
     assert rc == L.DA_ERR_SCRATCH
