@@ -88,6 +88,11 @@ def parse():
                         "with --model, every layer of the model uses it")
     p.add_argument("--adapt-chunk", type=int, default=4096)
     p.add_argument("--adapt-threshold", type=float, default=0.95)
+    p.add_argument("--energy", action="store_true",
+                   help="power-limit evidence: the fused kernel (1)+(3) at 32 and 64 query rows "
+                        "per wave, kernel (2), and a hipBLASLt bf16 GEMM (8192^3), each run back "
+                        "to back for about 1.5 s on the workload's N(0,1) inputs and on zeros, "
+                        "with engine clock and package power sampled; one JSON line")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -609,6 +614,81 @@ def load_traffic(name):
         return None
 
 
+def energy(a, q, k, v, dev, O):
+    """The same instruction stream on N(0,1) data and on zeros, beside a
+    hipBLASLt GEMM: under the package power cap the engine clock drops with
+    the switching activity of the operands, so the time per launch follows
+    the energy per launch (package power x time). Prints one JSON line."""
+    import torch
+    from delta_attention import ops
+    from delta_attention import _lib as L
+    B, H, Hkv, S, D = a.batch, a.heads, a.kv_heads, a.seq, a.head_dim
+    scale = D ** -0.5
+    cut_n, s_p, n_anchor = ops.anchor_layout(S, a.gamma)
+    idx = ops.selected_rows(S, a.gamma, str(dev))
+    out = torch.empty(B, S, H, D, device=dev, dtype=torch.bfloat16)
+    dense_sel = torch.zeros(B, n_anchor, H, D, device=dev, dtype=torch.bfloat16)
+    ws = ops.qsparse_workspace(B, H, Hkv, idx.numel(), S, D, dev)
+    zeros = tuple(torch.zeros_like(x) for x in (q, k, v))
+    # algorithmic work: the fused launch covers rows < s_p, kernel (2) the selected rows
+    f_fused = 4.0 * D * H * B * float(O.sparse_row_counts(S, a.window, a.sink)[:s_p].sum())
+    f_rows = O.flops_qsparse(B, H, D, O.selected_rows(S, a.gamma))
+
+    def run(fn, flop, seconds=1.5):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(); fn(); e1.record(); torch.cuda.synchronize()
+        n = max(10, int(seconds * 1e3 / max(e0.elapsed_time(e1), 1e-3)))
+        st = GpuState()
+        with st:
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record(); torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n
+        g = st.summary()
+        w = g["power_w"]["median"] if g["power_w"] else None
+        tf = flop / (ms * 1e-3) / 1e12
+        return {"ms": round(ms, 4), "tflops": round(tf, 1), "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4),
+                "sclk_mhz": g["sclk_mhz"]["median"] if g["sclk_mhz"] else None, "power_w": w,
+                "joule": round(w * ms * 1e-3, 4) if w else None,
+                "pj_per_flop": round(w * ms * 1e-3 / flop * 1e12, 4) if w else None, "launches": n}
+
+    recs = []
+    prev = ops.set_sparse_rows_per_wave(32)
+    try:
+        for rows in (32, 64):
+            ops.set_sparse_rows_per_wave(rows)
+            for data, (qq, kk, vv) in (("normal", (q, k, v)), ("zeros", zeros)):
+                r = run(lambda: ops.sparse_attention_delta(qq, kk, vv, window=a.window, sink=a.sink,
+                                                           sm_scale=scale, dense_sel=dense_sel,
+                                                           gamma=a.gamma, s_p=s_p, out=out), f_fused)
+                recs.append({"kernel": "sparse_attn_delta", "rows_per_wave": rows, "data": data, **r})
+    finally:
+        ops.set_sparse_rows_per_wave(prev)
+    for data, (qq, kk, vv) in (("normal", (q, k, v)), ("zeros", zeros)):
+        r = run(lambda: ops.qsparse_attention(qq, kk, vv, idx, scale, q_rows=idx, epi=L.DA_EPI_DENSE,
+                                              out=out, n_anchor=n_anchor, delta=dense_sel, workspace=ws),
+                f_rows)
+        recs.append({"kernel": "qsparse_attn+merge", "data": data, **r})
+    M = 8192
+    x = torch.randn(M, M, device=dev).to(torch.bfloat16)
+    y = torch.randn(M, M, device=dev).to(torch.bfloat16)
+    z = torch.empty(M, M, device=dev, dtype=torch.bfloat16)
+    for data in ("normal", "zeros"):
+        if data == "zeros":
+            x.zero_(); y.zero_()
+        r = run(lambda: torch.matmul(x, y, out=z), 2.0 * M ** 3)
+        recs.append({"kernel": "hipblaslt_gemm_8192_bf16", "data": data, **r})
+    cap = GpuState().summary().get("power_cap_w")
+    print(json.dumps({"metric": "energy per launch under the package power cap", "power_cap_w": cap,
+                      "config": {"workload": "llama-3.1-8b-shaped delta-attention layer prefill",
+                                 "seq_len": S, "gamma": a.gamma, "window": a.window, "sink": a.sink},
+                      "records": recs}), flush=True)
+
+
 def train_step(a, q, k, v):
     """delta_forward_train forward and backward on the workload's q/k/v with
     a seeded N(0,1) upstream gradient: median ms of each over --steps after
@@ -686,6 +766,9 @@ def main():
         return
     if a.train:
         train_step(a, q, k, v)
+        return
+    if a.energy:
+        energy(a, q, k, v, dev, O)
         return
     if a.adaptive:
         adaptive_layer(a, q, k, v)

@@ -45,6 +45,7 @@
 //   * Per key tile, one scheduling region keeps the matrix pipe fed: the
 //     exponentials of tile t run under the score MFMAs of tile t+1, then the
 //     PV MFMAs of tile t follow with their V reads running ahead.
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -71,10 +72,10 @@ namespace da {
 #ifndef DA_DECODE_ITEMS
 #define DA_DECODE_ITEMS 512
 #endif
-// Row groups per wave of the head_dim-128 key-sparse launches and of the
-// selected-rows launches (1 or 2).
+// Row groups per wave of the head_dim-128 key-sparse launches (the default
+// of da_set_sparse_rows_per_wave) and of the selected-rows launches (1 or 2).
 #ifndef DA_RG_SPARSE
-#define DA_RG_SPARSE 2
+#define DA_RG_SPARSE 1
 #endif
 #ifndef DA_RG_ROWS
 #define DA_RG_ROWS 1
@@ -1264,11 +1265,15 @@ struct QsparsePlan {
   size_t ws_bytes;
 };
 
-// Rows per workgroup of a launch: 64 rows per wave (bm 256) for the
-// head_dim-128 key-sparse launches and, when DA_RG_ROWS is 2, selected-rows
-// launches; 32 rows per wave (bm 128) for the other head dims and for decode
+// Rows per workgroup of a launch: for the head_dim-128 key-sparse launches
+// 32 (bm 128, two workgroups per CU) or 64 query rows per wave (bm 256, one
+// workgroup per CU; da_set_sparse_rows_per_wave); 64 for the selected-rows
+// launches when DA_RG_ROWS is 2; 32 for the other head dims and for decode
 // rows (one query row per batch).
-static int sparse_bm(int D) { return D == 128 ? bm_of(DA_RG_SPARSE) : bm_of(1); }
+static std::atomic<int> g_rg_sparse{DA_RG_SPARSE};
+static int sparse_bm(int D) {
+  return D == 128 ? bm_of(g_rg_sparse.load(std::memory_order_relaxed)) : bm_of(1);
+}
 static int rows_bm(int D) { return D == 128 ? bm_of(DA_RG_ROWS) : bm_of(1); }
 
 // Merge workgroups per row tile at most: bm rows x D / 8 column chunks x 16
@@ -1443,6 +1448,14 @@ static int sparse_items(AttnArgs& a) {
   a.fd_gt = make_fastdiv(a.Gs);
   return DA_OK;
 }
+
+extern "C" int da_set_sparse_rows_per_wave(int rows) {
+  if (rows != 32 && rows != 64) return DA_ERR_INVALID_ARG;
+  g_rg_sparse.store(rows / 32, std::memory_order_relaxed);
+  return DA_OK;
+}
+
+extern "C" int da_sparse_rows_per_wave(void) { return 32 * g_rg_sparse.load(std::memory_order_relaxed); }
 
 extern "C" int da_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out,
                                   int B, int Hq, int Hkv, int S, int D,

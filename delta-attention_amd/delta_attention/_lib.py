@@ -61,6 +61,8 @@ EXPORTS = (
     "da_sparse_attn_fwd_rows",
     "da_adapt_layer_workspace_bytes",
     "da_adapt_layer_fwd",
+    "da_set_sparse_rows_per_wave",
+    "da_sparse_rows_per_wave",
 )
 
 _ERR_TEXT = {
@@ -124,6 +126,10 @@ def _load() -> ctypes.CDLL:
                                            _vp, _p3, _i, _i, _vp, _p3, _i, _vp]
     L.da_fused_delta_rows.restype = _i
     L.da_fused_delta_rows.argtypes = [_i, _i]
+    L.da_set_sparse_rows_per_wave.restype = _i
+    L.da_set_sparse_rows_per_wave.argtypes = [_i]
+    L.da_sparse_rows_per_wave.restype = _i
+    L.da_sparse_rows_per_wave.argtypes = []
     L.da_qsparse_workspace_bytes.restype = _sz
     L.da_qsparse_workspace_bytes.argtypes = [_i, _i, _i, _i, _i, _i]
     L.da_qsparse_attn_fwd.restype = _i

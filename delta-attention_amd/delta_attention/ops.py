@@ -103,6 +103,15 @@ def fused_delta_rows(H: int, Hkv: int) -> int:
     return int(L.lib().da_fused_delta_rows(int(H), int(Hkv)))
 
 
+def set_sparse_rows_per_wave(rows: int) -> int:
+    """Tile shape of the head_dim-128 key-sparse launches, process-wide: 32
+    (default) or 64 query rows per wave. Returns the previous value; the
+    outputs are bit-identical either way."""
+    prev = int(L.lib().da_sparse_rows_per_wave())
+    L.check(L.lib().da_set_sparse_rows_per_wave(int(rows)), "da_set_sparse_rows_per_wave")
+    return prev
+
+
 def sparse_attention_delta(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int,
                            sink: int, sm_scale: float, dense_sel: torch.Tensor, gamma: int,
                            s_p: int, out: torch.Tensor, delta_out: Optional[torch.Tensor] = None,

@@ -22,8 +22,10 @@
  *     owns all memory, including workspaces.
  *   - Return 0 on success or a negative DA_ERR_* code. No entry point keeps
  *     a pointer after it returns and, apart from the static scratch of
- *     da_decode_attn_fwd_dev_noalloc, there is no mutable global state, so
- *     calls are re-entrant.
+ *     da_decode_attn_fwd_dev_noalloc and the process-wide tile-shape choice
+ *     of da_set_sparse_rows_per_wave (read when a launch is issued; results do
+ *     not depend on it), there is no mutable global state, so calls are
+ *     re-entrant.
  */
 #ifndef DELTA_ATTN_H
 #define DELTA_ATTN_H
@@ -121,6 +123,19 @@ int da_sparse_attn_delta_fwd(const void* q, const void* k, const void* v, void* 
  * else one head per 128-row tile; the results do not depend on the packing.
  */
 int da_fused_delta_rows(int Hq, int Hkv);
+
+/*
+ * Query rows per wave of the head_dim-128 key-sparse launches (kernel (1),
+ * the fused delta launch and the adaptive layer's sparse passes): 32 (the
+ * default; two 4-wave workgroups per CU) or 64 (one workgroup per CU, each
+ * K/V fragment read from LDS feeding two MFMAs, O in AGPRs). Process-wide;
+ * returns DA_ERR_INVALID_ARG for other values. The per-row rescale decisions
+ * make every output bit independent of the choice. No counterpart in the
+ * reference: a tile-shape knob of this implementation (the reference's
+ * kernels pick their tiles internally).
+ */
+int da_set_sparse_rows_per_wave(int rows);
+int da_sparse_rows_per_wave(void);
 
 /*
  * Workspace (bytes) that da_qsparse_attn_fwd needs for these sizes; 0 is a

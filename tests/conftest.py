@@ -30,3 +30,13 @@ def gpu():
     from delta_attention import _lib
     _lib.lib()  # raises ExtensionMissing when the HIP library is not built
     return True
+
+
+@pytest.fixture(params=[32, 64], ids=["rows32", "rows64"])
+def rows_per_wave(request, gpu):
+    """Run the test with each tile shape of the head_dim-128 key-sparse
+    launches (32 or 64 query rows per wave), restoring the previous one."""
+    from delta_attention import ops
+    prev = ops.set_sparse_rows_per_wave(request.param)
+    yield request.param
+    ops.set_sparse_rows_per_wave(prev)

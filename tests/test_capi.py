@@ -175,6 +175,19 @@ def test_fused_delta_rows_and_checks(lib):
     assert call(S=0, s_p=0) == L.DA_OK
 
 
+def test_sparse_rows_per_wave_setting(lib):
+    # 32 (default) or 64 query rows per wave; anything else is refused and
+    # leaves the setting as it was
+    assert lib.da_sparse_rows_per_wave() == 32
+    for bad in (0, 16, 48, 96, 128, -32):
+        assert lib.da_set_sparse_rows_per_wave(bad) == L.DA_ERR_INVALID_ARG
+        assert lib.da_sparse_rows_per_wave() == 32
+    assert lib.da_set_sparse_rows_per_wave(64) == L.DA_OK
+    assert lib.da_sparse_rows_per_wave() == 64
+    assert lib.da_set_sparse_rows_per_wave(32) == L.DA_OK
+    assert lib.da_sparse_rows_per_wave() == 32
+
+
 def test_norm_and_swiglu_checks(lib):
     P = ctypes.c_void_p
     assert lib.da_add_rmsnorm(P(16), 4096, None, 0, None, 0, P(16), 4096, P(16), 8, 3000, 1e-5,

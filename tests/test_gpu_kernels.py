@@ -40,11 +40,11 @@ def _sparse_case(B, H, Hkv, S, D, window, sink, qb=64, dtype=torch.bfloat16, see
     (1, 8, 2, 1100, 32, 300, 16),      # head_dim 32
     (2, 6, 3, 500, 32, 64, 0),         # head_dim 32, GQA 2, batch 2
 ])
-def test_sparse_attention_parity(gpu, B, H, Hkv, S, D, window, sink):
+def test_sparse_attention_parity(gpu, rows_per_wave, B, H, Hkv, S, D, window, sink):
     _sparse_case(B, H, Hkv, S, D, window, sink)
 
 
-def test_sparse_attention_fp16_and_q_block(gpu):
+def test_sparse_attention_fp16_and_q_block(gpu, rows_per_wave):
     _sparse_case(1, 8, 2, 640, 128, 160, 16, qb=32, dtype=torch.float16)
     _sparse_case(1, 4, 1, 256, 64, 64, 8, qb=1)
 
@@ -53,7 +53,7 @@ def test_sparse_attention_fp16_and_q_block(gpu):
     (8, 2, 128, 256, 16, (0, 300, 301, 1024, 1500)),   # GQA 4: two heads per 64-row tile
     (5, 1, 64, 100, 0, (0, 64, 500, 1500)),            # GQA 5: one head per 128-row tile
 ])
-def test_sparse_attention_row_ranges(gpu, H, Hkv, D, window, sink, cuts):
+def test_sparse_attention_row_ranges(gpu, rows_per_wave, H, Hkv, D, window, sink, cuts):
     """Row ranges of the key-sparse pass (da_sparse_attn_fwd_rows), launched
     one after another into one output, give the full launch's bits; rows
     outside a launched range are left untouched."""
@@ -70,6 +70,31 @@ def test_sparse_attention_row_ranges(gpu, H, Hkv, D, window, sink, cuts):
     ops.sparse_attention(q, k, v, window=window, sink=sink, sm_scale=scale, out=part, rows=(301, 700))
     assert torch.equal(part[:, 301:1001], full[:, 301:1001])
     assert bool((part[:, :301] == 7.0).all()) and bool((part[:, 1001:] == 7.0).all())
+
+
+@pytest.mark.parametrize("H,Hkv,S,window,sink,gamma", [
+    (8, 2, 3000, 1024, 128, 64),    # GQA 4: two heads per 64-row tile (32 rows per wave) or four (64)
+    (10, 2, 1700, 512, 16, 16),     # GQA 5: one head per 128- or 256-row tile
+    (4, 4, 900, 128, 3, 32),        # MHA
+])
+def test_sparse_bits_independent_of_rows_per_wave(gpu, H, Hkv, S, window, sink, gamma):
+    """Kernel (1) and the fused delta launch at 64 query rows per wave (one
+    workgroup per CU, O in AGPRs) give the bits of the 32-rows-per-wave
+    launch: same row maxima, same accumulation order, per-row rescale."""
+    from delta_attention import ops
+    q, k, v = gen_qkv(1, H, Hkv, S, 128, seed=S + H, model_layout=True)
+    scale = 128 ** -0.5
+    res = {}
+    for rows in (32, 64):
+        prev = ops.set_sparse_rows_per_wave(rows)
+        try:
+            res[rows] = (ops.sparse_attention(q, k, v, window=window, sink=sink, sm_scale=scale),
+                         ops.delta_prefill(q, k, v, gamma=gamma, window=window, sink=sink, sm_scale=scale))
+            torch.cuda.synchronize()
+        finally:
+            ops.set_sparse_rows_per_wave(prev)
+    assert torch.equal(res[32][0], res[64][0])
+    assert torch.equal(res[32][1], res[64][1])
 
 
 def test_sparse_attention_model_layout(gpu):

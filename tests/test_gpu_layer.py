@@ -390,7 +390,7 @@ def test_adaptive_policy_sparse_only_returns_the_sparse_pass(gpu):
                                           # against kernel (1)'s two-head packing
     (1, 8, 2, 1000, 256, 64, 256, 16),    # head_dim 256
 ])
-def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
+def test_fused_delta_bit_identical(gpu, rows_per_wave, B, H, Hkv, S, D, gamma, window, sink):
     """Kernel (3) fused into kernel (1)'s epilogue (kernel (2) first) gives the
     same bits as the three-kernel sequence, deltas included, and matches the
     oracle's delta_forward."""
@@ -412,7 +412,7 @@ def test_fused_delta_bit_identical(gpu, B, H, Hkv, S, D, gamma, window, sink):
 
 @pytest.mark.parametrize("H,Hkv,D,gamma", [(8, 2, 128, 64), (4, 4, 64, 32), (10, 2, 128, 16),
                                             (8, 2, 64, 128)])
-def test_fused_delta_bit_identical_fp16(gpu, H, Hkv, D, gamma):
+def test_fused_delta_bit_identical_fp16(gpu, rows_per_wave, H, Hkv, D, gamma):
     """The fused order in fp16 (the delta and the add round to fp16): same bits
     as the three-kernel sequence, within the T1 gate of the oracle."""
     from delta_attention import ops

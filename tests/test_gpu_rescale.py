@@ -44,7 +44,7 @@ KINDS = ["growing", "outliers", "wide"]
 
 
 @pytest.mark.parametrize("kind", KINDS)
-def test_rescale_key_sparse(gpu, kind):
+def test_rescale_key_sparse(gpu, rows_per_wave, kind):
     from delta_attention import ops
     q, k, v = _inputs(kind, 1, 8, 2, 1500, 128, seed=41)
     scale = 128 ** -0.5
@@ -67,7 +67,7 @@ def test_rescale_query_sparse(gpu, kind):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-def test_rescale_fused_layer(gpu, kind):
+def test_rescale_fused_layer(gpu, rows_per_wave, kind):
     from delta_attention import ops
     q, k, v = _inputs(kind, 1, 8, 2, 1300, 128, seed=43)
     scale = 128 ** -0.5
@@ -122,7 +122,7 @@ def test_rescale_bits_independent_of_packing(gpu, kind):
 
 
 @pytest.mark.parametrize("kind", ["growing", "outliers"])
-def test_rescale_fp16(gpu, kind):
+def test_rescale_fp16(gpu, rows_per_wave, kind):
     """fp16 inputs whose scores jump by far more than 2^16 in the exponential
     (outlier keys at 40x): with a lazy-rescale bound above 16 the packed fp16
     probabilities would overflow to inf. Kernel (1), kernel (2) and the decode
