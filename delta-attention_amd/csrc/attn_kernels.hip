@@ -1182,33 +1182,64 @@ __global__ __launch_bounds__(MTHR) void qsparse_merge_kernel(MergeArgs a) {
     const int i = mflat / G;
     const int h = hk * G + mflat % G;
 
-    float M = NEG_BIG;
-    for (int s = p; s < nsv; s += P) {
-      const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
-      M = fmaxf(M, a.part_ml[w * 2 * a.ws_rows + r]);
-    }
-    for (int off = 1; off < P; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
-    float L = 0.f;
+    // One pass over this lane's splits s = p, p + P, ... with an online max:
+    // the (max, sum, O) state takes split s as M' = max(M, m_s), weights
+    // 2^(M - M') on the state and 2^(m_s - M') l_s on the stored O_s / l_s.
+    // The loads of MU splits are issued before any of them is combined, so
+    // a lane has all its partial reads in flight at once.
+    constexpr int MU = 4;
+    float M = NEG_BIG, L = 0.f;
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    for (int s = p; s < nsv; s += P) {
-      const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
-      // split weight exp2(m_s - M) l_s on the stored O_s / l_s
-      const float sc = fast_exp2(a.part_ml[w * 2 * a.ws_rows + r] - M) *
-                       a.part_ml[w * 2 * a.ws_rows + a.ws_rows + r];
-      L += sc;
-      const u32x4 x = *(const u32x4*)(a.part_o + (w * a.ws_rows + r) * (D / 2) + 4 * c);
+    auto take = [&](float m, float l, const float (&o)[8]) __attribute__((always_inline)) {
+      const float mn = fmaxf(M, m);
+      const float wa = fast_exp2(M - mn), wb = fast_exp2(m - mn) * l;
+      L = L * wa + wb;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[2 * e] += sc * E::lo(x[e]);
-        acc[2 * e + 1] += sc * E::hi(x[e]);
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] * wa + o[e] * wb;
+      M = mn;
+    };
+    for (int s0 = p; s0 < nsv; s0 += MU * P) {
+      float ms[MU], ls[MU];
+      u32x4 xs[MU];
+#pragma unroll
+      for (int u = 0; u < MU; ++u) {
+        const int s = s0 + u * P;
+        if (s < nsv) {
+          const int64_t w = ((int64_t)bh * a.n_splits + s) * a.n_mtiles + mt;
+          ms[u] = a.part_ml[w * 2 * a.ws_rows + r];
+          ls[u] = a.part_ml[w * 2 * a.ws_rows + a.ws_rows + r];
+          xs[u] = *(const u32x4*)(a.part_o + (w * a.ws_rows + r) * (D / 2) + 4 * c);
+        } else {
+          ms[u] = NEG_BIG;
+          ls[u] = 0.f;
+          xs[u] = (u32x4){0, 0, 0, 0};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < MU; ++u) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[2 * e] = E::lo(xs[u][e]);
+          o[2 * e + 1] = E::hi(xs[u][e]);
+        }
+        take(ms[u], ls[u], o);
       }
     }
+    // the P lanes of the task combine their states the same way
     for (int off = 1; off < P; off <<= 1) {
-      L += __shfl_xor(L, off);
+      float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], off);
+      for (int e = 0; e < 8; ++e) o[e] = __shfl_xor(acc[e], off);
+      const float mo = __shfl_xor(M, off), lo = __shfl_xor(L, off);
+      const float mn = fmaxf(M, mo);
+      const float wa = fast_exp2(M - mn), wb = fast_exp2(mo - mn);
+      L = L * wa + lo * wb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] * wa + o[e] * wb;
+      M = mn;
     }
     if (p != 0) return;
     const float inv = L > 0.f ? 1.f / L : 0.f;
