@@ -24,7 +24,9 @@
 //     summed by dq_reduce_kernel.
 //   * dkdv_kernel: one workgroup per 128 keys (32 per wave, K and V fragments
 //     in registers) and a chunk of the rows that see them; per 32-row tile and
-//     query head it stages Q, dO, lse and rowsum(dO * O) in LDS and forms
+//     query head it stages Q, dO, lse and rowsum(dO * O) in LDS (key-sparse
+//     rows: by buffer-load DMA into two stages, the next tile's rows in flight
+//     under this tile's products) and forms
 //     S = Q K^T, dP = dO V^T (rows x keys), then dV^T += dO^T P and
 //     dK^T += Q^T dS from transposed LDS reads. Sink keys are seen by every
 //     later row, so their row range is cut into chunks like any other; each
@@ -434,13 +436,18 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
   using E = Elt<T>;
   constexpr int NDS = D / 16, NDT = D / 32, DCH = D / 8, RB = 2 * D;
   constexpr int TB = RT * RB;
-  // Q and dO rows of up to HGM query heads per step (all of a KV head's query
-  // heads for GQA up to 8): one load round trip and one barrier pair serve
-  // that many heads' products
-  constexpr int HGM = 8;
-  __shared__ __attribute__((aligned(1024))) char smem[2][HGM][TB];   // Q, dO
-  __shared__ __attribute__((aligned(16))) float s_lse[HGM][RT], s_d[HGM][RT];
-  __shared__ __attribute__((aligned(16))) int s_lim[RT], s_lo[RT];
+  // Q and dO rows of HGM query heads per step. Selected rows (gathered Q
+  // rows): up to 8 heads (all of a KV head's query heads for GQA up to 8) in
+  // one stage filled through registers, so one load round trip and one
+  // barrier pair serve that many heads' products. Key-sparse rows (contiguous
+  // list positions): 4 heads per step in two stages filled by buffer-load
+  // DMA, the next step's rows landing while this step's products run.
+  constexpr int HGM = ROWS ? 8 : 4;
+  constexpr int NSTG = ROWS ? 1 : 2;
+  static_assert(NSTG * HGM == 8, "same LDS footprint for both staging forms");
+  __shared__ __attribute__((aligned(1024))) char smem[NSTG][2][HGM][TB];   // [stage][Q, dO][head]
+  __shared__ __attribute__((aligned(16))) float s_lse[NSTG][HGM][RT], s_d[NSTG][HGM][RT];
+  __shared__ __attribute__((aligned(16))) int s_lim[NSTG][RT], s_lo[NSTG][RT];
   const size_t esz = sizeof(T);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -514,58 +521,18 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
   const float c2 = a.scale_log2;
   const int sink = ROWS ? 0 : a.sink;
 
-  for (int r0 = c_start; r0 <= c_end; r0 += RT) {
-    for (int g0 = 0; g0 < a.G; g0 += HGM) {
-      const int hg = min(HGM, a.G - g0);
-      // stage Q and dO rows of list positions r0 .. r0 + RT - 1 of heads
-      // g0 .. g0 + hg - 1 (zero past the chunk end)
-      for (int slot = tid; slot < hg * RT * DCH; slot += NTHR) {
-        const int gg = slot / (RT * DCH), rem = slot % (RT * DCH);
-        const int rr = rem / DCH, pc = rem % DCH;
-        const int h = hk * a.G + g0 + gg;
-        const int i = r0 + rr;
-        const bool ok = i <= c_end;
-        u32x4 qv = {0, 0, 0, 0}, gv = {0, 0, 0, 0};
-        if (ok) {
-          const int qrow = ROWS ? (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1)) : i;
-          qv = *(const u32x4*)((const char*)a.q + ((int64_t)b * a.qs_b + (int64_t)h * a.qs_h + (int64_t)qrow * a.qs_s) * esz + pc * 16);
-          gv = *(const u32x4*)((const char*)a.dout + ((int64_t)b * a.gs_b + (int64_t)h * a.gs_h + (int64_t)i * a.gs_s) * esz + pc * 16);
-        }
-        *(DA_LDS u32x4*)((DA_LDS char*)&smem[0][gg][0] + rr * RB + ((pc ^ swz<D>(rr)) * 16)) = qv;
-        *(DA_LDS u32x4*)((DA_LDS char*)&smem[1][gg][0] + rr * RB + ((pc ^ swz<D>(rr)) * 16)) = gv;
-      }
-      if (tid < hg * RT) {
-        const int gg = tid / RT, t = tid % RT;
-        const int i = r0 + t;
-        const bool ok = i <= c_end;
-        const int64_t rix = ((int64_t)b * a.Hq + hk * a.G + g0 + gg) * a.n_rows + i;
-        s_lse[gg][t] = ok ? a.lse[rix] : INFINITY;
-        s_d[gg][t] = ok ? a.dvec[rix] : 0.f;
-        if (gg == 0) {
-          int lim = -1, lo = 0;
-          if (ok) {
-            if (ROWS) {
-              const int64_t l = min(a.row_last[i], (int64_t)(a.n_kv - 1));
-              lim = (int)(l < -1 ? -1 : l);
-            } else {
-              lim = i;
-              lo = win_lo(i, a.q_block, a.window);
-            }
-          }
-          s_lim[t] = lim;
-          s_lo[t] = lo;
-        }
-      }
-      __syncthreads();
-      // this wave's 32 keys visible to every row of the step (wave-uniform):
-      // the per-key test is skipped
-      const int kw = k0 + wave * 32;
-      const bool full = r0 + RT - 1 <= c_end &&
-                        (ROWS ? kw + 31 <= s_lim[0]
-                              : kw + 31 <= r0 && (kw + 31 < sink || kw >= s_lo[RT - 1]));
-      for (int gg = 0; gg < hg; ++gg) {
-      const DA_LDS char* qs = (const DA_LDS char*)&smem[0][gg][0];
-      const DA_LDS char* gs = (const DA_LDS char*)&smem[1][gg][0];
+  // Products of one step: the hg heads staged in stage st for list positions
+  // r0 .. r0 + RT - 1 (rows past the chunk end read as zero, lse +inf)
+  auto compute = [&](int st, int r0, int hg) __attribute__((always_inline)) {
+    // this wave's 32 keys visible to every row of the step (wave-uniform):
+    // the per-key test is skipped
+    const int kw = k0 + wave * 32;
+    const bool full = r0 + RT - 1 <= c_end &&
+                      (ROWS ? kw + 31 <= s_lim[st][0]
+                            : kw + 31 <= r0 && (kw + 31 < sink || kw >= s_lo[st][RT - 1]));
+    for (int gg = 0; gg < hg; ++gg) {
+      const DA_LDS char* qs = (const DA_LDS char*)&smem[st][0][gg][0];
+      const DA_LDS char* gs = (const DA_LDS char*)&smem[st][1][gg][0];
 
       // S = Q K^T and dP = dO V^T (rows x keys); element e of this lane is
       // row 16 (e / 8) + 8 lg + e % 8 of the step, key `key`
@@ -585,10 +552,10 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int rb = 16 * half + 8 * lg;
-        const f32x4 l0 = *(const DA_LDS f32x4*)&s_lse[gg][rb], l1 = *(const DA_LDS f32x4*)&s_lse[gg][rb + 4];
-        const f32x4 d0 = *(const DA_LDS f32x4*)&s_d[gg][rb], d1 = *(const DA_LDS f32x4*)&s_d[gg][rb + 4];
-        const u32x4 m0 = *(const DA_LDS u32x4*)&s_lim[rb], m1 = *(const DA_LDS u32x4*)&s_lim[rb + 4];
-        const u32x4 o0 = *(const DA_LDS u32x4*)&s_lo[rb], o1 = *(const DA_LDS u32x4*)&s_lo[rb + 4];
+        const f32x4 l0 = *(const DA_LDS f32x4*)&s_lse[st][gg][rb], l1 = *(const DA_LDS f32x4*)&s_lse[st][gg][rb + 4];
+        const f32x4 d0 = *(const DA_LDS f32x4*)&s_d[st][gg][rb], d1 = *(const DA_LDS f32x4*)&s_d[st][gg][rb + 4];
+        const u32x4 m0 = *(const DA_LDS u32x4*)&s_lim[st][rb], m1 = *(const DA_LDS u32x4*)&s_lim[st][rb + 4];
+        const u32x4 o0 = *(const DA_LDS u32x4*)&s_lo[st][rb], o1 = *(const DA_LDS u32x4*)&s_lo[st][rb + 4];
         float pv[8], dv[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -619,8 +586,139 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
           adk[dt] = E::mfma(read_tr<D>(qs, tro[dt], kk), sf, adk[dt]);
         }
       }
-      }   // heads of the step
+    }   // heads of the step
+  };
+
+  if constexpr (ROWS) {
+    for (int r0 = c_start; r0 <= c_end; r0 += RT) {
+      for (int g0 = 0; g0 < a.G; g0 += HGM) {
+        const int hg = min(HGM, a.G - g0);
+        // stage Q and dO rows of list positions r0 .. r0 + RT - 1 of heads
+        // g0 .. g0 + hg - 1 (zero past the chunk end)
+        for (int slot = tid; slot < hg * RT * DCH; slot += NTHR) {
+          const int gg = slot / (RT * DCH), rem = slot % (RT * DCH);
+          const int rr = rem / DCH, pc = rem % DCH;
+          const int h = hk * a.G + g0 + gg;
+          const int i = r0 + rr;
+          const bool ok = i <= c_end;
+          u32x4 qv = {0, 0, 0, 0}, gv = {0, 0, 0, 0};
+          if (ok) {
+            const int qrow = (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1));
+            qv = *(const u32x4*)((const char*)a.q + ((int64_t)b * a.qs_b + (int64_t)h * a.qs_h + (int64_t)qrow * a.qs_s) * esz + pc * 16);
+            gv = *(const u32x4*)((const char*)a.dout + ((int64_t)b * a.gs_b + (int64_t)h * a.gs_h + (int64_t)i * a.gs_s) * esz + pc * 16);
+          }
+          *(DA_LDS u32x4*)((DA_LDS char*)&smem[0][0][gg][0] + rr * RB + ((pc ^ swz<D>(rr)) * 16)) = qv;
+          *(DA_LDS u32x4*)((DA_LDS char*)&smem[0][1][gg][0] + rr * RB + ((pc ^ swz<D>(rr)) * 16)) = gv;
+        }
+        if (tid < hg * RT) {
+          const int gg = tid / RT, t = tid % RT;
+          const int i = r0 + t;
+          const bool ok = i <= c_end;
+          const int64_t rix = ((int64_t)b * a.Hq + hk * a.G + g0 + gg) * a.n_rows + i;
+          s_lse[0][gg][t] = ok ? a.lse[rix] : INFINITY;
+          s_d[0][gg][t] = ok ? a.dvec[rix] : 0.f;
+          if (gg == 0) {
+            int lim = -1;
+            if (ok) {
+              const int64_t l = min(a.row_last[i], (int64_t)(a.n_kv - 1));
+              lim = (int)(l < -1 ? -1 : l);
+            }
+            s_lim[0][t] = lim;
+            s_lo[0][t] = 0;
+          }
+        }
+        __syncthreads();
+        compute(0, r0, hg);
+        __syncthreads();
+      }
+    }
+  } else {
+    // steps j = (row step, head group), head groups innermost; step j's Q and
+    // dO rows go to stage j & 1 by DMA: 16-byte chunk slot (c NWAVE + wave)
+    // 64 + lane of the stage is [tensor][head][row][position], filled from
+    // the source chunk that position holds under the swizzle. One buffer
+    // resource per (tensor, head) covers the step's rows up to the chunk
+    // end, so rows past it (and heads past the group) read as zero.
+    constexpr int NC = 2 * HGM * RT * DCH / NTHR;   // DMA chunks per thread per step
+    static_assert(NC * NTHR == 2 * HGM * RT * DCH && (RT * DCH) % 64 == 0, "whole waves per (tensor, head)");
+    const int n_g = (a.G + HGM - 1) / HGM;
+    const int n_steps = c_end >= c_start ? ((c_end - c_start) / RT + 1) * n_g : 0;
+    const uint32_t qrow_b = (uint32_t)(a.qs_s * (int64_t)esz);
+    const uint32_t grow_b = (uint32_t)(a.gs_s * (int64_t)esz);
+    // wave instructions per (tensor, head) block of the stage; when the four
+    // waves' instructions c NWAVE + wave of one c fall in one block, the
+    // block (hence the buffer resource) depends on c only
+    constexpr int IPB = RT * DCH / 64;
+    const char* qb0 = (const char*)a.q + ((int64_t)b * a.qs_b + (int64_t)hk * a.G * a.qs_h) * esz;
+    const char* gb0 = (const char*)a.dout + ((int64_t)b * a.gs_b + (int64_t)hk * a.G * a.gs_h) * esz;
+    auto issue = [&](int j, int st) __attribute__((always_inline)) {
+      const int r0 = c_start + (j / n_g) * RT, g0 = (j % n_g) * HGM;
+      const int hg = min(HGM, a.G - g0);
+      const uint32_t nrow = (uint32_t)min(RT, c_end - r0 + 1);
+      const char* qb = qb0 + ((int64_t)g0 * a.qs_h + (int64_t)r0 * a.qs_s) * esz;
+      const char* gb = gb0 + ((int64_t)g0 * a.gs_h + (int64_t)r0 * a.gs_s) * esz;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int slot = (c * NWAVE + wave) * 64 + lane;
+        const int row = (slot / DCH) % RT, pc = slot % DCH;
+        int blk;
+        if constexpr (IPB % NWAVE == 0) blk = c / (IPB / NWAVE);
+        else blk = (c * NWAVE + wave) / IPB;
+        const int tensor = blk / HGM, gg = blk % HGM;
+        const char* base = tensor == 0 ? qb + (int64_t)gg * a.qs_h * esz : gb + (int64_t)gg * a.gs_h * esz;
+        const uint32_t rb = tensor == 0 ? qrow_b : grow_b;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, gg < hg ? nrow * rb : 0u);
+        dma16(rs, (DA_LDS void*)((DA_LDS char*)&smem[st][0][0][0] + (c * NWAVE + wave) * 1024),
+              (uint32_t)row * rb + (uint32_t)((pc ^ swz<D>(row)) * 16));
+      }
+    };
+    // row statistics of step j (threads below HGM * RT: head tid / RT, row
+    // tid % RT), loaded a step ahead and stored to its stage after the
+    // current step's products
+    auto stat_load = [&](int j, float& l, float& dd) __attribute__((always_inline)) {
+      l = INFINITY;
+      dd = 0.f;
+      if (tid < HGM * RT) {
+        const int r0 = c_start + (j / n_g) * RT, g0 = (j % n_g) * HGM;
+        const int gg = tid / RT, i = r0 + tid % RT;
+        if (i <= c_end && g0 + gg < a.G) {
+          const int64_t rix = ((int64_t)b * a.Hq + hk * a.G + g0 + gg) * a.n_rows + i;
+          l = a.lse[rix];
+          dd = a.dvec[rix];
+        }
+      }
+    };
+    auto stat_store = [&](int j, int st, float l, float dd) __attribute__((always_inline)) {
+      if (tid < HGM * RT) {
+        s_lse[st][tid / RT][tid % RT] = l;
+        s_d[st][tid / RT][tid % RT] = dd;
+      }
+      if (tid < RT) {
+        const int i = c_start + (j / n_g) * RT + tid;
+        s_lim[st][tid] = i <= c_end ? i : -1;
+        s_lo[st][tid] = win_lo(i, a.q_block, a.window);
+      }
+    };
+    if (n_steps > 0) {
+      float l, dd;
+      stat_load(0, l, dd);
+      issue(0, 0);
+      stat_store(0, 0, l, dd);
+      wait_dma();
       __syncthreads();
+      for (int j = 0; j < n_steps; ++j) {
+        const int st = j & 1;
+        const bool more = j + 1 < n_steps;
+        // stage st ^ 1 was last read in step j - 1, before the barrier
+        if (more) {
+          stat_load(j + 1, l, dd);
+          issue(j + 1, st ^ 1);
+        }
+        compute(st, c_start + (j / n_g) * RT, min(HGM, a.G - (j % n_g) * HGM));
+        if (more) stat_store(j + 1, st ^ 1, l, dd);
+        wait_dma();
+        __syncthreads();
+      }
     }
   }
 
