@@ -24,9 +24,9 @@
 //     summed by dq_reduce_kernel.
 //   * dkdv_kernel: one workgroup per 128 keys (32 per wave, K and V fragments
 //     in registers) and a chunk of the rows that see them; per 32-row tile and
-//     query head it stages Q, dO, lse and rowsum(dO * O) in LDS (key-sparse
-//     rows: by buffer-load DMA into two stages, the next tile's rows in flight
-//     under this tile's products) and forms
+//     query head it stages Q, dO, lse and rowsum(dO * O) in LDS (by
+//     buffer-load DMA into two stages, the next tile's rows in flight under
+//     this tile's products; selected rows' q rows gathered per lane) and forms
 //     S = Q K^T, dP = dO V^T (rows x keys), then dV^T += dO^T P and
 //     dK^T += Q^T dS from transposed LDS reads. Sink keys are seen by every
 //     later row, so their row range is cut into chunks like any other; each
@@ -79,6 +79,7 @@ struct BwdArgs {
   const int64_t* q_rows;         // selected rows: q row of list position i
   const int64_t* row_last;       // selected rows: last visible key, ascending
   int accumulate;                // outputs: out = rnd(out + rnd(grad))
+  int q32;                       // selected rows: every q row of a head within 32-bit byte offsets
   // dq kernel
   int n_mtiles, n_splits, chunk;
   float* dq_part;                // [item][BM][D] when n_splits > 1
@@ -436,15 +437,12 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
   using E = Elt<T>;
   constexpr int NDS = D / 16, NDT = D / 32, DCH = D / 8, RB = 2 * D;
   constexpr int TB = RT * RB;
-  // Q and dO rows of HGM query heads per step. Selected rows (gathered Q
-  // rows): up to 8 heads (all of a KV head's query heads for GQA up to 8) in
-  // one stage filled through registers, so one load round trip and one
-  // barrier pair serve that many heads' products. Key-sparse rows (contiguous
-  // list positions): 4 heads per step in two stages filled by buffer-load
-  // DMA, the next step's rows landing while this step's products run.
-  constexpr int HGM = ROWS ? 8 : 4;
-  constexpr int NSTG = ROWS ? 1 : 2;
-  static_assert(NSTG * HGM == 8, "same LDS footprint for both staging forms");
+  // Q and dO rows of HGM = 4 query heads per step in two LDS stages filled by
+  // buffer-load DMA, the next step's rows landing while this step's products
+  // run. Selected rows whose q tensor does not fit 32-bit offsets fall back
+  // to one stage filled through registers.
+  constexpr int HGM = 4;
+  constexpr int NSTG = 2;
   __shared__ __attribute__((aligned(1024))) char smem[NSTG][2][HGM][TB];   // [stage][Q, dO][head]
   __shared__ __attribute__((aligned(16))) float s_lse[NSTG][HGM][RT], s_d[NSTG][HGM][RT];
   __shared__ __attribute__((aligned(16))) int s_lim[NSTG][RT], s_lo[NSTG][RT];
@@ -589,7 +587,7 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
     }   // heads of the step
   };
 
-  if constexpr (ROWS) {
+  if (ROWS && !a.q32) {
     for (int r0 = c_start; r0 <= c_end; r0 += RT) {
       for (int g0 = 0; g0 < a.G; g0 += HGM) {
         const int hg = min(HGM, a.G - g0);
@@ -637,26 +635,47 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
     // dO rows go to stage j & 1 by DMA: 16-byte chunk slot (c NWAVE + wave)
     // 64 + lane of the stage is [tensor][head][row][position], filled from
     // the source chunk that position holds under the swizzle. One buffer
-    // resource per (tensor, head) covers the step's rows up to the chunk
-    // end, so rows past it (and heads past the group) read as zero.
+    // resource per (tensor, head): key-sparse rows and dO from the step's
+    // first row, with the range ending at the chunk's last row; selected Q
+    // rows from the head's row 0, each lane at its gathered row (prefetched a
+    // step ahead), rows past the chunk end out of range. Rows past the
+    // chunk end and heads past the group read as zero.
     constexpr int NC = 2 * HGM * RT * DCH / NTHR;   // DMA chunks per thread per step
     static_assert(NC * NTHR == 2 * HGM * RT * DCH && (RT * DCH) % 64 == 0, "whole waves per (tensor, head)");
-    const int n_g = (a.G + HGM - 1) / HGM;
-    const int n_steps = c_end >= c_start ? ((c_end - c_start) / RT + 1) * n_g : 0;
-    const uint32_t qrow_b = (uint32_t)(a.qs_s * (int64_t)esz);
-    const uint32_t grow_b = (uint32_t)(a.gs_s * (int64_t)esz);
     // wave instructions per (tensor, head) block of the stage; when the four
     // waves' instructions c NWAVE + wave of one c fall in one block, the
     // block (hence the buffer resource) depends on c only
     constexpr int IPB = RT * DCH / 64;
+    // a lane's Q chunks c cover QR distinct rows: row(c) = (rq0 + c * RPI) % RT
+    constexpr int RPI = NWAVE * 64 / DCH;          // rows per instruction index step
+    constexpr int QR = RT / (RPI % RT == 0 ? RT : (RPI % RT));
+    static_assert(RPI % RT == 0 || RT % (RPI % RT) == 0, "row period");
+    const int rq0 = (wave * 64 + lane) / DCH % RT;
+    const int n_g = (a.G + HGM - 1) / HGM;
+    const int n_steps = c_end >= c_start ? ((c_end - c_start) / RT + 1) * n_g : 0;
+    const uint32_t qrow_b = (uint32_t)(a.qs_s * (int64_t)esz);
+    const uint32_t grow_b = (uint32_t)(a.gs_s * (int64_t)esz);
     const char* qb0 = (const char*)a.q + ((int64_t)b * a.qs_b + (int64_t)hk * a.G * a.qs_h) * esz;
     const char* gb0 = (const char*)a.dout + ((int64_t)b * a.gs_b + (int64_t)hk * a.G * a.gs_h) * esz;
-    auto issue = [&](int j, int st) __attribute__((always_inline)) {
+    // selected rows: the gathered q rows of this lane's QR rows of step j
+    // (-1 past the chunk end)
+    auto qrows_of = [&](int j, int (&qr)[QR]) __attribute__((always_inline)) {
+      if constexpr (ROWS) {
+        const int r0 = c_start + (j / n_g) * RT;
+#pragma unroll
+        for (int u = 0; u < QR; ++u) {
+          const int i = r0 + (rq0 + u * RPI) % RT;
+          qr[u] = i <= c_end ? (int)min(max(a.q_rows[i], (int64_t)0), (int64_t)(a.n_q - 1)) : -1;
+        }
+      }
+    };
+    auto issue = [&](int j, int st, const int (&qr)[QR]) __attribute__((always_inline)) {
       const int r0 = c_start + (j / n_g) * RT, g0 = (j % n_g) * HGM;
       const int hg = min(HGM, a.G - g0);
       const uint32_t nrow = (uint32_t)min(RT, c_end - r0 + 1);
-      const char* qb = qb0 + ((int64_t)g0 * a.qs_h + (int64_t)r0 * a.qs_s) * esz;
+      const char* qb = qb0 + ((int64_t)g0 * a.qs_h + (ROWS ? 0 : (int64_t)r0 * a.qs_s)) * esz;
       const char* gb = gb0 + ((int64_t)g0 * a.gs_h + (int64_t)r0 * a.gs_s) * esz;
+      const uint32_t qrange = ROWS ? (uint32_t)a.n_q * qrow_b : nrow * qrow_b;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int slot = (c * NWAVE + wave) * 64 + lane;
@@ -665,21 +684,36 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
         if constexpr (IPB % NWAVE == 0) blk = c / (IPB / NWAVE);
         else blk = (c * NWAVE + wave) / IPB;
         const int tensor = blk / HGM, gg = blk % HGM;
-        const char* base = tensor == 0 ? qb + (int64_t)gg * a.qs_h * esz : gb + (int64_t)gg * a.gs_h * esz;
-        const uint32_t rb = tensor == 0 ? qrow_b : grow_b;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, gg < hg ? nrow * rb : 0u);
-        dma16(rs, (DA_LDS void*)((DA_LDS char*)&smem[st][0][0][0] + (c * NWAVE + wave) * 1024),
-              (uint32_t)row * rb + (uint32_t)((pc ^ swz<D>(row)) * 16));
+        const uint32_t chunk = (uint32_t)((pc ^ swz<D>(row)) * 16);
+        const char* base;
+        uint32_t range, voff;
+        if (tensor == 0) {
+          base = qb + (int64_t)gg * a.qs_h * esz;
+          range = gg < hg ? qrange : 0u;
+          if constexpr (ROWS) {
+            const int q = qr[c % QR];
+            voff = q >= 0 ? (uint32_t)q * qrow_b + chunk : 0xfffffff0u;
+          } else {
+            voff = (uint32_t)row * qrow_b + chunk;
+          }
+        } else {
+          base = gb + (int64_t)gg * a.gs_h * esz;
+          range = gg < hg ? nrow * grow_b : 0u;
+          voff = (uint32_t)row * grow_b + chunk;
+        }
+        dma16(make_rsrc(base, range), (DA_LDS void*)((DA_LDS char*)&smem[st][0][0][0] + (c * NWAVE + wave) * 1024),
+              voff);
       }
     };
     // row statistics of step j (threads below HGM * RT: head tid / RT, row
-    // tid % RT), loaded a step ahead and stored to its stage after the
-    // current step's products
-    auto stat_load = [&](int j, float& l, float& dd) __attribute__((always_inline)) {
+    // tid % RT; the row limits from threads below RT), loaded a step ahead
+    // and stored to its stage after the current step's products
+    auto stat_load = [&](int j, float& l, float& dd, int& lim) __attribute__((always_inline)) {
       l = INFINITY;
       dd = 0.f;
+      lim = -1;
+      const int r0 = c_start + (j / n_g) * RT, g0 = (j % n_g) * HGM;
       if (tid < HGM * RT) {
-        const int r0 = c_start + (j / n_g) * RT, g0 = (j % n_g) * HGM;
         const int gg = tid / RT, i = r0 + tid % RT;
         if (i <= c_end && g0 + gg < a.G) {
           const int64_t rix = ((int64_t)b * a.Hq + hk * a.G + g0 + gg) * a.n_rows + i;
@@ -687,23 +721,37 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
           dd = a.dvec[rix];
         }
       }
+      if (tid < RT) {
+        const int i = r0 + tid;
+        if (i <= c_end) {
+          if constexpr (ROWS) {
+            const int64_t lr = min(a.row_last[i], (int64_t)(a.n_kv - 1));
+            lim = (int)(lr < -1 ? -1 : lr);
+          } else {
+            lim = i;
+          }
+        }
+      }
     };
-    auto stat_store = [&](int j, int st, float l, float dd) __attribute__((always_inline)) {
+    auto stat_store = [&](int j, int st, float l, float dd, int lim) __attribute__((always_inline)) {
       if (tid < HGM * RT) {
         s_lse[st][tid / RT][tid % RT] = l;
         s_d[st][tid / RT][tid % RT] = dd;
       }
       if (tid < RT) {
-        const int i = c_start + (j / n_g) * RT + tid;
-        s_lim[st][tid] = i <= c_end ? i : -1;
-        s_lo[st][tid] = win_lo(i, a.q_block, a.window);
+        s_lim[st][tid] = lim;
+        s_lo[st][tid] = ROWS ? 0 : win_lo(c_start + (j / n_g) * RT + tid, a.q_block, a.window);
       }
     };
     if (n_steps > 0) {
       float l, dd;
-      stat_load(0, l, dd);
-      issue(0, 0);
-      stat_store(0, 0, l, dd);
+      int lim;
+      int qr[QR], qn[QR];
+      qrows_of(0, qr);
+      stat_load(0, l, dd, lim);
+      if (n_steps > 1) qrows_of(1, qn);
+      issue(0, 0, qr);
+      stat_store(0, 0, l, dd, lim);
       wait_dma();
       __syncthreads();
       for (int j = 0; j < n_steps; ++j) {
@@ -711,11 +759,14 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
         const bool more = j + 1 < n_steps;
         // stage st ^ 1 was last read in step j - 1, before the barrier
         if (more) {
-          stat_load(j + 1, l, dd);
-          issue(j + 1, st ^ 1);
+#pragma unroll
+          for (int u = 0; u < QR; ++u) qr[u] = qn[u];
+          if (j + 2 < n_steps) qrows_of(j + 2, qn);
+          stat_load(j + 1, l, dd, lim);
+          issue(j + 1, st ^ 1, qr);
         }
         compute(st, c_start + (j / n_g) * RT, min(HGM, a.G - (j % n_g) * HGM));
-        if (more) stat_store(j + 1, st ^ 1, l, dd);
+        if (more) stat_store(j + 1, st ^ 1, l, dd, lim);
         wait_dma();
         __syncthreads();
       }
@@ -1100,6 +1151,9 @@ extern "C" int da_qsparse_attn_bwd(const void* q, const void* k, const void* v, 
                     dtype);
   if (rc != DA_OK) return rc;
   a.q_rows = q_rows; a.row_last = row_last;
+  // the dK/dV kernel's DMA addresses a head's gathered q rows from its row 0
+  // with 32-bit byte offsets (else it stages them through registers)
+  a.q32 = (uint64_t)a.n_q * (uint64_t)a.qs_s * 2u <= 0xfffff000ull;
   a.window = 0; a.sink = 0; a.q_block = 1;
   const int bn = D == 128 ? 32 : 64;
   const DqPlan dqp = plan_dq(B, Hkv, a.G, n, ((int64_t)Skv + bn - 1) / bn, true);

@@ -142,3 +142,34 @@ def test_full_size_properties(gpu):
     for a, b in zip(grads[0][1:], grads[1][1:]):
         assert torch.isfinite(a).all()
         assert torch.equal(a * 2, b)
+
+
+def test_rows_bwd_q_rows_past_32bit_offsets(gpu):
+    """Selected-rows backward with q rows spread over more than 4 GB (a view
+    with a 4M-element row stride): the dK/dV kernel cannot address a head's
+    gathered q rows with 32-bit offsets from its row 0, stages them through
+    registers instead of by DMA, and gives the bits of a contiguous copy."""
+    from delta_attention import ops
+    B, H, Hkv, Sq, D = 1, 4, 2, 600, 128
+    print("rows backward: q rows past 32-bit offsets", flush=True)
+    g = torch.Generator().manual_seed(5)
+    qc = torch.randn(B, H, Sq, D, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(B, Hkv, Sq, D, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(B, Hkv, Sq, D, generator=g).to(torch.bfloat16).cuda()
+    rows = torch.arange(3, Sq, 7, dtype=torch.int64).cuda()
+    scale = D ** -0.5
+    out, lse = ops.rows_attention_lse(qc, k, v, rows, scale)
+    dout = torch.randn(out.shape, generator=g).to(torch.bfloat16).cuda()
+    stride = 4_000_000                      # elements per q row: Sq * stride * 2 B = 4.8 GB
+    buf = torch.empty(Sq * stride, dtype=torch.bfloat16, device="cuda")
+    qv = buf.as_strided((B, H, Sq, D), (Sq * stride, D, stride, 1))
+    qv.copy_(qc)
+    res = []
+    for qq in (qc, qv):
+        dq = torch.zeros(B, H, Sq, D, dtype=torch.bfloat16, device="cuda")
+        res.append(ops.rows_attention_bwd(qq, k, v, rows, out, dout, lse, sm_scale=scale, dq=dq))
+    torch.cuda.synchronize()
+    del buf, qv
+    for a, b in zip(*res):
+        assert torch.isfinite(a).all()
+        assert torch.equal(a, b)
