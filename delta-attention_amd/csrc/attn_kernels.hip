@@ -65,6 +65,12 @@ namespace da {
 #ifndef DA_ROWS_MIN_TILES
 #define DA_ROWS_MIN_TILES 56
 #endif
+// Longest split item of a selected-rows launch, in key tiles: past 256K keys
+// the item target alone would give items of thousands of tiles, and the
+// longest ones, dispatched last, would run alone at the end of the launch.
+#ifndef DA_ROWS_MAX_TILES
+#define DA_ROWS_MAX_TILES 512
+#endif
 // Split items a decode-row launch aims for: one workgroup per resident slot
 // of the 256-CU gfx950 (two per CU), so the items run in a single round
 // (dense row over 131072 keys: 106-111 us against 118 us at 1024 items and
@@ -1315,7 +1321,7 @@ constexpr int64_t MERGE_WGS_MAX = (int64_t)BM_MAX * (256 / 8) * 16 / MTHR;
 // item takes `chunk` consecutive tiles of it (at least `min_chunk`); `target`
 // items in total.
 static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int D, int target,
-                                int min_chunk, int bm) {
+                                int min_chunk, int bm, int max_chunk = 0x7fffffff) {
   QsparsePlan p;
   const int G = Hq / Hkv;
   p.bm = bm;
@@ -1326,6 +1332,7 @@ static QsparsePlan plan_qsparse(int B, int Hq, int Hkv, int n, int64_t vis, int 
   if (want < 1) want = 1;
   if (want > vis) want = vis;
   p.chunk = (int)((vis + want - 1) / want);
+  if (p.chunk > max_chunk) p.chunk = max_chunk;
   if (p.chunk < min_chunk) p.chunk = (int)min((int64_t)min_chunk, vis);
   p.n_splits = (int)((vis + p.chunk - 1) / p.chunk);
   const int64_t items = base * p.n_splits;
@@ -1352,7 +1359,7 @@ static QsparsePlan plan_rows(int B, int Hq, int Hkv, int n, int Skv, int D) {
   const int bm = rows_bm(D);
   const int64_t tiles = (int64_t)B * Hkv * (((int64_t)n * (Hq / Hkv) + bm - 1) / bm);
   if (tiles < 64) return plan_qsparse(B, Hq, Hkv, n, vis, D, 1024, 16, bm);
-  return plan_qsparse(B, Hq, Hkv, n, vis, D, DA_ROWS_ITEMS, DA_ROWS_MIN_TILES, bm);
+  return plan_qsparse(B, Hq, Hkv, n, vis, D, DA_ROWS_ITEMS, DA_ROWS_MIN_TILES, bm, DA_ROWS_MAX_TILES);
 }
 
 // Split plan for n rows of which about n_live hold keys (the others are -1
