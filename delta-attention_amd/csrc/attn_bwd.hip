@@ -15,8 +15,9 @@
 // Two kernels per attention:
 //   * dq_kernel: one workgroup per 128 flattened (row, head) pairs (the G
 //     query heads of a KV head packed, as in the forward) and a chunk of their
-//     key-tile list; K and V tiles arrive in LDS by buffer-load DMA through a
-//     three-stage ring (two tiles in flight), tiles wholly visible skip the
+//     key-tile list; 64-key K and V tiles arrive in LDS by buffer-load DMA
+//     through a ring (head_dim 128: two stages, each tile's two 32-key halves
+//     computed in turn; else three stages), tiles wholly visible skip the
 //     per-key mask; S^T = K Q^T and dP^T = V dO^T
 //     with Q and dO fragments in registers, dQ^T += K^T dS^T from transposed
 //     LDS reads. It also writes rowsum(dO * O) for the other kernel. Long
@@ -44,10 +45,11 @@ namespace bwd {
 constexpr int NWAVE = 4;
 constexpr int NTHR = 64 * NWAVE;
 constexpr int BM = 32 * NWAVE;   // dq kernel: flattened (row, head) pairs per workgroup
-// dq kernel: keys per tile (32 at head_dim 128 keeps the score registers
-// small enough for two waves per SIMD; 64 otherwise)
+// dq kernel: keys per tile (at head_dim 128 computed as two 32-key halves one
+// after the other, which keeps the score registers small enough for two waves
+// per SIMD)
 template <int D>
-constexpr int dq_bn() { return D == 128 ? 32 : 64; }
+constexpr int dq_bn() { return 64; }
 constexpr int KT = 32 * NWAVE;   // dkdv kernel: keys per workgroup
 constexpr int RT = 32;           // dkdv kernel: rows per step
 constexpr int RPC_MAX = 4096;    // dkdv kernel: rows per chunk at most
@@ -148,7 +150,7 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-constexpr int NST = 3;   // LDS stages of the dq kernel's DMA ring
+constexpr int NST = 3;   // LDS stages of the dq kernel's DMA ring (head_dim < 128)
 
 template <typename T>
 __device__ __forceinline__ uint32_t acc_pack(uint32_t old, float lo, float hi, bool accumulate) {
@@ -162,12 +164,16 @@ template <typename T, int D, bool ROWS>
 __global__ __launch_bounds__(NTHR, 2) void dq_kernel(BwdArgs a) {
   using E = Elt<T>;
   constexpr int BN = dq_bn<D>(), NH = BN / 32;
+  // head_dim 128: two stages of 64-key tiles whose 32-key halves are computed
+  // one after the other (the score registers of one half); else three stages
+  constexpr int NSQ = D == 128 ? 2 : NST;
+  constexpr bool SEQH = D == 128;
   constexpr int NDS = D / 16, NDT = D / 32, DCH = D / 8, RB = 2 * D;
   constexpr int TB = BN * RB;
   constexpr int NLD = TB / (NTHR * 16);   // 16-byte DMA chunks per thread per K (or V) tile
   static_assert(NLD >= 1, "tile load");
   // [stage][K, V][tile]
-  __shared__ __attribute__((aligned(1024))) char smem[NST][2][TB];
+  __shared__ __attribute__((aligned(1024))) char smem[NSQ][2][TB];
   __shared__ int red[4][NWAVE];
   const size_t esz = sizeof(T);
 
@@ -299,27 +305,36 @@ __global__ __launch_bounds__(NTHR, 2) void dq_kernel(BwdArgs a) {
   int tro[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) tro[dt] = tr_offset<D>(lane, dt);
-  // ring of NST stages: tiles t + 1 and t + 2 are in flight while tile t is
-  // consumed (the stage tile t + 2 lands in was last read in step t - 1,
-  // before its barrier); each issue is 2 NLD DMAs per lane
+  // ring of NSQ stages: with three, tiles t + 1 and t + 2 are in flight while
+  // tile t is consumed (the stage tile t + 2 lands in was last read in step
+  // t - 1, before its barrier); with two (head_dim 128, 64 KB of LDS for two
+  // workgroups per CU), tile t + 1 is; each issue is 2 NLD DMAs per lane
   if (nt > 0) {
     issue(0, 0);
-    if (nt > 1) issue(1, 1);
-    if (nt > 1) wait_vm<2 * NLD>();
+    if (NSQ == 3 && nt > 1) issue(1, 1);
+    if (NSQ == 3 && nt > 1) wait_vm<2 * NLD>();
     else wait_dma();
     __syncthreads();
   }
   for (int t = 0; t < nt; ++t) {
     const int n0 = tile_n0(t);
-    if (t + 2 < nt) issue(t + 2, (t + 2) % NST);
-    const DA_LDS char* ks = (const DA_LDS char*)&smem[t % NST][0][0];
-    const DA_LDS char* vs = (const DA_LDS char*)&smem[t % NST][1][0];
+    if (NSQ == 3) {
+      if (t + 2 < nt) issue(t + 2, (t + 2) % NSQ);
+    } else {
+      if (t + 1 < nt) issue(t + 1, (t + 1) % NSQ);
+    }
+    const DA_LDS char* ks = (const DA_LDS char*)&smem[t % NSQ][0][0];
+    const DA_LDS char* vs = (const DA_LDS char*)&smem[t % NSQ][1][0];
+    const int n1 = n0 + BN - 1;
+    const bool full = n1 <= hi_min && n1 < a.n_kv && (n1 < sink || n0 >= lo_max);
+    auto halves = [&](int h0, auto nh_c) __attribute__((always_inline)) {
+    constexpr int NHH = decltype(nh_c)::value;
 
     // S^T = K Q^T and dP^T = V dO^T; element j of half hf is key
     // n0 + 32 hf + 16 (j / 8) + 8 lg + j % 8 (rows sigma(ln) of the A tiles)
-    f32x16 x[NH], y[NH];
+    f32x16 x[NHH], y[NHH];
 #pragma unroll
-    for (int hf = 0; hf < NH; ++hf)
+    for (int hf = 0; hf < NHH; ++hf)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         x[hf][j] = 0.f;
@@ -328,24 +343,21 @@ __global__ __launch_bounds__(NTHR, 2) void dq_kernel(BwdArgs a) {
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds)
 #pragma unroll
-      for (int hf = 0; hf < NH; ++hf) {
-        const int r = sigma32(ln) + 32 * hf;
+      for (int hf = 0; hf < NHH; ++hf) {
+        const int r = sigma32(ln) + 32 * (h0 + hf);
         x[hf] = E::mfma(read_rows<D>(ks, r, ds, lg), qf[ds], x[hf]);
         y[hf] = E::mfma(read_rows<D>(vs, r, ds, lg), df[ds], y[hf]);
       }
-    // every key of the tile visible to every valid row: no per-key test
-    const int n1 = n0 + BN - 1;
-    const bool full = n1 <= hi_min && n1 < a.n_kv && (n1 < sink || n0 >= lo_max);
-    uint32_t dsp[8 * NH];
+    uint32_t dsp[8 * NHH];
 #pragma unroll
-    for (int hf = 0; hf < NH; ++hf)
+    for (int hf = 0; hf < NHH; ++hf)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         float d2[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const int jj = 2 * j + e;
-          const int key = n0 + 32 * hf + 16 * (jj >> 3) + 8 * lg + (jj & 7);
+          const int key = n0 + 32 * (h0 + hf) + 16 * (jj >> 3) + 8 * lg + (jj & 7);
           const bool vis = full || (key <= hi && (key < sink || key >= lo));
           const float p = vis ? fast_exp2(fmaf(x[hf][jj], c2, -lse)) : 0.f;
           d2[e] = p * (y[hf][jj] - Di);
@@ -354,13 +366,20 @@ __global__ __launch_bounds__(NTHR, 2) void dq_kernel(BwdArgs a) {
       }
     // dQ^T += K^T dS^T
 #pragma unroll
-    for (int kk = 0; kk < 2 * NH; ++kk) {
+    for (int kk = 0; kk < 2 * NHH; ++kk) {
       const u32x4 sf = {dsp[4 * kk], dsp[4 * kk + 1], dsp[4 * kk + 2], dsp[4 * kk + 3]};
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) acc[dt] = E::mfma(read_tr<D>(ks, tro[dt], kk), sf, acc[dt]);
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] = E::mfma(read_tr<D>(ks, tro[dt], 2 * h0 + kk), sf, acc[dt]);
     }
-    // tile t + 1 must have landed (tile t + 2 may still be in flight)
-    if (t + 2 < nt) wait_vm<2 * NLD>();
+    };
+    if constexpr (SEQH) {
+#pragma unroll
+      for (int h = 0; h < NH; ++h) halves(h, std::integral_constant<int, 1>());
+    } else {
+      halves(0, std::integral_constant<int, NH>());
+    }
+    // tile t + 1 must have landed (three stages: tile t + 2 may still be in flight)
+    if (NSQ == 3 && t + 2 < nt) wait_vm<2 * NLD>();
     else wait_dma();
     __syncthreads();
   }
