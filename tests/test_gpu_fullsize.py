@@ -1,7 +1,8 @@
 """Parity at the benchmark configurations' full sizes (Llama-3.1-8B shape at 32K
 and 128K tokens, the 128K stride sweep gamma 16 / 32 / 64 / 128, Qwen3-14B shape
 at 64K with batch 2 and GQA 5, and the 32-layer random-init Llama-3.1-8B model
-prefilling 131072 tokens), where the oracle cannot run whole layers:
+prefilling 131072 tokens, and the reference's long-context geometry at 1M tokens),
+where the oracle cannot run whole layers:
 
 * exact, size-independent composition over EVERY row: the delta output equals
   rnd(sparse + rnd(dense[anchor] - sparse[anchor])) recomputed with torch bf16
@@ -35,6 +36,11 @@ CONFIGS = {
                             theta=500000.0, qk_norm=False, q_scale=True),
     "qwen3-64k-b2": dict(B=2, H=40, Hkv=8, S=65536, D=128, window=4096, sink=64, gamma=64,
                          theta=1000000.0, qk_norm=True, q_scale=False),
+    # the reference's published long-context geometry (1024 sinks) at 1M tokens:
+    # kernel (2)'s items at their 512-tile cap, 32 splits per row tile
+    "llama-1m-sink1024": dict(B=1, H=32, Hkv=8, S=1048576, D=128, window=2048, sink=1024,
+                              gamma=64, theta=500000.0, qk_norm=False, q_scale=True,
+                              dense_sample=4),
 }
 
 
@@ -42,12 +48,12 @@ def _f32(t):
     return t.detach().float().cpu().numpy()
 
 
-def check_layer(q, k, v, out, window, sink, gamma, name, dense_sample=8):
+def check_layer(q, k, v, out, window, sink, gamma, name, dense_sample=8, kv_groups=None):
     """The size-independent checks of one delta layer output `out` [B,S,H,D]
     computed from q [B,H,S,D], k/v [B,Hkv,S,D]: exact index set, exact bf16
     composition over every row against the sparse-only and recompute outputs,
     and sampled sparse / dense rows of every kv-head group of every batch
-    against the oracle (float32 on the same bf16 inputs)."""
+    (or of `kv_groups`) against the oracle (float32 on the same bf16 inputs)."""
     from delta_attention import ops
     B, H, S, D = q.shape
     Hkv = k.shape[1]
@@ -85,7 +91,7 @@ def check_layer(q, k, v, out, window, sink, gamma, name, dense_sample=8):
     drows = np.unique(np.concatenate([anchors[[0, 1, len(anchors) // 2, -1]], tail[[0, -1]],
                                       rng.choice(anchors, dense_sample)]))
     for b in range(B):
-        for hk in range(Hkv):
+        for hk in (range(Hkv) if kv_groups is None else kv_groups):
             hs = slice(hk * G, (hk + 1) * G)
             kk = _f32(k[b:b + 1, hk:hk + 1])
             vv = _f32(v[b:b + 1, hk:hk + 1])
@@ -109,7 +115,8 @@ def test_fullsize_layer(gpu, name):
                               q_scale=c["q_scale"])
     out = ops.delta_prefill(q, k, v, mode="delta", gamma=c["gamma"], window=c["window"],
                             sink=c["sink"], sm_scale=D ** -0.5)
-    check_layer(q, k, v, out, c["window"], c["sink"], c["gamma"], name)
+    check_layer(q, k, v, out, c["window"], c["sink"], c["gamma"], name,
+                dense_sample=c.get("dense_sample", 8), kv_groups=c.get("kv_groups"))
 
 
 def test_fullsize_model_prefill_llama8b_128k(gpu):
