@@ -1639,12 +1639,18 @@ static int run_qsparse(const QsparsePlan& p, const void* q, const void* k, const
   m.n_splits = p.n_splits; m.chunk = p.chunk; m.n_kv_dev = n_kv_dev;
   m.B = B; m.n_rows_dev = n_rows_dev;
   m.window = window; m.sink = sink;
-  // P threads per (row, column chunk) task: about 4 splits each, up to 16;
-  // workgroups per row tile cover its valid rows only
-  m.lanes = 1;
-  while (m.lanes < 16 && m.lanes * 4 < p.n_splits) m.lanes <<= 1;
+  // P threads per (row, column chunk) task: about 4 splits each, up to 16,
+  // but no more threads than about half the GPU holds (2^18): a merge with
+  // that many tasks already has enough loads in flight with one lane each,
+  // and more lanes only add rounds of waves (128K layer: 36 us at one lane
+  // vs 62 us at four; 32K: 11 vs 20 us), while a few decode rows need the
+  // lanes; workgroups per row tile cover its valid rows only
   {
     const int64_t rows = min((int64_t)p.bm, (int64_t)n * a.G);
+    const int64_t tasks = (int64_t)B * Hkv * p.n_mtiles * rows * (D / 8);
+    m.lanes = 1;
+    while (m.lanes < 16 && m.lanes * 4 < p.n_splits) m.lanes <<= 1;
+    while (m.lanes > 1 && tasks * m.lanes > (1 << 18)) m.lanes >>= 1;
     m.wgs = (int)((rows * (D / 8) * m.lanes + MTHR - 1) / MTHR);
   }
   m.part_o = a.part_o; m.part_ml = a.part_ml; m.ws_rows = p.ws_rows; m.bm = p.bm;
