@@ -34,6 +34,7 @@
 //     chunk writes fp32 partials that dkdv_reduce_kernel sums per key.
 // Every MFMA is v_mfma_f32_32x32x16 (bf16 or fp16 operands, fp32 accumulate).
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "device_common.h"
@@ -52,7 +53,7 @@ template <int D>
 constexpr int dq_bn() { return 64; }
 constexpr int KT = 32 * NWAVE;   // dkdv kernel: keys per workgroup
 constexpr int RT = 32;           // dkdv kernel: rows per step
-constexpr int RPC_MAX = 4096;    // dkdv kernel: rows per chunk at most
+constexpr int RPC_MAX = 8192;    // dkdv kernel: rows per chunk at most (default)
 constexpr int RED = 256;         // threads of the reduce / compose kernels
 
 struct BwdArgs {
@@ -971,21 +972,32 @@ struct KvPlan {
   int n_blk, nsb, ncs, nco, rpc, items_per_bh;
 };
 
+// Rows per dK/dV chunk at most (process-wide; da_set_bwd_rows_per_chunk).
+static std::atomic<int> g_rpc_max{RPC_MAX};
+
+// A block's rows are cut into equal chunks of at most the cap: with a fixed
+// chunk of the cap, a span just past it left a chunk of a few rows per block
+// (window 4096: 4096 + 128 rows), each a whole item with its K/V loads and
+// dK/dV partials (Qwen3 64K x 2 backward 102 ms; 66 ms with one 4224-row
+// chunk per block).
 KvPlan plan_kv(int n_rows, int n_kv, int window, int sink, bool rows) {
   KvPlan p;
   p.n_blk = (n_kv + KT - 1) / KT;
+  const int64_t cap = g_rpc_max.load(std::memory_order_relaxed);
   auto up = [](int64_t x) { return (int)(((x + RT - 1) / RT) * RT); };
+  auto split = [&](int64_t span, int& rpc, int& n) {
+    span = std::max<int64_t>(span, 1);
+    const int64_t k = (span + cap - 1) / cap;
+    rpc = up((span + k - 1) / k);
+    n = (int)((span + rpc - 1) / rpc);
+  };
   if (rows) {
     p.nsb = 0;
-    p.rpc = up(std::min<int64_t>(std::max(n_rows, 1), RPC_MAX));
+    split(n_rows, p.rpc, p.nco);
     p.ncs = 1;
-    p.nco = (n_rows + p.rpc - 1) / p.rpc;
-    if (p.nco < 1) p.nco = 1;
   } else {
     p.nsb = std::min(p.n_blk, (sink + KT - 1) / KT);
-    const int64_t span = (int64_t)KT + window;   // rows a non-sink block can need
-    p.rpc = up(std::min<int64_t>(std::max<int64_t>(span, 1), RPC_MAX));
-    p.nco = (int)((span + p.rpc - 1) / p.rpc);
+    split((int64_t)KT + window, p.rpc, p.nco);   // rows a non-sink block can need
     p.ncs = (n_rows + p.rpc - 1) / p.rpc;
     if (p.ncs < 1) p.ncs = 1;
   }
@@ -1086,6 +1098,13 @@ int bwd_args(BwdArgs& a, const void* q, const void* k, const void* v, const void
 }
 
 }  // namespace
+
+extern "C" int da_set_bwd_rows_per_chunk(int rows) {
+  if (rows == 0) rows = RPC_MAX;
+  if (rows < RT || rows % RT != 0 || rows > (1 << 20)) return DA_ERR_INVALID_ARG;
+  g_rpc_max.store(rows, std::memory_order_relaxed);
+  return DA_OK;
+}
 
 extern "C" size_t da_sparse_attn_bwd_workspace_bytes(int B, int Hq, int Hkv, int S, int D,
                                                      int window, int sink, int q_block) {

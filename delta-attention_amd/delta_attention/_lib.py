@@ -63,6 +63,7 @@ EXPORTS = (
     "da_adapt_layer_fwd",
     "da_set_sparse_rows_per_wave",
     "da_sparse_rows_per_wave",
+    "da_set_bwd_rows_per_chunk",
 )
 
 _ERR_TEXT = {
@@ -130,6 +131,8 @@ def _load() -> ctypes.CDLL:
     L.da_set_sparse_rows_per_wave.argtypes = [_i]
     L.da_sparse_rows_per_wave.restype = _i
     L.da_sparse_rows_per_wave.argtypes = []
+    L.da_set_bwd_rows_per_chunk.restype = _i
+    L.da_set_bwd_rows_per_chunk.argtypes = [_i]
     L.da_qsparse_workspace_bytes.restype = _sz
     L.da_qsparse_workspace_bytes.argtypes = [_i, _i, _i, _i, _i, _i]
     L.da_qsparse_attn_fwd.restype = _i

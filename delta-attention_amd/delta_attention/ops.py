@@ -112,6 +112,14 @@ def set_sparse_rows_per_wave(rows: int) -> int:
     return prev
 
 
+def set_bwd_rows_per_chunk(rows: int) -> None:
+    """Rows per dK/dV work item at most in the training backward,
+    process-wide (0: the default, 8192). Set it before the backward's
+    workspace is sized; results agree to the rounding of the chunks'
+    partial sums."""
+    L.check(L.lib().da_set_bwd_rows_per_chunk(int(rows)), "da_set_bwd_rows_per_chunk")
+
+
 def sparse_attention_delta(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, window: int,
                            sink: int, sm_scale: float, dense_sel: torch.Tensor, gamma: int,
                            s_p: int, out: torch.Tensor, delta_out: Optional[torch.Tensor] = None,

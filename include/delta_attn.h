@@ -483,6 +483,18 @@ int da_qsparse_attn_fwd_lse(const void* q, const void* k, const void* v,
  * query heads); accumulate != 0 adds them instead: x = rnd(x + rnd(grad)).
  * Workspace: da_sparse_attn_bwd_workspace_bytes.
  */
+/*
+ * Rows per dK/dV work item at most in the two backward entry points below
+ * (a key block's rows are cut into equal chunks of at most this many; the
+ * chunks' fp32 partials are summed by a reduce launch): a positive multiple
+ * of 32 up to 2^20, or 0 for the default 8192. Process-wide, read when a
+ * plan is made: set it before the workspace queries (the workspace follows
+ * the chunk count). Results agree to the rounding of the partial sums. No
+ * counterpart in the reference: a work-split knob of this implementation,
+ * which the tests use to drive the multi-chunk paths at small sizes.
+ */
+int da_set_bwd_rows_per_chunk(int rows);
+
 size_t da_sparse_attn_bwd_workspace_bytes(int B, int Hq, int Hkv, int S, int D,
                                           int window, int sink, int q_block);
 int da_sparse_attn_bwd(const void* q, const void* k, const void* v, const void* o,

@@ -79,6 +79,34 @@ def test_delta_forward_train_grads(gpu, c):
     _grad_close(vv.grad, dv, "dv", (br1[2], br2[2]))
 
 
+@pytest.mark.parametrize("c", [CASES[0], CASES[2], CASES[4]],
+                         ids=lambda c: "-".join(str(x).replace("torch.", "") for x in c))
+def test_delta_forward_train_grads_in_row_chunks(gpu, c):
+    """The same gradients with every key block's rows cut into 64-row dK/dV
+    items (the default cap of 8192 rows gives one item per block at these
+    sizes): the sink blocks' row chunks, several chunks per window block and
+    per selected-row list, and the reduce over their fp32 partials."""
+    from delta_attention import ops
+    from delta_attention.train.flex_delta import delta_forward_train
+    B, H, Hkv, S, D, gamma, window, sink, dtype, arm = c
+    print(f"train case {c}, 64-row chunks", flush=True)
+    q, k, v, up = _inputs(B, H, Hkv, S, D, seed=S + D + H + 1, dtype=dtype)
+    scale = D ** -0.5
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    ops.set_bwd_rows_per_chunk(64)
+    try:
+        out = delta_forward_train(qq, kk, vv, gamma, window, sink, scale)
+        out.backward(up)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_bwd_rows_per_chunk(0)
+    (dq, dk, dv), br1, br2 = O.delta_train_grads(np64(q), np64(k), np64(v), gamma, window, sink,
+                                                 scale, np64(up), parts=True)
+    _grad_close(qq.grad, dq, "dq", (br1[0], br2[0]))
+    _grad_close(kk.grad, dk, "dk", (br1[1], br2[1]))
+    _grad_close(vv.grad, dv, "dv", (br1[2], br2[2]))
+
+
 def test_forward_row_statistics(gpu):
     """lse of both forward kernels against the oracle's log2-sum-exp2 of the
     scaled scores (every visible key; +inf for rows without one)."""
