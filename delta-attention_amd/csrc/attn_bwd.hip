@@ -108,8 +108,21 @@ __device__ __forceinline__ int sigma32(int r) {
 }
 
 // LDS rows of D elements; 16-byte chunk c of row r sits at chunk c ^ swz(r).
+// The tiles are read two ways: 16-byte row pieces (16 lanes, 16 rows r0 ..
+// r0 + 15 in some order, one chunk) and transposed 8-byte reads (4
+// consecutive rows 4m .. 4m + 3 x chunks 4 dt .. 4 dt + 3). A row read is
+// conflict-free when the 16 rows land on 16 distinct 16-byte bank columns, a
+// transposed read when the 4 rows' swizzles differ above bit 1. Bank column
+// of (r, c): (r DCH + (c ^ swz(r))) mod 16. head_dim 128 (one row per bank
+// row): the two 2-bit halves of r & 15 swapped; 64 (two rows per bank row):
+// bit 2 from r bit 1, bits 0-1 from r bits 2-3; 32 (four): r bits 2-3.
+// (4 (r & 3) alone left the row reads 4-way, at head_dim 64 8-way, in conflict.)
 template <int D>
-__device__ __forceinline__ int swz(int row) { return (4 * (row & 3)) & (D / 8 - 1); }
+__device__ __forceinline__ int swz(int row) {
+  if constexpr (D == 128) return ((row & 3) << 2) | ((row >> 2) & 3);
+  else if constexpr (D == 64) return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
+  else return (row >> 2) & 3;
+}
 
 // A-operand fragment (32 rows x 16 dims, k-step ds) of a row-major LDS tile:
 // lane (ln, lg) reads row `row`, dims 16 ds + 8 lg .. +7.
@@ -128,10 +141,13 @@ __device__ __forceinline__ int tr_offset(int lane, int dt) {
   const int lc = 4 * dt + 2 * hh + ((j & 3) >> 1);
   return row * (2 * D) + ((lc ^ swz<D>(row)) * 16) + (j & 1) * 8;
 }
+// The second read's rows are 4 on: their (r >> 2) is odd where the first
+// read's is even, which under swz flips chunk bit 0 (address bit 4); 16 rows
+// on, swz repeats.
 template <int D>
 __device__ __forceinline__ u32x4 read_tr(const DA_LDS char* t, int off, int kk) {
   const u32x2 a = read_tr16(t + off + (16 * kk) * (2 * D));
-  const u32x2 b = read_tr16(t + off + (16 * kk + 4) * (2 * D));
+  const u32x2 b = read_tr16(t + (off ^ 16) + (16 * kk + 4) * (2 * D));
   return (u32x4){a[0], a[1], b[0], b[1]};
 }
 
