@@ -577,10 +577,23 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
         y[j] = 0.f;
       }
       const int r = sigma32(ln);
+      // Each MFMA pair's LDS fragments are read one pair ahead: at one wave
+      // per SIMD nothing else hides a fragment read's latency, and read right
+      // before its MFMA every pair waited for it (backward 35.6 -> 31.8 ms at
+      // 128K keys; pinned by scheduling barriers it was slower, 37.7 ms)
+      {
+        u32x4 qa[2], ga[2];
+        qa[0] = read_rows<D>(qs, r, 0, lg);
+        ga[0] = read_rows<D>(gs, r, 0, lg);
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) {
-        x = E::mfma(read_rows<D>(qs, r, ds, lg), kf[ds], x);
-        y = E::mfma(read_rows<D>(gs, r, ds, lg), vf[ds], y);
+        for (int ds = 0; ds < NDS; ++ds) {
+          if (ds + 1 < NDS) {
+            qa[(ds + 1) & 1] = read_rows<D>(qs, r, ds + 1, lg);
+            ga[(ds + 1) & 1] = read_rows<D>(gs, r, ds + 1, lg);
+          }
+          x = E::mfma(qa[ds & 1], kf[ds], x);
+          y = E::mfma(ga[ds & 1], vf[ds], y);
+        }
       }
       uint32_t pp[8], dsp[8];
 #pragma unroll
@@ -609,15 +622,24 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
           dsp[4 * half + e] = E::pack2(dv[2 * e], dv[2 * e + 1]);
         }
       }
-      // dV^T += dO^T P and dK^T += Q^T dS (two 16-row k-steps)
+      // dV^T += dO^T P and dK^T += Q^T dS (two 16-row k-steps), the
+      // transposed fragments read one MFMA pair ahead as above
+      {
+        u32x4 ta[2], tb[2];
+        ta[0] = read_tr<D>(gs, tro[0], 0);
+        tb[0] = read_tr<D>(qs, tro[0], 0);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const u32x4 pf = {pp[4 * kk], pp[4 * kk + 1], pp[4 * kk + 2], pp[4 * kk + 3]};
-        const u32x4 sf = {dsp[4 * kk], dsp[4 * kk + 1], dsp[4 * kk + 2], dsp[4 * kk + 3]};
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          adv[dt] = E::mfma(read_tr<D>(gs, tro[dt], kk), pf, adv[dt]);
-          adk[dt] = E::mfma(read_tr<D>(qs, tro[dt], kk), sf, adk[dt]);
+        for (int i = 0; i < 2 * NDT; ++i) {
+          const int kk = i / NDT, dt = i % NDT;
+          if (i + 1 < 2 * NDT) {
+            const int kn = (i + 1) / NDT, dn = (i + 1) % NDT;
+            ta[(i + 1) & 1] = read_tr<D>(gs, tro[dn], kn);
+            tb[(i + 1) & 1] = read_tr<D>(qs, tro[dn], kn);
+          }
+          const u32x4 pf = {pp[4 * kk], pp[4 * kk + 1], pp[4 * kk + 2], pp[4 * kk + 3]};
+          const u32x4 sf = {dsp[4 * kk], dsp[4 * kk + 1], dsp[4 * kk + 2], dsp[4 * kk + 3]};
+          adv[dt] = E::mfma(ta[i & 1], pf, adv[dt]);
+          adk[dt] = E::mfma(tb[i & 1], sf, adk[dt]);
         }
       }
     }   // heads of the step
