@@ -595,7 +595,6 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
           y = E::mfma(ga[ds & 1], vf[ds], y);
         }
       }
-      uint32_t pp[8], dsp[8];
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int rb = 16 * half + 8 * lg;
@@ -616,30 +615,25 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
           pv[e] = p;
           dv[e] = p * (y[jj] - de);
         }
+        u32x4 pf, sf;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pp[4 * half + e] = E::pack2(pv[2 * e], pv[2 * e + 1]);
-          dsp[4 * half + e] = E::pack2(dv[2 * e], dv[2 * e + 1]);
+          pf[e] = E::pack2(pv[2 * e], pv[2 * e + 1]);
+          sf[e] = E::pack2(dv[2 * e], dv[2 * e + 1]);
         }
-      }
-      // dV^T += dO^T P and dK^T += Q^T dS (two 16-row k-steps), the
-      // transposed fragments read one MFMA pair ahead as above
-      {
+        // dV^T += dO^T P and dK^T += Q^T dS for this half's 16 rows (k-step
+        // `half`), the transposed fragments read one MFMA pair ahead
         u32x4 ta[2], tb[2];
-        ta[0] = read_tr<D>(gs, tro[0], 0);
-        tb[0] = read_tr<D>(qs, tro[0], 0);
+        ta[0] = read_tr<D>(gs, tro[0], half);
+        tb[0] = read_tr<D>(qs, tro[0], half);
 #pragma unroll
-        for (int i = 0; i < 2 * NDT; ++i) {
-          const int kk = i / NDT, dt = i % NDT;
-          if (i + 1 < 2 * NDT) {
-            const int kn = (i + 1) / NDT, dn = (i + 1) % NDT;
-            ta[(i + 1) & 1] = read_tr<D>(gs, tro[dn], kn);
-            tb[(i + 1) & 1] = read_tr<D>(qs, tro[dn], kn);
+        for (int dt = 0; dt < NDT; ++dt) {
+          if (dt + 1 < NDT) {
+            ta[(dt + 1) & 1] = read_tr<D>(gs, tro[dt + 1], half);
+            tb[(dt + 1) & 1] = read_tr<D>(qs, tro[dt + 1], half);
           }
-          const u32x4 pf = {pp[4 * kk], pp[4 * kk + 1], pp[4 * kk + 2], pp[4 * kk + 3]};
-          const u32x4 sf = {dsp[4 * kk], dsp[4 * kk + 1], dsp[4 * kk + 2], dsp[4 * kk + 3]};
-          adv[dt] = E::mfma(ta[i & 1], pf, adv[dt]);
-          adk[dt] = E::mfma(tb[i & 1], sf, adk[dt]);
+          adv[dt] = E::mfma(ta[dt & 1], pf, adv[dt]);
+          adk[dt] = E::mfma(tb[dt & 1], sf, adk[dt]);
         }
       }
     }   // heads of the step
