@@ -120,6 +120,26 @@ def test_qsparse_t1(gpu):
     assert_close(np64(out), ref, what="T1")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_qsparse_one_merge_lane_per_task(gpu, dtype):
+    """A selected-rows launch with 2^18 merge tasks (8 kv heads x 16 row tiles
+    of 128 (row, head) pairs x 16 sixteen-byte columns) and 5 splits per row
+    tile at 16K keys merges each task's splits in one lane; smaller launches
+    share a task between lanes. Both dtypes against the oracle; fp16 at a
+    bound near its own rounding (the split partials are stored in the
+    element type)."""
+    from delta_attention import ops
+    B, H, Hkv, S, D = 1, 32, 8, 16384, 128
+    q, k, v = gen_qkv(B, H, Hkv, S, D, seed=11, dtype=dtype)
+    rows = torch.randperm(S, generator=torch.Generator().manual_seed(12))[:512].sort().values
+    print(f"qsparse 512 rows x 32 heads, {dtype}", flush=True)
+    out = ops.qsparse_attention(q, k, v, rows.cuda(), D ** -0.5, q_rows=rows.cuda())
+    torch.cuda.synchronize()
+    ref = O.qsparse_attention(np64(q)[:, :, rows.numpy()], np64(k), np64(v), rows.numpy(), D ** -0.5)
+    assert_close(np64(out), ref, atol=2e-2 if dtype == torch.bfloat16 else 2e-3,
+                 what=f"one merge lane per task ({dtype})")
+
+
 @pytest.mark.parametrize("kind", ["rectangle", "irregular", "causal"])
 def test_qsparse_reference_kernel_tests(gpu, kind):
     # delta_kernel.py:332-469: Z=1, H=2, N_CTX=1024, D=64, std 0.5, seed 20, atol 1e-2
