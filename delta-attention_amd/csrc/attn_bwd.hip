@@ -88,6 +88,7 @@ struct BwdArgs {
   float* dq_part;                // [item][BM][D] when n_splits > 1
   // dkdv kernel
   int n_blk, nsb, ncs, nco, rpc, items_per_bh;
+  int red_keys;                  // keys per (batch, kv head) the reduce sums: blocks of several items
   float* kv_part;                // [B * Hkv * items_per_bh][2][KT][D]
 };
 
@@ -825,7 +826,30 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
     }
   }
 
-  // partials of this item: [2][KT][D] (dK scaled by sm_scale, dV)
+  // A block whose rows are one item writes its dK (scaled by sm_scale) and
+  // dV directly, as the reduce would from a single partial (the same bits);
+  // a block of several items writes partials [2][KT][D] for the reduce.
+  if ((blk < a.nsb ? a.ncs : a.nco) == 1) {
+    if (key >= a.n_kv) return;
+    u32x2* ok = (u32x2*)((char*)a.dk + ((int64_t)b * a.dks_b + (int64_t)hk * a.dks_h + (int64_t)key * a.dks_s) * esz);
+    u32x2* ov = (u32x2*)((char*)a.dv + ((int64_t)b * a.dvs_b + (int64_t)hk * a.dvs_h + (int64_t)key * a.dvs_s) * esz);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const int d4 = (32 * dt + 8 * jq + 4 * lg) / 4;
+        const u32x2 pk0 = a.accumulate ? ok[d4] : (u32x2){0, 0};
+        const u32x2 pv0 = a.accumulate ? ov[d4] : (u32x2){0, 0};
+        u32x2 nk, nv;
+        nk[0] = acc_pack<T>(pk0[0], adk[dt][4 * jq] * a.sm_scale, adk[dt][4 * jq + 1] * a.sm_scale, a.accumulate);
+        nk[1] = acc_pack<T>(pk0[1], adk[dt][4 * jq + 2] * a.sm_scale, adk[dt][4 * jq + 3] * a.sm_scale, a.accumulate);
+        nv[0] = acc_pack<T>(pv0[0], adv[dt][4 * jq], adv[dt][4 * jq + 1], a.accumulate);
+        nv[1] = acc_pack<T>(pv0[1], adv[dt][4 * jq + 2], adv[dt][4 * jq + 3], a.accumulate);
+        ok[d4] = nk;
+        ov[d4] = nv;
+      }
+    return;
+  }
   float* pk = a.kv_part + (int64_t)blockIdx.x * 2 * KT * D + (int64_t)(wave * 32 + ln) * D;
   float* pv = pk + (int64_t)KT * D;
 #pragma unroll
@@ -840,12 +864,14 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
     }
 }
 
-// dK, dV of every key: the sum of its block's chunk partials, 8 dims per thread.
+// dK, dV of the keys of blocks cut into several items (every key, or the
+// sink blocks' keys 0 .. red_keys - 1 when only those are): the sum of its
+// block's chunk partials, 8 dims per thread.
 template <typename T, int D>
 __global__ __launch_bounds__(RED) void dkdv_reduce_kernel(BwdArgs a) {
   constexpr int CPR = D / 8;
   const int64_t task = (int64_t)blockIdx.x * RED + threadIdx.x;
-  const int64_t per_bh = (int64_t)a.n_kv * CPR;
+  const int64_t per_bh = (int64_t)a.red_keys * CPR;
   if (task >= (int64_t)a.B * a.Hkv * per_bh) return;
   const int bh = (int)(task / per_bh);
   const int rem = (int)(task % per_bh);
@@ -859,6 +885,7 @@ __global__ __launch_bounds__(RED) void dkdv_reduce_kernel(BwdArgs a) {
     first = a.nsb * a.ncs + (blk - a.nsb) * a.nco;
     cnt = a.nco;
   }
+  if (cnt == 1) return;   // written by its dkdv item
   float sk[8], sv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -1063,9 +1090,10 @@ void launch_bwd(const BwdArgs& a, hipStream_t s) {
   }
   const int gk = a.B * a.Hkv * a.items_per_bh;
   hipLaunchKernelGGL((dkdv_kernel<T, D, ROWS>), dim3(gk), dim3(NTHR), 0, s, a);
-  const int64_t tasks = (int64_t)a.B * a.Hkv * a.n_kv * (D / 8);
-  hipLaunchKernelGGL((dkdv_reduce_kernel<T, D>), dim3((unsigned)((tasks + RED - 1) / RED)),
-                     dim3(RED), 0, s, a);
+  const int64_t tasks = (int64_t)a.B * a.Hkv * a.red_keys * (D / 8);
+  if (tasks > 0)
+    hipLaunchKernelGGL((dkdv_reduce_kernel<T, D>), dim3((unsigned)((tasks + RED - 1) / RED)),
+                       dim3(RED), 0, s, a);
 }
 
 template <bool ROWS>
@@ -1163,6 +1191,7 @@ static void place_workspace(BwdArgs& a, const DqPlan& dq, const KvPlan& kv, int 
   a.n_mtiles = dq.n_mtiles; a.n_splits = dq.n_splits; a.chunk = dq.chunk;
   a.n_blk = kv.n_blk; a.nsb = kv.nsb; a.ncs = kv.ncs; a.nco = kv.nco; a.rpc = kv.rpc;
   a.items_per_bh = kv.items_per_bh;
+  a.red_keys = kv.nco > 1 ? a.n_kv : kv.ncs > 1 ? std::min(a.n_kv, kv.nsb * KT) : 0;
   char* p = (char*)ws;
   size_t off = (size_t)a.B * a.Hq * a.n_rows * sizeof(float);
   off = (off + 255) / 256 * 256;
