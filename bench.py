@@ -143,7 +143,7 @@ def make_inputs(a, device):
 def cpu_threads():
     """Host threads for the CPU oracle: the cores this process may run on
     (sched_getaffinity), capped by OMP_NUM_THREADS when it is set (the CPU
-    share of a shared GPU box). -> (threads, affinity count)."""
+    share of a shared machine). -> (threads, affinity count)."""
     aff = len(os.sched_getaffinity(0))
     cap = os.environ.get("OMP_NUM_THREADS", "")
     n = min(aff, int(cap)) if cap.isdigit() and int(cap) > 0 else aff

@@ -2,7 +2,7 @@
 inputs (the oracle runs in float64 on the bf16/fp16-rounded values).
 
 Tolerance (the reference's T1 gate, tests/test_math_identities.py:85-89, and
-the north-star bar): per-row cosine > 0.999 and max |diff| < 2e-2 for the
+the layer's parity bar): per-row cosine > 0.999 and max |diff| < 2e-2 for the
 attention kernels; the delta-add kernel is bit-exact against the reference's
 bf16 elementwise arithmetic.
 """

@@ -172,7 +172,7 @@ def test_module_forward_and_qwen3(gpu):
         qr, kr = O.round_bf16(qr).astype(np.float64), O.round_bf16(kr).astype(np.float64)
         vr = O.round_bf16(vp).astype(np.float64)
         att = O.delta_forward(qr, kr, vr, 64, 256, 16, 128 ** -0.5)
-        # the layer's delta attention itself, at the north-star bar
+        # the layer's delta attention itself, at cosine 0.999 / max |diff| 2e-2
         assert len(seen) == 1 and seen[0].shape == (1, 1024, H * 128)
         assert_close(np64(seen[0]).reshape(1, 1024, H, 128), att, what=f"{cls.__name__} attention")
         # and through o_proj (a bf16 GEMM of 1024 x H*128 by the random weights)
