@@ -394,6 +394,25 @@ def test_split_plans_refuse_grid_overflow(lib):
     assert lib.da_qsparse_workspace_bytes(1, 32, 8, 2174, 131072, 128) > 0
 
 
+def test_bwd_rows_per_chunk_setting(lib):
+    """The dK/dV rows-per-item cap: positive multiples of 32 up to 2^20, 0 for
+    the default (8192); read when a plan is made, so a smaller cap cuts the
+    key blocks into more items, whose partials the workspace holds."""
+    B, H, Hkv, S, D = 1, 8, 2, 4096, 128
+    base = lib.da_sparse_attn_bwd_workspace_bytes(B, H, Hkv, S, D, 2048, 16, 64)
+    base_rows = lib.da_qsparse_attn_bwd_workspace_bytes(B, H, Hkv, 1000, S, D)
+    for bad in (-32, 16, 33, 100, (1 << 20) + 32):
+        assert lib.da_set_bwd_rows_per_chunk(bad) == L.DA_ERR_INVALID_ARG
+    try:
+        assert lib.da_set_bwd_rows_per_chunk(64) == L.DA_OK
+        assert lib.da_sparse_attn_bwd_workspace_bytes(B, H, Hkv, S, D, 2048, 16, 64) > base
+        assert lib.da_qsparse_attn_bwd_workspace_bytes(B, H, Hkv, 1000, S, D) > base_rows
+    finally:
+        assert lib.da_set_bwd_rows_per_chunk(0) == L.DA_OK
+    assert lib.da_sparse_attn_bwd_workspace_bytes(B, H, Hkv, S, D, 2048, 16, 64) == base
+    assert lib.da_qsparse_attn_bwd_workspace_bytes(B, H, Hkv, 1000, S, D) == base_rows
+
+
 def test_training_entry_checks(lib):
     """The training-path entries: workspace sizes, and every refusal happens
     before a launch (null pointers, head_dim, dtype, row alignment, lse
