@@ -200,7 +200,11 @@ __global__ __launch_bounds__(NTHR, 2) void dq_kernel(BwdArgs a) {
   // DMA right after issuing it; the loop orders DMA and reads itself
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 31, lg = lane >> 5;
-  const int w = blockIdx.x;
+  // XCD-aware: workgroup b runs item (b % 8) per + b / 8, so each XCD takes a
+  // contiguous range of row tiles, whose key/value tiles overlap in its L2
+  const int per = (int)(gridDim.x >> 3);
+  const int w = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (w >= a.B * a.Hkv * a.n_mtiles * a.n_splits) return;
   const int mt = w % a.n_mtiles;
   const int split = (w / a.n_mtiles) % a.n_splits;
   const int bh = w / a.n_mtiles / a.n_splits;
@@ -487,8 +491,13 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 31, lg = lane >> 5;
-  const int item = blockIdx.x % a.items_per_bh;
-  const int bh = blockIdx.x / a.items_per_bh;
+  // XCD-aware: each XCD takes a contiguous range of key blocks, whose
+  // query rows overlap in its L2
+  const int per = (int)(gridDim.x >> 3);
+  const int wi = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (wi >= a.B * a.Hkv * a.items_per_bh) return;
+  const int item = wi % a.items_per_bh;
+  const int bh = wi / a.items_per_bh;
   const int hk = bh % a.Hkv, b = bh / a.Hkv;
   int blk, c;
   if (item < a.nsb * a.ncs) {
@@ -850,7 +859,7 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
       }
     return;
   }
-  float* pk = a.kv_part + (int64_t)blockIdx.x * 2 * KT * D + (int64_t)(wave * 32 + ln) * D;
+  float* pk = a.kv_part + (int64_t)wi * 2 * KT * D + (int64_t)(wave * 32 + ln) * D;
   float* pv = pk + (int64_t)KT * D;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
@@ -1082,14 +1091,14 @@ size_t bwd_ws_bytes(int B, int Hq, int Hkv, int n_rows, int n_kv, int D, const D
 template <typename T, int D, bool ROWS>
 void launch_bwd(const BwdArgs& a, hipStream_t s) {
   const int gq = a.B * a.Hkv * a.n_mtiles * a.n_splits;
-  hipLaunchKernelGGL((dq_kernel<T, D, ROWS>), dim3(gq), dim3(NTHR), 0, s, a);
+  hipLaunchKernelGGL((dq_kernel<T, D, ROWS>), dim3((gq + 7) / 8 * 8), dim3(NTHR), 0, s, a);
   if (a.n_splits > 1) {
     const int64_t tasks = (int64_t)a.B * a.Hkv * a.n_mtiles * BM * (D / 8);
     hipLaunchKernelGGL((dq_reduce_kernel<T, D, ROWS>), dim3((unsigned)((tasks + RED - 1) / RED)),
                        dim3(RED), 0, s, a);
   }
   const int gk = a.B * a.Hkv * a.items_per_bh;
-  hipLaunchKernelGGL((dkdv_kernel<T, D, ROWS>), dim3(gk), dim3(NTHR), 0, s, a);
+  hipLaunchKernelGGL((dkdv_kernel<T, D, ROWS>), dim3((gk + 7) / 8 * 8), dim3(NTHR), 0, s, a);
   const int64_t tasks = (int64_t)a.B * a.Hkv * a.red_keys * (D / 8);
   if (tasks > 0)
     hipLaunchKernelGGL((dkdv_reduce_kernel<T, D>), dim3((unsigned)((tasks + RED - 1) / RED)),
