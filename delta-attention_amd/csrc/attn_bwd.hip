@@ -89,7 +89,8 @@ struct BwdArgs {
   // dkdv kernel
   int n_blk, nsb, ncs, nco, rpc, items_per_bh;
   int red_keys;                  // keys per (batch, kv head) the reduce sums: blocks of several items
-  float* kv_part;                // [B * Hkv * items_per_bh][2][KT][D]
+  int part_per_bh;               // partial slots per (batch, kv head): the items of those blocks
+  float* kv_part;                // [B * Hkv * part_per_bh][2][KT][D]
 };
 
 // Key tiles (BN keys) a row tile visits, in order: the sink tiles, then the
@@ -859,7 +860,9 @@ __global__ __launch_bounds__(NTHR, 1) void dkdv_kernel(BwdArgs a) {
       }
     return;
   }
-  float* pk = a.kv_part + (int64_t)wi * 2 * KT * D + (int64_t)(wave * 32 + ln) * D;
+  // (those items come first in a (batch, kv head)'s item order: every item
+  // when the window blocks are cut too, else the sink blocks' items)
+  float* pk = a.kv_part + ((int64_t)bh * a.part_per_bh + item) * 2 * KT * D + (int64_t)(wave * 32 + ln) * D;
   float* pv = pk + (int64_t)KT * D;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
@@ -902,7 +905,7 @@ __global__ __launch_bounds__(RED) void dkdv_reduce_kernel(BwdArgs a) {
     sv[e] = 0.f;
   }
   for (int it = 0; it < cnt; ++it) {
-    const float* p = a.kv_part + ((int64_t)bh * a.items_per_bh + first + it) * 2 * KT * D +
+    const float* p = a.kv_part + ((int64_t)bh * a.part_per_bh + first + it) * 2 * KT * D +
                      (int64_t)kl * D + 8 * c;
     const f32x4 k0 = ((const f32x4*)p)[0], k1 = ((const f32x4*)p)[1];
     const f32x4 v0 = ((const f32x4*)(p + KT * D))[0], v1 = ((const f32x4*)(p + KT * D))[1];
@@ -1038,6 +1041,7 @@ DqPlan plan_dq(int B, int Hkv, int G, int n_rows, int64_t list_tiles, bool rows)
 
 struct KvPlan {
   int n_blk, nsb, ncs, nco, rpc, items_per_bh;
+  int part_per_bh;   // items whose block is cut into several (they write partials)
 };
 
 // Rows per dK/dV chunk at most (process-wide; da_set_bwd_rows_per_chunk).
@@ -1070,6 +1074,7 @@ KvPlan plan_kv(int n_rows, int n_kv, int window, int sink, bool rows) {
     if (p.ncs < 1) p.ncs = 1;
   }
   p.items_per_bh = p.nsb * p.ncs + (p.n_blk - p.nsb) * p.nco;
+  p.part_per_bh = p.nco > 1 ? p.items_per_bh : p.ncs > 1 ? p.nsb * p.ncs : 0;
   return p;
 }
 
@@ -1082,7 +1087,7 @@ size_t bwd_ws_bytes(int B, int Hq, int Hkv, int n_rows, int n_kv, int D, const D
   if (dq.n_splits > 1)
     bytes += (size_t)B * Hkv * dq.n_splits * dq.n_mtiles * BM * D * sizeof(float);
   bytes = (bytes + 255) / 256 * 256;
-  bytes += (size_t)B * Hkv * kv.items_per_bh * 2 * KT * D * sizeof(float);
+  bytes += (size_t)B * Hkv * kv.part_per_bh * 2 * KT * D * sizeof(float);
   (void)rows;
   (void)esz;
   return bytes;
@@ -1201,6 +1206,7 @@ static void place_workspace(BwdArgs& a, const DqPlan& dq, const KvPlan& kv, int 
   a.n_blk = kv.n_blk; a.nsb = kv.nsb; a.ncs = kv.ncs; a.nco = kv.nco; a.rpc = kv.rpc;
   a.items_per_bh = kv.items_per_bh;
   a.red_keys = kv.nco > 1 ? a.n_kv : kv.ncs > 1 ? std::min(a.n_kv, kv.nsb * KT) : 0;
+  a.part_per_bh = kv.part_per_bh;
   char* p = (char*)ws;
   size_t off = (size_t)a.B * a.Hq * a.n_rows * sizeof(float);
   off = (off + 255) / 256 * 256;
