@@ -36,6 +36,8 @@ def _layer(B, H, Hkv, S, D, gamma, window, sink, mode="delta", seed=0, dtype=tor
     (1, 4, 4, 900, 32, 128, 128, 8),      # head_dim 32, gamma 128 with MHA (fused, 128-row tiles)
     (1, 8, 2, 1500, 256, 64, 384, 16),    # head_dim 256 (one workgroup per CU), fused order
     (1, 4, 4, 700, 256, 32, 128, 4),      # head_dim 256, MHA: one head per 128-row tile
+    (1, 16, 2, 1536, 128, 64, 384, 32),   # GQA 8 (Llama-3-70B ratio): four head splits per row block
+    (1, 8, 1, 1000, 64, 32, 256, 8),      # GQA 8, one kv head, head_dim 64, s % gamma != 0
 ])
 def test_delta_prefill_parity(gpu, B, H, Hkv, S, D, gamma, window, sink):
     got, ref, _ = _layer(B, H, Hkv, S, D, gamma, window, sink)

@@ -2,7 +2,7 @@
 forward equal to the inference layer, the saved row statistics against the
 oracle's log-sum-exp, and dq / dk / dv against the oracle's float64
 gradients (delta_train_grads, pinned by tests/test_oracle_train.py) for GQA
-1-5, head_dim 32/64/128, bf16 and fp16, the detach and gradient-scale arms,
+1-5 and 8, head_dim 32/64/128, bf16 and fp16, the detach and gradient-scale arms,
 sinks beyond the window and a window covering every key. Each case prints
 its parameters before it runs."""
 
@@ -49,6 +49,7 @@ CASES = [
     (1, 8, 2, 512, 64, 16, 128, 64, torch.bfloat16, "detach"),
     (1, 8, 2, 512, 64, 16, 128, 64, torch.bfloat16, "scaled"),
     (1, 4, 2, 128, 64, 64, 64, 8, torch.bfloat16, "plain"),          # s <= cut_n: all rows dense
+    (1, 16, 2, 448, 128, 32, 128, 16, torch.bfloat16, "plain"),      # GQA 8: two four-head dK/dV steps
 ]
 
 
