@@ -50,6 +50,7 @@ CASES = [
     (1, 8, 2, 512, 64, 16, 128, 64, torch.bfloat16, "scaled"),
     (1, 4, 2, 128, 64, 64, 64, 8, torch.bfloat16, "plain"),          # s <= cut_n: all rows dense
     (1, 16, 2, 448, 128, 32, 128, 16, torch.bfloat16, "plain"),      # GQA 8: two four-head dK/dV steps
+    (1, 8, 2, 384, 128, 64, 128, 16, torch.float16, "plain"),        # fp16 at head_dim 128
 ]
 
 
